@@ -1,0 +1,276 @@
+/*
+ * qvp.h - C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * This is the drop-in boundary below the C++17 host API (allocator, cache
+ * manager, scheduler). Everything crossing it is a plain pointer, an integer
+ * or a float; there are no C++ types, no exceptions and no torch types.
+ *
+ * Reference interfaces each group of entry points replaces (paths relative to
+ * the QwenVL-Paged source tree):
+ *   block pool        include/qwenvl_paged/Block.h:59-70,99-166 (PhysicalBlock
+ *                     storage, HostMemoryOptions), src/Block.cpp:21-44
+ *                     (alignment rounding), src/MemoryAllocator.cpp:8-26
+ *   ragged pack       docs/architecture.md:117-120 (flatten BlockTable::entries()
+ *                     into [num_seqs, max_blocks_per_seq]),
+ *                     include/qwenvl_paged/PagedAttention.h:15-22 (per-sequence
+ *                     context lengths), src/KVCacheManager.cpp:11-25 (unmapped or
+ *                     swapped blocks fault)
+ *   paged decode      include/qwenvl_paged/PagedAttention.h:53-127
+ *                     (paged_attention_decode<T>)
+ *   copy-on-write     include/qwenvl_paged/MemoryAllocator.h:116,
+ *                     src/MemoryAllocator.cpp:76-85 (copy_block)
+ *   swap              include/qwenvl_paged/SwapBackend.h:27-57,
+ *                     src/SwapBackend.cpp:10-43 (store/load of whole blocks)
+ *
+ * Conventions
+ *   - Every entry point returns a qvp_status; QVP_OK is 0. On any other value
+ *     nothing was enqueued and no output was touched (the reference's
+ *     "return false without touching out", PagedAttention.h:50-51,73-89).
+ *     qvp_last_error() returns a thread-local message for the last failure.
+ *   - `stream` arguments are hipStream_t values passed as void*; NULL is the
+ *     legacy default stream. Work is asynchronous unless stated otherwise.
+ *   - Not thread-safe per object: one engine thread drives a pool and a batch,
+ *     as the reference's single engine loop does (docs/architecture.md:70-83).
+ */
+#ifndef QVP_H
+#define QVP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* Status and element types                                                 */
+/* ------------------------------------------------------------------------ */
+
+typedef enum qvp_status {
+    QVP_OK = 0,
+    /* Shapes, sizes or dtypes are inconsistent (PagedAttention.h:59-68). */
+    QVP_ERR_INVALID_ARGUMENT = 1,
+    /* A block the call needs is unmapped, swapped out or not in the pool
+     * (PagedAttention.h:73-89, KVCacheManager.cpp:11-25). */
+    QVP_ERR_UNMAPPED = 2,
+    /* Device or pinned-host memory could not be allocated. */
+    QVP_ERR_OUT_OF_MEMORY = 3,
+    /* A caller-supplied buffer is smaller than the call needs. */
+    QVP_ERR_CAPACITY = 4,
+    /* A HIP runtime call failed; qvp_last_error() names it. */
+    QVP_ERR_DEVICE = 5
+} qvp_status;
+
+typedef enum qvp_dtype {
+    QVP_DTYPE_F32 = 0,
+    QVP_DTYPE_BF16 = 1,
+    QVP_DTYPE_F16 = 2
+} qvp_dtype;
+
+/* Block-table value for a logical block that has no resident frame (never
+ * mapped, or swapped out: BlockTable.h:18-24). Packing refuses it. */
+#define QVP_UNMAPPED_BLOCK 0xFFFFFFFFu
+
+/* Returns the message of the last failure on the calling thread ("" if none). */
+const char* qvp_last_error(void);
+/* Returns a static name for a status value. */
+const char* qvp_status_name(int status);
+/* Returns the library version as major*10000 + minor*100 + patch. */
+int qvp_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Runtime plumbing. No reference counterpart: these give hosts without a   */
+/* device runtime of their own (ctypes, cgo, a bare C++ engine) device      */
+/* memory, streams and events.                                              */
+/* ------------------------------------------------------------------------ */
+
+int qvp_device_count(int* count);
+int qvp_set_device(int device);
+int qvp_device_synchronize(void);
+
+int qvp_malloc(void** ptr, size_t bytes);
+int qvp_free(void* ptr);
+/* Pinned (page-locked) host memory that the device can read and write. */
+int qvp_host_alloc(void** ptr, size_t bytes);
+int qvp_host_free(void* ptr);
+/* Device-side address of pinned host memory from qvp_host_alloc. */
+int qvp_host_device_pointer(void** device_ptr, void* host_ptr);
+
+int qvp_memcpy_htod(void* dst, const void* src, size_t bytes, void* stream);
+int qvp_memcpy_dtoh(void* dst, const void* src, size_t bytes, void* stream);
+int qvp_memcpy_dtod(void* dst, const void* src, size_t bytes, void* stream);
+/* Fills device memory with a byte value using a fill kernel (safe inside
+ * graph capture, unlike a runtime memset node). */
+int qvp_fill_bytes(void* dst, uint8_t value, size_t bytes, void* stream);
+
+int qvp_stream_create(void** stream);
+int qvp_stream_destroy(void* stream);
+int qvp_stream_synchronize(void* stream);
+int qvp_event_create(void** event);
+int qvp_event_destroy(void* event);
+int qvp_event_record(void* event, void* stream);
+int qvp_event_synchronize(void* event);
+int qvp_stream_wait_event(void* stream, void* event);
+int qvp_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ------------------------------------------------------------------------ */
+/* Block pool: the physical KV frames in HBM                                */
+/* Replaces per-block std::aligned_alloc storage (Block.h:99-166,           */
+/* src/Block.cpp:30-44). Frame i lives at base + i * block_stride, where    */
+/* block_stride = round_up(block_bytes, alignment) like PhysicalBlock's     */
+/* size_bytes() (src/Block.cpp:30-44; alignment 0 means 256, Block.h:17).   */
+/* ------------------------------------------------------------------------ */
+
+typedef struct qvp_pool qvp_pool;
+
+int qvp_pool_create(uint32_t num_blocks, size_t block_bytes, size_t alignment, qvp_pool** pool);
+int qvp_pool_destroy(qvp_pool* pool);
+void* qvp_pool_base(const qvp_pool* pool);
+size_t qvp_pool_block_stride(const qvp_pool* pool);
+size_t qvp_pool_block_bytes(const qvp_pool* pool);
+uint32_t qvp_pool_num_blocks(const qvp_pool* pool);
+/* Device address of one frame, or NULL when block >= num_blocks
+ * (MemoryAllocator::block returns nullptr for invalid ids,
+ * src/MemoryAllocator.cpp:87-99). */
+void* qvp_pool_block_ptr(const qvp_pool* pool, uint32_t block);
+/* Host <-> frame byte copies at an offset inside one frame (the host writes
+ * the reference tests make through PhysicalBlock::data(),
+ * tests/PagedAttention.test.cpp:97-127). Asynchronous on `stream`; the host
+ * buffer must stay valid until the stream reaches the copy. */
+int qvp_pool_write(qvp_pool* pool, uint32_t block, size_t offset, const void* src, size_t bytes,
+                   void* stream);
+int qvp_pool_read(const qvp_pool* pool, uint32_t block, size_t offset, void* dst, size_t bytes,
+                  void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Ragged-batch packing (docs/architecture.md:117-120)                      */
+/* ------------------------------------------------------------------------ */
+
+typedef struct qvp_batch qvp_batch;
+
+/* Device-side arrays of the last successful qvp_pack on a batch.
+ *   block_tables  int32 [num_seqs][max_blocks_per_seq], row b holds the frames
+ *                 of logical blocks 0..ceil(seq_lens[b]/tokens_per_block)-1 in
+ *                 logical order, padded with -1
+ *   seq_lens      int32 [num_seqs]
+ *   cu_seqlens    int32 [num_seqs + 1], exclusive prefix sum of seq_lens
+ *   cu_splits     int32 [num_seqs + 1], exclusive prefix sum of each
+ *                 sequence's split count ceil(seq_lens[b] / split_tokens)
+ *   split_seq     int32 [num_splits], sequence of each split
+ *   split_start   int32 [num_splits], first token of each split             */
+typedef struct qvp_packed_view {
+    const int32_t* block_tables;
+    const int32_t* seq_lens;
+    const int32_t* cu_seqlens;
+    const int32_t* cu_splits;
+    const int32_t* split_seq;
+    const int32_t* split_start;
+    uint32_t num_seqs;
+    uint32_t max_blocks_per_seq;
+    uint32_t num_splits;
+    uint32_t split_tokens;
+    uint32_t tokens_per_block;
+    uint32_t num_pool_blocks;
+    uint32_t max_seq_len;
+    uint64_t total_tokens;
+} qvp_packed_view;
+
+int qvp_batch_create(qvp_batch** batch);
+int qvp_batch_destroy(qvp_batch* batch);
+
+/* Packs a ragged batch given in CSR form: sequence b owns
+ * block_ids[cu_blocks[b] .. cu_blocks[b+1]) in logical-block order (what
+ * BlockTable::entries() lists, BlockTable.h:105-108) and has context_lens[b]
+ * committed tokens. A sequence needs its first ceil(context_lens[b] /
+ * tokens_per_block) entries; each must be < num_pool_blocks and not
+ * QVP_UNMAPPED_BLOCK. The whole batch is validated before anything is written,
+ * so a refused call (QVP_ERR_INVALID_ARGUMENT for context_len == 0 or too few
+ * mapped blocks, QVP_ERR_UNMAPPED for a missing frame) leaves the batch's
+ * previous contents intact (PagedAttention.h:73-89).
+ * split_tokens (0 selects 512) is rounded up to a multiple of 128.
+ * The arrays are staged in pinned memory (double-buffered) and copied to the
+ * device asynchronously on `stream`. */
+int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
+             const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
+             uint32_t num_pool_blocks, uint32_t split_tokens, void* stream);
+int qvp_batch_view(const qvp_batch* batch, qvp_packed_view* view);
+
+/* ------------------------------------------------------------------------ */
+/* Paged decode (include/qwenvl_paged/PagedAttention.h:53-127)              */
+/* ------------------------------------------------------------------------ */
+
+/* One decode step for every sequence of a packed batch: for each sequence b
+ * and query head h, with g = h / (num_query_heads / num_kv_heads),
+ *   out[b][h][:] = sum_t w_t * V[b][t][g][:] / sum_t w_t,
+ *   w_t = exp(s_t - max_t s_t),  s_t = scale * <query[b][h][:], K[b][t][g][:]>
+ * over t < seq_lens[b], with fp32 accumulation (PagedAttention.h:94-124).
+ * K and V of token t of sequence b live in frame block_tables[b][t / tpb] at
+ * element offset layer * layer_stride + {0 | stream_stride} +
+ * (t % tpb) * token_stride + g * head_stride (CacheLayout.cpp:25-38); head_dim
+ * elements are contiguous. */
+typedef struct qvp_decode_args {
+    const void* query;          /* device, [num_seqs][num_query_heads][head_dim], kv_dtype */
+    void* out;                  /* device, [num_seqs][num_query_heads][head_dim], out_dtype */
+    const void* kv_base;        /* device address of frame 0 */
+    uint64_t block_stride;      /* bytes between frames */
+    const qvp_batch* batch;     /* packed by qvp_pack for this pool */
+    uint32_t kv_dtype;          /* qvp_dtype of query and cache elements */
+    uint32_t out_dtype;         /* qvp_dtype of out */
+    uint32_t layer;
+    uint32_t num_layers;
+    uint32_t num_query_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t tokens_per_block;
+    uint64_t head_stride;       /* elements, KVBlockLayout::head_stride() */
+    uint64_t token_stride;      /* elements, KVBlockLayout::token_stride() */
+    uint64_t stream_stride;     /* elements, KVBlockLayout::stream_stride() */
+    uint64_t layer_stride;      /* elements, KVBlockLayout::layer_stride() */
+    float scale;
+    void* workspace;            /* device scratch for split partials, or NULL */
+    uint64_t workspace_bytes;   /* size of workspace; ignored when it is NULL */
+} qvp_decode_args;
+
+/* Bytes of workspace qvp_paged_decode needs for this batch and head shape. */
+int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads,
+                               uint32_t head_dim, uint64_t* bytes);
+/* Validates everything on the host, then enqueues the split-K decode kernel
+ * and the split-merge kernel on `stream`. With workspace == NULL the library
+ * uses a per-device workspace it grows on demand. */
+int qvp_paged_decode(const qvp_decode_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Copy-on-write (MemoryAllocator::copy_block, src/MemoryAllocator.cpp:76-85)*/
+/* ------------------------------------------------------------------------ */
+
+/* Copies bytes [0, copy_bytes) of frame src_ids[i] onto frame dst_ids[i] for
+ * every i in one launch. src_ids/dst_ids are host arrays. Refused when an id is
+ * >= num_blocks, copy_bytes > block_stride, a destination repeats, or a
+ * destination is another pair's source (the result would depend on order).
+ * A pair with src == dst is a no-op. */
+int qvp_copy_blocks(void* kv_base, uint64_t block_stride, uint32_t num_blocks,
+                    const uint32_t* src_ids, const uint32_t* dst_ids, uint32_t num_pairs,
+                    uint64_t copy_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Swap (SwapBackend::store / load, src/SwapBackend.cpp:10-39)              */
+/* ------------------------------------------------------------------------ */
+
+/* Swap-out gather: frame frame_ids[i] -> arena + arena_offsets[i], copy_bytes
+ * each, in one launch. `arena` is pinned host memory from qvp_host_alloc
+ * (its host address); offsets + copy_bytes must lie inside arena_bytes, be
+ * 16-byte aligned and not overlap each other. */
+int qvp_swap_gather(const void* kv_base, uint64_t block_stride, uint32_t num_blocks,
+                    const uint32_t* frame_ids, const uint64_t* arena_offsets, uint32_t count,
+                    void* arena, uint64_t arena_bytes, uint64_t copy_bytes, void* stream);
+/* Swap-in scatter: arena + arena_offsets[i] -> frame frame_ids[i]. Destination
+ * frames must be distinct. */
+int qvp_swap_scatter(void* kv_base, uint64_t block_stride, uint32_t num_blocks,
+                     const uint32_t* frame_ids, const uint64_t* arena_offsets, uint32_t count,
+                     const void* arena, uint64_t arena_bytes, uint64_t copy_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QVP_H */

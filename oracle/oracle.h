@@ -1,0 +1,100 @@
+/*
+ * oracle.h - CPU restatement of the QwenVL-Paged hot path, for checking only.
+ *
+ * TEST INFRASTRUCTURE. Nothing in the product (qwenvl-paged_amd/, include/)
+ * links, loads or calls this code; only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py use it, always as the checker, never as the thing
+ * measured on the GPU.
+ *
+ * Every function cites the reference source it restates (paths relative to the
+ * QwenVL-Paged tree). Pinning (see tests/test_oracle.py): the decode matches
+ * the compiled reference bit for bit (oracle/_ref) and the committed fixtures
+ * under tests/golden/, and the closed-form cases of
+ * tests/PagedAttention.test.cpp (uniform keys, one-hot selection, GQA, CoW
+ * branches); the layout functions match CacheView.test.cpp's invariants; pack
+ * and copy are checked against BlockTable entries and memcpy identity.
+ */
+#ifndef QVP_ORACLE_H
+#define QVP_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_F32 = 0, ORC_BF16 = 1, ORC_F16 = 2 };
+
+/* Element conversions (round to nearest, ties to even; NaN stays NaN). */
+uint16_t orc_bf16_from_f32(float x);
+float orc_f32_from_bf16(uint16_t h);
+uint16_t orc_f16_from_f32(float x);
+float orc_f32_from_f16(uint16_t h);
+void orc_round_to_bf16(const float* src, uint16_t* dst, size_t n);
+void orc_round_to_f16(const float* src, uint16_t* dst, size_t n);
+
+/* BlockShape::byte_size (src/Block.cpp:8-13). */
+uint64_t orc_block_byte_size(uint32_t tokens_per_block, uint32_t num_layers, uint32_t num_kv_heads,
+                             uint32_t head_dim, uint32_t bytes_per_element);
+/* PhysicalBlock::size_bytes: round up to the alignment, 0 -> 256, never 0
+ * (src/Block.cpp:21-38). */
+uint64_t orc_block_stride(uint64_t byte_size, uint64_t alignment);
+
+/* KVBlockLayout strides in elements: out[0..4] = head, token, stream, layer,
+ * element_count (src/CacheLayout.cpp:5-23). */
+void orc_layout_strides(uint32_t tokens_per_block, uint32_t num_layers, uint32_t num_kv_heads,
+                        uint32_t head_dim, uint64_t out[5]);
+/* KVBlockLayout::element_offset, -1 when out of range (src/CacheLayout.cpp:25-38). */
+int64_t orc_element_offset(uint32_t tokens_per_block, uint32_t num_layers, uint32_t num_kv_heads,
+                           uint32_t head_dim, uint32_t layer, uint32_t stream, uint32_t token_in_block,
+                           uint32_t kv_head);
+
+/*
+ * paged_attention_decode<T> for one sequence (PagedAttention.h:53-127) over a
+ * flat pool: frame i at pool + i * block_stride, logical block j of the
+ * sequence in frame table[j] (QVP unmapped value 0xFFFFFFFF = no frame).
+ * dtype is the element type of query, cache and out (ORC_F32 / ORC_BF16 /
+ * ORC_F16). out_f32, when not NULL, receives accumulator / denominator before
+ * the final cast. Returns 1 on success, 0 on refusal with out and out_f32
+ * untouched.
+ */
+int orc_paged_attention_decode(const uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks,
+                               const uint32_t* table, uint32_t table_len, int dtype, const void* query,
+                               uint32_t layer, uint32_t num_layers, uint32_t num_query_heads,
+                               uint32_t num_kv_heads, uint32_t head_dim, uint32_t tokens_per_block,
+                               uint32_t context_len, float scale, void* out, float* out_f32);
+
+/* The same for every sequence of a CSR batch (sequence b owns
+ * ids[cu_blocks[b] .. cu_blocks[b+1])), query/out laid out [b][h][d].
+ * threads > 1 splits the sequences over that many host threads. Returns the
+ * number of sequences refused (0 = all succeeded). */
+int orc_paged_decode_batch(const uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks,
+                           uint32_t num_seqs, const uint32_t* ids, const uint32_t* cu_blocks,
+                           const uint32_t* context_lens, int dtype, const void* query, uint32_t layer,
+                           uint32_t num_layers, uint32_t num_query_heads, uint32_t num_kv_heads,
+                           uint32_t head_dim, uint32_t tokens_per_block, float scale, void* out,
+                           float* out_f32, int threads);
+
+/* Expected arrays of qvp_pack for the same inputs (docs/architecture.md:117-120).
+ * Sizes: tables num_seqs*max_nb, seq_lens num_seqs, cu_seqlens/cu_splits
+ * num_seqs+1, split_seq/split_start num_splits. Returns 0, or -1 when the batch
+ * would be refused. max_nb / num_splits are written first when the size query
+ * pointers are given and the arrays are NULL. */
+int orc_pack(uint32_t num_seqs, const uint32_t* ids, const uint32_t* cu_blocks,
+             const uint32_t* context_lens, uint32_t tokens_per_block, uint32_t num_pool_blocks,
+             uint32_t split_tokens, uint32_t* max_nb, uint32_t* num_splits, int32_t* tables,
+             int32_t* seq_lens, int32_t* cu_seqlens, int32_t* cu_splits, int32_t* split_seq,
+             int32_t* split_start);
+
+/* MemoryAllocator::copy_block over a flat pool (src/MemoryAllocator.cpp:76-85):
+ * memcpy of copy_bytes from frame src to frame dst, silently ignored for ids
+ * outside the pool. */
+void orc_copy_block(uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks, uint32_t src,
+                    uint32_t dst, uint64_t copy_bytes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QVP_ORACLE_H */

@@ -1,0 +1,210 @@
+// Batched block movement: copy-on-write materialisation and swap gather/scatter.
+//
+// copy_blocks replaces a loop of MemoryAllocator::copy_block calls, each a
+// std::memcpy of the whole padded frame (src/MemoryAllocator.cpp:76-85, caller
+// src/KVCacheManager.cpp:141-150), with one launch. Swap gather/scatter replace
+// HostSwapBackend::store / load (src/SwapBackend.cpp:10-39): whole frames move
+// between HBM and a pinned host arena, the GPU itself driving the host link.
+//
+// All three share one kernel: a list of (source, destination) segments of equal
+// length travels in the kernel arguments (no staging buffer, no extra copy), and
+// each workgroup moves a 16 KiB chunk of one segment with 16-byte accesses.
+#include "common.h"
+
+#include <algorithm>
+#include <vector>
+
+namespace {
+
+using qvp::fail;
+
+constexpr int kSegmentsPerLaunch = 128;
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 4;
+constexpr uint64_t kChunkBytes = static_cast<uint64_t>(kCopyThreads) * 16 * kCopyUnroll;
+
+struct SegmentList {
+    const uint8_t* src[kSegmentsPerLaunch];
+    uint8_t* dst[kSegmentsPerLaunch];
+};
+
+__global__ __launch_bounds__(kCopyThreads) void copy_segments(SegmentList list, uint64_t bytes) {
+    const uint8_t* __restrict__ src = list.src[blockIdx.y];
+    uint8_t* __restrict__ dst = list.dst[blockIdx.y];
+    if (src == dst) return;
+    const uint64_t chunk0 = static_cast<uint64_t>(blockIdx.x) * kChunkBytes;
+    const uint64_t chunk_end = min(chunk0 + kChunkBytes, bytes);
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0;
+    if (vec && chunk_end - chunk0 == kChunkBytes) {
+        const uint4* s4 = reinterpret_cast<const uint4*>(src + chunk0);
+        uint4* d4 = reinterpret_cast<uint4*>(dst + chunk0);
+        uint4 r[kCopyUnroll];
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) r[u] = s4[threadIdx.x + u * kCopyThreads];
+#pragma unroll
+        for (int u = 0; u < kCopyUnroll; ++u) d4[threadIdx.x + u * kCopyThreads] = r[u];
+        return;
+    }
+    if (vec) {
+        const uint64_t vec_end = chunk0 + (chunk_end - chunk0) / 16 * 16;
+        for (uint64_t off = chunk0 + 16u * threadIdx.x; off < vec_end; off += 16u * kCopyThreads) {
+            *reinterpret_cast<uint4*>(dst + off) = *reinterpret_cast<const uint4*>(src + off);
+        }
+        for (uint64_t off = vec_end + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
+        return;
+    }
+    for (uint64_t off = chunk0 + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
+}
+
+// Enqueues segments [0, n) in launches of kSegmentsPerLaunch.
+int launch_segments(const std::vector<const uint8_t*>& src, const std::vector<uint8_t*>& dst,
+                    uint64_t bytes, hipStream_t stream) {
+    const size_t n = src.size();
+    if (n == 0 || bytes == 0) return QVP_OK;
+    const uint64_t chunks = (bytes + kChunkBytes - 1) / kChunkBytes;
+    if (chunks > 0x7fffffffu) return fail(QVP_ERR_INVALID_ARGUMENT, "segment too large");
+    for (size_t first = 0; first < n; first += kSegmentsPerLaunch) {
+        const size_t count = std::min<size_t>(kSegmentsPerLaunch, n - first);
+        SegmentList list{};
+        for (size_t i = 0; i < count; ++i) {
+            list.src[i] = src[first + i];
+            list.dst[i] = dst[first + i];
+        }
+        hipLaunchKernelGGL(copy_segments, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(count)),
+                           dim3(kCopyThreads), 0, stream, list, bytes);
+        QVP_HIP(hipGetLastError());
+    }
+    return QVP_OK;
+}
+
+int check_frames(const uint32_t* ids, uint32_t count, uint32_t num_blocks, const char* what) {
+    if (count > 0 && ids == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "%s ids are NULL", what);
+    for (uint32_t i = 0; i < count; ++i) {
+        if (ids[i] >= num_blocks) {
+            return fail(QVP_ERR_UNMAPPED, "%s id %u at %u outside pool of %u blocks", what, ids[i], i,
+                        num_blocks);
+        }
+    }
+    return QVP_OK;
+}
+
+// Rejects a repeated id (distinct destinations are required so the result does
+// not depend on launch order).
+int check_distinct(const uint32_t* ids, uint32_t count, const char* what) {
+    std::vector<uint32_t> sorted(ids, ids + count);
+    std::sort(sorted.begin(), sorted.end());
+    for (uint32_t i = 1; i < count; ++i) {
+        if (sorted[i] == sorted[i - 1]) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "%s id %u appears twice", what, sorted[i]);
+        }
+    }
+    return QVP_OK;
+}
+
+int check_arena_ranges(const uint64_t* offsets, uint32_t count, uint64_t bytes, uint64_t arena_bytes,
+                       bool require_disjoint) {
+    if (count > 0 && offsets == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "offsets are NULL");
+    for (uint32_t i = 0; i < count; ++i) {
+        if (offsets[i] % 16 != 0) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "arena offset %llu is not 16-byte aligned",
+                        static_cast<unsigned long long>(offsets[i]));
+        }
+        if (offsets[i] > arena_bytes || bytes > arena_bytes - offsets[i]) {
+            return fail(QVP_ERR_CAPACITY, "arena range [%llu, +%llu) outside %llu bytes",
+                        static_cast<unsigned long long>(offsets[i]), static_cast<unsigned long long>(bytes),
+                        static_cast<unsigned long long>(arena_bytes));
+        }
+    }
+    if (require_disjoint && count > 1) {
+        std::vector<uint64_t> sorted(offsets, offsets + count);
+        std::sort(sorted.begin(), sorted.end());
+        for (uint32_t i = 1; i < count; ++i) {
+            if (sorted[i] - sorted[i - 1] < bytes) {
+                return fail(QVP_ERR_INVALID_ARGUMENT, "arena ranges at %llu and %llu overlap",
+                            static_cast<unsigned long long>(sorted[i - 1]),
+                            static_cast<unsigned long long>(sorted[i]));
+            }
+        }
+    }
+    return QVP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qvp_copy_blocks(void* kv_base, uint64_t block_stride, uint32_t num_blocks, const uint32_t* src_ids,
+                    const uint32_t* dst_ids, uint32_t num_pairs, uint64_t copy_bytes, void* stream) {
+    if (num_pairs == 0) return QVP_OK;
+    if (kv_base == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "kv_base is NULL");
+    if (copy_bytes > block_stride) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "copy of %llu bytes exceeds frame stride %llu",
+                    static_cast<unsigned long long>(copy_bytes), static_cast<unsigned long long>(block_stride));
+    }
+    QVP_TRY(check_frames(src_ids, num_pairs, num_blocks, "source"));
+    QVP_TRY(check_frames(dst_ids, num_pairs, num_blocks, "destination"));
+    QVP_TRY(check_distinct(dst_ids, num_pairs, "destination"));
+    // A destination that is another pair's source would make the result depend
+    // on the order in which workgroups run.
+    {
+        std::vector<uint32_t> srcs(src_ids, src_ids + num_pairs);
+        std::sort(srcs.begin(), srcs.end());
+        for (uint32_t i = 0; i < num_pairs; ++i) {
+            if (dst_ids[i] == src_ids[i]) continue;
+            if (std::binary_search(srcs.begin(), srcs.end(), dst_ids[i])) {
+                return fail(QVP_ERR_INVALID_ARGUMENT, "destination %u is also a source", dst_ids[i]);
+            }
+        }
+    }
+    uint8_t* base = static_cast<uint8_t*>(kv_base);
+    std::vector<const uint8_t*> src(num_pairs);
+    std::vector<uint8_t*> dst(num_pairs);
+    for (uint32_t i = 0; i < num_pairs; ++i) {
+        src[i] = base + static_cast<uint64_t>(src_ids[i]) * block_stride;
+        dst[i] = base + static_cast<uint64_t>(dst_ids[i]) * block_stride;
+    }
+    return launch_segments(src, dst, copy_bytes, qvp::as_stream(stream));
+}
+
+int qvp_swap_gather(const void* kv_base, uint64_t block_stride, uint32_t num_blocks,
+                    const uint32_t* frame_ids, const uint64_t* arena_offsets, uint32_t count, void* arena,
+                    uint64_t arena_bytes, uint64_t copy_bytes, void* stream) {
+    if (count == 0) return QVP_OK;
+    if (kv_base == nullptr || arena == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "NULL base or arena");
+    if (copy_bytes > block_stride) return fail(QVP_ERR_INVALID_ARGUMENT, "copy exceeds frame stride");
+    QVP_TRY(check_frames(frame_ids, count, num_blocks, "frame"));
+    QVP_TRY(check_arena_ranges(arena_offsets, count, copy_bytes, arena_bytes, true));
+    void* arena_dev = nullptr;
+    QVP_HIP(hipHostGetDevicePointer(&arena_dev, arena, 0));
+    const uint8_t* base = static_cast<const uint8_t*>(kv_base);
+    std::vector<const uint8_t*> src(count);
+    std::vector<uint8_t*> dst(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        src[i] = base + static_cast<uint64_t>(frame_ids[i]) * block_stride;
+        dst[i] = static_cast<uint8_t*>(arena_dev) + arena_offsets[i];
+    }
+    return launch_segments(src, dst, copy_bytes, qvp::as_stream(stream));
+}
+
+int qvp_swap_scatter(void* kv_base, uint64_t block_stride, uint32_t num_blocks, const uint32_t* frame_ids,
+                     const uint64_t* arena_offsets, uint32_t count, const void* arena, uint64_t arena_bytes,
+                     uint64_t copy_bytes, void* stream) {
+    if (count == 0) return QVP_OK;
+    if (kv_base == nullptr || arena == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "NULL base or arena");
+    if (copy_bytes > block_stride) return fail(QVP_ERR_INVALID_ARGUMENT, "copy exceeds frame stride");
+    QVP_TRY(check_frames(frame_ids, count, num_blocks, "frame"));
+    QVP_TRY(check_distinct(frame_ids, count, "frame"));
+    QVP_TRY(check_arena_ranges(arena_offsets, count, copy_bytes, arena_bytes, false));
+    void* arena_dev = nullptr;
+    QVP_HIP(hipHostGetDevicePointer(&arena_dev, const_cast<void*>(arena), 0));
+    uint8_t* base = static_cast<uint8_t*>(kv_base);
+    std::vector<const uint8_t*> src(count);
+    std::vector<uint8_t*> dst(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        src[i] = static_cast<const uint8_t*>(arena_dev) + arena_offsets[i];
+        dst[i] = base + static_cast<uint64_t>(frame_ids[i]) * block_stride;
+    }
+    return launch_segments(src, dst, copy_bytes, qvp::as_stream(stream));
+}
+
+}  // extern "C"

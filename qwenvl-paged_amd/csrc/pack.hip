@@ -1,0 +1,260 @@
+// Ragged-batch packing: per scheduler step, flatten the decode batch's block
+// tables into the device arrays the decode kernels index.
+//
+// Reference: docs/architecture.md:117-120 ("flatten entries() into the
+// [num_seqs, max_blocks_per_seq] tensor that a paged kernel indexes"),
+// include/qwenvl_paged/PagedAttention.h:15-22 (per-sequence context lengths)
+// and :73-89 (resolve every needed block before writing any output).
+//
+// Host work is one pass over the CSR input into a pinned staging buffer; the
+// buffers alternate between two calls so the host can fill one while the DMA
+// engine still reads the other, and the device receives all arrays in a single
+// asynchronous copy.
+#include "common.h"
+
+#include <algorithm>
+#include <new>
+
+namespace {
+
+constexpr uint32_t kSplitQuantum = 128;   // 4 waves x 32-token tiles
+constexpr uint32_t kDefaultSplit = 512;
+constexpr uint32_t kMaxSplit = 8192;
+constexpr size_t kAlignInts = 64;         // 256-byte alignment of sub-arrays
+
+size_t align_ints(size_t n) { return (n + kAlignInts - 1) / kAlignInts * kAlignInts; }
+
+struct Layout {
+    size_t tables, seq_lens, cu_seqlens, cu_splits, split_seq, split_start, total;
+};
+
+Layout make_layout(uint32_t num_seqs, uint32_t max_nb, uint32_t num_splits) {
+    Layout l{};
+    size_t off = 0;
+    l.tables = off;
+    off += align_ints(static_cast<size_t>(num_seqs) * max_nb);
+    l.seq_lens = off;
+    off += align_ints(num_seqs);
+    l.cu_seqlens = off;
+    off += align_ints(static_cast<size_t>(num_seqs) + 1);
+    l.cu_splits = off;
+    off += align_ints(static_cast<size_t>(num_seqs) + 1);
+    l.split_seq = off;
+    off += align_ints(num_splits);
+    l.split_start = off;
+    off += align_ints(num_splits);
+    l.total = off;
+    return l;
+}
+
+}  // namespace
+
+struct qvp_batch {
+    int32_t* staging[2]{nullptr, nullptr};
+    size_t staging_cap[2]{0, 0};  // in int32 elements
+    hipEvent_t staging_done[2]{nullptr, nullptr};
+    bool staging_pending[2]{false, false};
+    int parity{0};
+    int32_t* device{nullptr};
+    size_t device_cap{0};
+    bool valid{false};
+    qvp_packed_view view{};
+};
+
+using qvp::fail;
+
+extern "C" {
+
+int qvp_batch_create(qvp_batch** batch) {
+    if (batch == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "batch is NULL");
+    *batch = nullptr;
+    qvp_batch* b = new (std::nothrow) qvp_batch();
+    if (b == nullptr) return fail(QVP_ERR_OUT_OF_MEMORY, "batch descriptor");
+    for (int i = 0; i < 2; ++i) {
+        hipError_t err = hipEventCreateWithFlags(&b->staging_done[i], hipEventDisableTiming);
+        if (err != hipSuccess) {
+            if (i == 1) (void)hipEventDestroy(b->staging_done[0]);
+            delete b;
+            return qvp::hip_fail(err, "hipEventCreateWithFlags");
+        }
+    }
+    *batch = b;
+    return QVP_OK;
+}
+
+int qvp_batch_destroy(qvp_batch* batch) {
+    if (batch == nullptr) return QVP_OK;
+    int status = QVP_OK;
+    for (int i = 0; i < 2; ++i) {
+        if (batch->staging_pending[i]) (void)hipEventSynchronize(batch->staging_done[i]);
+        if (batch->staging[i] != nullptr && hipHostFree(batch->staging[i]) != hipSuccess) {
+            status = fail(QVP_ERR_DEVICE, "hipHostFree(staging)");
+        }
+        (void)hipEventDestroy(batch->staging_done[i]);
+    }
+    if (batch->device != nullptr && hipFree(batch->device) != hipSuccess) {
+        status = fail(QVP_ERR_DEVICE, "hipFree(batch)");
+    }
+    delete batch;
+    return status;
+}
+
+int qvp_batch_view(const qvp_batch* batch, qvp_packed_view* view) {
+    if (batch == nullptr || view == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "NULL argument");
+    if (!batch->valid) return fail(QVP_ERR_INVALID_ARGUMENT, "batch has not been packed");
+    *view = batch->view;
+    return QVP_OK;
+}
+
+int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
+             const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
+             uint32_t num_pool_blocks, uint32_t split_tokens, void* stream) {
+    if (batch == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "batch is NULL");
+    if (tokens_per_block == 0) return fail(QVP_ERR_INVALID_ARGUMENT, "tokens_per_block is 0");
+    if (num_seqs > 0 && (cu_blocks == nullptr || context_lens == nullptr)) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "cu_blocks or context_lens is NULL");
+    }
+    if (split_tokens == 0) split_tokens = kDefaultSplit;
+    if (split_tokens > kMaxSplit) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "split_tokens %u exceeds %u", split_tokens, kMaxSplit);
+    }
+    split_tokens = static_cast<uint32_t>(qvp::round_up(split_tokens, kSplitQuantum));
+
+    // Pass 1: validate everything before touching the batch.
+    uint32_t max_nb = 0;
+    uint32_t max_len = 0;
+    uint64_t num_splits = 0;
+    uint64_t total_tokens = 0;
+    if (num_seqs > 0 && cu_blocks[0] != 0) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "cu_blocks[0] must be 0");
+    }
+    for (uint32_t b = 0; b < num_seqs; ++b) {
+        const uint32_t len = context_lens[b];
+        if (len == 0) return fail(QVP_ERR_INVALID_ARGUMENT, "sequence %u has context_len 0", b);
+        if (cu_blocks[b + 1] < cu_blocks[b]) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "cu_blocks decreases at sequence %u", b);
+        }
+        const uint32_t mapped = cu_blocks[b + 1] - cu_blocks[b];
+        const uint32_t needed = (len + tokens_per_block - 1) / tokens_per_block;
+        if (needed > mapped) {
+            return fail(QVP_ERR_INVALID_ARGUMENT,
+                        "sequence %u needs %u blocks for %u tokens but maps %u", b, needed, len,
+                        mapped);
+        }
+        if (needed > 0 && block_ids == nullptr) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "block_ids is NULL");
+        }
+        const uint32_t* ids = block_ids + cu_blocks[b];
+        for (uint32_t j = 0; j < needed; ++j) {
+            if (ids[j] == QVP_UNMAPPED_BLOCK || ids[j] >= num_pool_blocks) {
+                return fail(QVP_ERR_UNMAPPED, "sequence %u logical block %u has no frame (%u)", b,
+                            j, ids[j]);
+            }
+        }
+        max_nb = std::max(max_nb, needed);
+        max_len = std::max(max_len, len);
+        num_splits += (len + split_tokens - 1) / split_tokens;
+        total_tokens += len;
+    }
+    if (num_pool_blocks > 0x7fffffffu) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "pool of %u blocks exceeds int32 ids", num_pool_blocks);
+    }
+    if (num_splits > 0x7fffffffu || total_tokens > 0x7fffffffu) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "batch too large for int32 indexing");
+    }
+
+    const Layout lay = make_layout(num_seqs, max_nb, static_cast<uint32_t>(num_splits));
+    const int slot = batch->parity;
+
+    // The staging buffer about to be reused may still be read by the copy of
+    // the call before last.
+    if (batch->staging_pending[slot]) {
+        QVP_HIP(hipEventSynchronize(batch->staging_done[slot]));
+        batch->staging_pending[slot] = false;
+    }
+    if (batch->staging_cap[slot] < lay.total) {
+        if (batch->staging[slot] != nullptr) QVP_HIP(hipHostFree(batch->staging[slot]));
+        batch->staging[slot] = nullptr;
+        batch->staging_cap[slot] = 0;
+        const size_t cap = std::max<size_t>(lay.total, 4096);
+        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&batch->staging[slot]), cap * sizeof(int32_t),
+                              hipHostMallocDefault));
+        batch->staging_cap[slot] = cap;
+    }
+    if (batch->device_cap < lay.total) {
+        batch->valid = false;
+        if (batch->device != nullptr) QVP_HIP(hipFree(batch->device));
+        batch->device = nullptr;
+        batch->device_cap = 0;
+        const size_t cap = std::max<size_t>(lay.total, 4096);
+        QVP_HIP(hipMalloc(reinterpret_cast<void**>(&batch->device), cap * sizeof(int32_t)));
+        batch->device_cap = cap;
+    }
+
+    // Pass 2: fill the staging buffer.
+    int32_t* h = batch->staging[slot];
+    int32_t* tables = h + lay.tables;
+    int32_t* seq_lens = h + lay.seq_lens;
+    int32_t* cu_seqlens = h + lay.cu_seqlens;
+    int32_t* cu_splits = h + lay.cu_splits;
+    int32_t* split_seq = h + lay.split_seq;
+    int32_t* split_start = h + lay.split_start;
+    int32_t token_acc = 0;
+    int32_t split_acc = 0;
+    for (uint32_t b = 0; b < num_seqs; ++b) {
+        const uint32_t len = context_lens[b];
+        const uint32_t needed = (len + tokens_per_block - 1) / tokens_per_block;
+        const uint32_t* ids = block_ids + cu_blocks[b];
+        int32_t* row = tables + static_cast<size_t>(b) * max_nb;
+        for (uint32_t j = 0; j < needed; ++j) row[j] = static_cast<int32_t>(ids[j]);
+        for (uint32_t j = needed; j < max_nb; ++j) row[j] = -1;
+        seq_lens[b] = static_cast<int32_t>(len);
+        cu_seqlens[b] = token_acc;
+        cu_splits[b] = split_acc;
+        token_acc += static_cast<int32_t>(len);
+        const uint32_t nsplit = (len + split_tokens - 1) / split_tokens;
+        for (uint32_t s = 0; s < nsplit; ++s) {
+            split_seq[split_acc] = static_cast<int32_t>(b);
+            split_start[split_acc] = static_cast<int32_t>(s * split_tokens);
+            ++split_acc;
+        }
+    }
+    cu_seqlens[num_seqs] = token_acc;
+    cu_splits[num_seqs] = split_acc;
+
+    hipStream_t s = qvp::as_stream(stream);
+    hipError_t err = hipMemcpyAsync(batch->device, h, lay.total * sizeof(int32_t),
+                                    hipMemcpyHostToDevice, s);
+    if (err != hipSuccess) {
+        batch->valid = false;
+        return qvp::hip_fail(err, "hipMemcpyAsync(pack)");
+    }
+    err = hipEventRecord(batch->staging_done[slot], s);
+    if (err != hipSuccess) {
+        batch->valid = false;
+        return qvp::hip_fail(err, "hipEventRecord(pack)");
+    }
+    batch->staging_pending[slot] = true;
+    batch->parity ^= 1;
+
+    int32_t* d = batch->device;
+    qvp_packed_view& v = batch->view;
+    v.block_tables = d + lay.tables;
+    v.seq_lens = d + lay.seq_lens;
+    v.cu_seqlens = d + lay.cu_seqlens;
+    v.cu_splits = d + lay.cu_splits;
+    v.split_seq = d + lay.split_seq;
+    v.split_start = d + lay.split_start;
+    v.num_seqs = num_seqs;
+    v.max_blocks_per_seq = max_nb;
+    v.num_splits = static_cast<uint32_t>(num_splits);
+    v.split_tokens = split_tokens;
+    v.tokens_per_block = tokens_per_block;
+    v.num_pool_blocks = num_pool_blocks;
+    v.max_seq_len = max_len;
+    v.total_tokens = total_tokens;
+    batch->valid = true;
+    return QVP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,247 @@
+"""GPU parity: paged decode through the C ABI against the CPU oracle.
+
+Mirrors tests/PagedAttention.test.cpp of the reference (numeric cases and
+refusals) at batch scale, plus the BASELINE configurations. The oracle is the
+C restatement of paged_attention_decode<T> (oracle/oracle.c), itself pinned
+bit-for-bit to the compiled reference in tests/test_oracle.py.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import qvp
+import workloads as W
+from helpers import F32_ABS_TOL, GpuRun, assert_close_bf16, oracle_decode, to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def _parity(w: W.Workload, out_dtypes=(None,), split_tokens=None):
+    run = GpuRun(w)
+    ref_out, ref32 = oracle_decode(w, run.image, run.query)
+    results = {}
+    for od in out_dtypes:
+        od = w.kv_dtype if od is None else od
+        got = to_f32(run.decode(out_dtype=od, split_tokens=split_tokens), od)
+        if w.kv_dtype == qvp.DTYPE_F32 and od == qvp.DTYPE_F32:
+            err = float(np.abs(got - ref32).max())
+            assert err <= F32_ABS_TOL, f"fp32 max abs {err:.3e}"
+            results[od] = {"max_abs": err}
+        elif od == qvp.DTYPE_F32:
+            results[od] = assert_close_bf16(got, ref32, f"{w.name} fp32 out")
+        else:
+            # Both sides round nearly equal fp32 values to 16 bits; compare the
+            # rounded values against the oracle's fp32 result.
+            results[od] = assert_close_bf16(got, ref32, f"{w.name} 16-bit out")
+    return results
+
+
+def test_config1_fp32_matches_oracle():
+    print("case: config1 fp32", flush=True)
+    _parity(W.config1())
+
+
+def test_config2_bf16_matches_oracle_fp32_and_bf16_outputs():
+    print("case: config2 bf16 B=64", flush=True)
+    _parity(W.config2(), out_dtypes=(qvp.DTYPE_F32, qvp.DTYPE_BF16))
+
+
+@pytest.mark.parametrize("split", [128, 256, 512, 1024, 4096])
+def test_split_size_does_not_change_the_result(split):
+    print(f"case: config2 B=8 split={split}", flush=True)
+    _parity(W.config2(seed=11, num_seqs=8), out_dtypes=(qvp.DTYPE_F32,), split_tokens=split)
+
+
+EDGE_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 511, 512, 513, 1000]
+
+
+@pytest.mark.parametrize("kv_dtype", [qvp.DTYPE_BF16, qvp.DTYPE_F32])
+def test_ragged_lengths_across_block_and_split_edges(kv_dtype):
+    print(f"case: edge lengths dtype={kv_dtype}", flush=True)
+    w = W.custom(EDGE_LENGTHS, 28, 4, 128, kv_dtype=kv_dtype, seed=5)
+    _parity(w, out_dtypes=(qvp.DTYPE_F32,))
+
+
+@pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (28, 4), (32, 4), (64, 4), (16, 1), (12, 2)])
+def test_grouped_query_head_shapes(hq, hkv):
+    print(f"case: gqa hq={hq} hkv={hkv}", flush=True)
+    w = W.custom([70, 300, 513], hq, hkv, 128, seed=hq * 31 + hkv)
+    _parity(w, out_dtypes=(qvp.DTYPE_F32,))
+
+
+@pytest.mark.parametrize("d", [4, 64, 80, 256])
+def test_other_head_dims_use_the_generic_kernel(d):
+    print(f"case: head_dim={d}", flush=True)
+    w = W.custom([9, 40, 77], 8, 2, d, seed=d)
+    _parity(w, out_dtypes=(qvp.DTYPE_F32,))
+
+
+@pytest.mark.parametrize("tpb", [4, 8, 32, 64])
+def test_other_block_sizes(tpb):
+    print(f"case: tokens_per_block={tpb}", flush=True)
+    w = W.custom([5, 129, 600], 28, 4, 128, tokens_per_block=tpb, seed=tpb)
+    _parity(w, out_dtypes=(qvp.DTYPE_F32,))
+
+
+def test_multi_layer_frames_read_only_the_requested_layer():
+    # Each layer holds different data (tests/PagedAttention.test.cpp:481-494).
+    for layer in (0, 1, 2):
+        print(f"case: 3-layer frames, layer {layer}", flush=True)
+        w = W.custom([33, 200], 28, 4, 128, num_layers=3, layer=layer, seed=9)
+        _parity(w, out_dtypes=(qvp.DTYPE_F32,))
+
+
+def test_fp16_cache_generic_path():
+    print("case: fp16 cache", flush=True)
+    w = W.custom([50, 130], 8, 2, 128, kv_dtype=qvp.DTYPE_F16, seed=3)
+    # fp16 pool: reinterpret the fp32 draws rounded to fp16.
+    image32 = W.custom([50, 130], 8, 2, 128, kv_dtype=qvp.DTYPE_F32, seed=3)
+    raw = image32.pool_image().view(np.float32)
+    image = raw.astype(np.float16).view(np.uint8)
+    q = image32.query().astype(np.float16).view(np.uint16)
+    run = GpuRun(w, image=image, query=q)
+    _, ref32 = oracle_decode(w, image, q)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    assert_close_bf16(got, ref32, "fp16 cache")
+
+
+def test_uniform_keys_average_the_values_on_the_mfma_path():
+    # Closed form (tests/PagedAttention.test.cpp:380-411): equal keys make the
+    # softmax uniform, so the output is the plain mean of the cached values.
+    w = W.custom([16 * 5 + 3], 7, 1, 128, seed=1)
+    image = w.pool_image()
+    frames = image.reshape(w.num_pool_blocks, w.block_stride)
+    ctx = int(w.context_lens[0])
+    st = w.strides
+    values = []
+    for t in range(ctx):
+        blk = int(w.ids[t // 16])
+        k_off = ((t % 16) * st["token_stride"]) * 2
+        v_off = (st["stream_stride"] + (t % 16) * st["token_stride"]) * 2
+        frames[blk, k_off:k_off + 256] = W.f32_to_bf16_bits(np.full(128, 0.25, np.float32)).view(np.uint8)
+        val = np.float32(t % 11 - 5) / np.float32(4.0)
+        values.append(val)
+        frames[blk, v_off:v_off + 256] = W.f32_to_bf16_bits(np.full(128, val, np.float32)).view(np.uint8)
+    run = GpuRun(w, image=image)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    expected = np.float64(np.mean(values))
+    assert np.abs(got - expected).max() <= 1e-5
+
+
+def test_one_hot_keys_select_each_logical_token_in_order():
+    # tests/PagedAttention.test.cpp:413-458 at the Qwen shape: token t's key is
+    # one-hot in dim t and a sharp query picks exactly that logical token out of
+    # scattered frames.
+    ctx = 100
+    w = W.custom([ctx], 1, 1, 128, seed=4, scale=50.0)
+    image = w.pool_image()
+    frames = image.reshape(w.num_pool_blocks, w.block_stride)
+    st = w.strides
+    for t in range(ctx):
+        blk = int(w.ids[t // 16])
+        k_off = ((t % 16) * st["token_stride"]) * 2
+        v_off = (st["stream_stride"] + (t % 16) * st["token_stride"]) * 2
+        key = np.zeros(128, np.float32)
+        key[t] = 1.0
+        frames[blk, k_off:k_off + 256] = W.f32_to_bf16_bits(key).view(np.uint8)
+        frames[blk, v_off:v_off + 256] = W.f32_to_bf16_bits(np.full(128, t + 1, np.float32)).view(np.uint8)
+    run = GpuRun(w, image=image)
+    for target in (0, 15, 16, 17, 63, 64, 99):
+        q = np.zeros((1, 1, 128), np.float32)
+        q[0, 0, target] = 1.0
+        run.q.upload(W.f32_to_bf16_bits(q))
+        got = run.decode(out_dtype=qvp.DTYPE_F32)
+        assert np.abs(got - (target + 1)).max() <= 1e-3 * (target + 1), f"target {target}"
+
+
+# --------------------------------------------------------------------------
+# Refusals: nothing is written when the call is refused
+# (tests/PagedAttention.test.cpp:255-376).
+# --------------------------------------------------------------------------
+
+
+def _prepared(w):
+    run = GpuRun(w)
+    out = qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4)
+    out.fill(0x7F)
+    return run, out
+
+
+def _args(run, out, **over):
+    w = run.w
+    kw = dict(query=run.q.ptr, out=out.ptr, kv_base=run.pool.base, block_stride=run.pool.stride, batch=run.batch,
+              kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_F32, layer=0, num_layers=w.num_layers,
+              num_query_heads=w.num_query_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+              tokens_per_block=w.tokens_per_block, scale=w.scale)
+    kw.update(over)
+    return qvp.decode_args(**kw)
+
+
+def _untouched(out):
+    return bool(np.all(out.download(np.uint8, out.nbytes) == 0x7F))
+
+
+def test_swapped_out_block_refuses_the_whole_batch_without_writing():
+    w = W.custom([40, 64], 28, 4, 128, seed=2)
+    run, out = _prepared(w)
+    run.batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks)
+    ids = w.ids.copy()
+    ids[4] = qvp.UNMAPPED_BLOCK  # second sequence's first block is swapped out
+    with pytest.raises(qvp.QvpError) as e:
+        run.batch.pack(ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks)
+    assert e.value.status == qvp.ERR_UNMAPPED
+    # The batch keeps its previous contents, and no decode ran.
+    assert _untouched(out)
+
+
+def test_pack_refuses_context_longer_than_the_mapped_blocks_and_zero_context():
+    w = W.custom([40], 4, 4, 128, seed=2)
+    batch = qvp.Batch()
+    with pytest.raises(qvp.QvpError) as e:
+        batch.pack(w.ids, w.cu_blocks, [49], 16, w.num_pool_blocks)
+    assert e.value.status == qvp.ERR_INVALID_ARGUMENT
+    with pytest.raises(qvp.QvpError) as e:
+        batch.pack(w.ids, w.cu_blocks, [0], 16, w.num_pool_blocks)
+    assert e.value.status == qvp.ERR_INVALID_ARGUMENT
+    with pytest.raises(qvp.QvpError) as e:
+        batch.pack(w.ids, w.cu_blocks, [40], 16, int(w.ids.max()))  # an id outside the pool
+    assert e.value.status == qvp.ERR_UNMAPPED
+
+
+@pytest.mark.parametrize(
+    "over",
+    [
+        {"num_query_heads": 27},     # does not group onto 4 kv heads
+        {"num_query_heads": 0},
+        {"layer": 1},                # beyond the block shape
+        {"head_dim": 256},           # layout would address past the frame
+        {"tokens_per_block": 8},     # batch was packed for 16
+        {"kv_dtype": 7},
+    ],
+)
+def test_invalid_decode_arguments_are_refused_before_launch(over):
+    w = W.custom([40, 64], 28, 4, 128, seed=2)
+    run, out = _prepared(w)
+    run.batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks)
+    with pytest.raises(qvp.QvpError) as e:
+        qvp.paged_decode(_args(run, out, **over))
+    assert e.value.status == qvp.ERR_INVALID_ARGUMENT
+    assert _untouched(out)
+
+
+def test_caller_workspace_too_small_is_refused_and_exact_size_works():
+    w = W.custom([300, 700], 28, 4, 128, seed=8)
+    run, out = _prepared(w)
+    run.batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks)
+    need = run.batch.workspace_bytes(28, 128)
+    small = qvp.DeviceBuffer(need - 256)
+    with pytest.raises(qvp.QvpError) as e:
+        qvp.paged_decode(_args(run, out, workspace=small.ptr, workspace_bytes=small.nbytes))
+    assert e.value.status == qvp.ERR_CAPACITY
+    assert _untouched(out)
+    ws = qvp.DeviceBuffer(need)
+    got = run.decode(out_dtype=qvp.DTYPE_F32, workspace=ws)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    assert_close_bf16(got, ref32, "caller workspace")
