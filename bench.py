@@ -1,0 +1,288 @@
+"""Benchmark of the paged-decode hot path on one MI355X.
+
+Workload: Qwen2-VL-7B single-layer decode, 28 query
+heads / 4 kv heads / head_dim 128, block size 16, bf16 KV cache, batch 64 with
+context lengths uniform on [512, 4096], block tables scattered over a shuffled
+pool holding 10% spare frames. Synthetic data (seeded N(0,1) queries, N(0,0.5)
+K/V, rounded to bf16).
+
+A step is one decode of the whole batch (the split-K kernel plus the split
+merge) with the packed batch and the cache already in HBM. Three independent
+copies of the pool rotate between steps so the 256 MB Infinity Cache cannot
+serve a step from the previous step's reads. `value` is algorithmic HBM bytes
+per step / step time. The pack-inclusive rate (host pack + pinned H2D + decode)
+is reported beside it as `step_with_pack_*`.
+
+`roofline` uses the split-K kernel's own average duration, measured with HIP
+events recorded on the decode stream around it. `cpu_baseline` times the
+compiled reference paged_attention_decode<T> (oracle/_ref) on this host over
+the same batch, single-threaded like the reference engine loop.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "qwenvl-paged_amd"))
+
+import numpy as np  # noqa: E402
+
+import qvp  # noqa: E402
+import workloads as W  # noqa: E402
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "paged-decode HBM GB/s (% of peak) + decode tokens/s at Qwen2-VL-7B shape"
+TRAFFIC_FILE = ROOT / "profiles" / "decode_mfma_bf16_d128_config2_traffic.json"
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(w: W.Workload, image: np.ndarray, query: np.ndarray, reps: int) -> dict:
+    """Times the reference CPU decode over the same batch (median of `reps`)."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle as O
+
+    tokens = w.num_seqs
+    algo = w.algorithmic_bytes()
+    if O.reference_available():
+        sess = O.RefSession(image, w.block_stride, w.num_pool_blocks, w.tokens_per_block, w.num_layers,
+                            w.num_kv_heads, w.head_dim, w.elem_bytes)
+        times = []
+        for _ in range(reps):
+            refused, _, secs = sess.decode(w.ids, w.cu_blocks, w.context_lens, O.ORC_BF16, query, w.layer,
+                                           w.num_query_heads, w.head_dim, w.scale)
+            assert refused == 0
+            times.append(secs)
+        sess.close()
+        kind = "reference"
+        what = "compiled reference paged_attention_decode<bf16> (oracle/_ref, g++ -O2), one call per sequence"
+    else:
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            refused, _, _ = O.decode_batch(image, w.block_stride, w.num_pool_blocks, w.ids, w.cu_blocks,
+                                           w.context_lens, O.ORC_BF16, query, w.layer, w.num_layers,
+                                           w.num_query_heads, w.num_kv_heads, w.head_dim, w.tokens_per_block,
+                                           w.scale, 1)
+            times.append(time.perf_counter() - t0)
+            assert refused == 0
+        kind = "port"
+        what = "C restatement of paged_attention_decode (oracle/oracle.c, gcc -O2)"
+    t = statistics.median(times)
+    return {
+        "value": algo / t / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": f"full config2 batch ({w.num_seqs} sequences, {int(w.context_lens.sum())} cached tokens), "
+                  f"median of {reps} runs of {what} on {cpu_model()} "
+                  f"({os.cpu_count()} logical CPUs visible, 1 used)",
+        "seconds_per_step": t,
+        "decode_tokens_per_s": tokens / t,
+    }
+
+
+def load_traffic() -> dict | None:
+    if TRAFFIC_FILE.exists():
+        try:
+            return json.loads(TRAFFIC_FILE.read_text())
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def copy_calibration(steps: int) -> int:
+    """copy_blocks of 128 x 1 MiB frames onto 128 others in one launch:
+    128 MiB read and 128 MiB written per launch, nothing else."""
+    nblocks = 1024
+    block = 1 << 20
+    pool = qvp.BlockPool(nblocks, block)
+    pool.upload_all(np.zeros(nblocks * pool.stride, np.uint8))
+    perm = W.permutation(1, nblocks)
+    src, dst = perm[:128], perm[128:256]
+    stream = qvp.Stream()
+    for _ in range(3):
+        qvp.copy_blocks(pool.base, pool.stride, nblocks, src, dst, block, stream)
+    stream.synchronize()
+    e0, e1 = qvp.Event(), qvp.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        qvp.copy_blocks(pool.base, pool.stride, nblocks, src, dst, block, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    moved = 2 * 128 * block
+    print(json.dumps({"mode": "copy_calibration", "bytes_read_per_launch": moved // 2,
+                      "bytes_written_per_launch": moved // 2, "avg_ms": ms,
+                      "read_plus_write_GBps": moved / (ms * 1e-3) / 1e9}))
+    return 0
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--split", type=int, default=512, help="split-K partition in tokens")
+    ap.add_argument("--pools", type=int, default=3, help="independent pool copies rotated between steps")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
+                         "used to scale rocprof FETCH_SIZE / WRITE_SIZE)")
+    args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.steps)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build measures one GPU; the decode shards by sequence or kv head "
+                                   "with no exchange (see DESIGN.md), and multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}))
+        return 2
+
+    w = W.config2()
+    t_setup = time.perf_counter()
+    image = w.pool_image()
+    query = w.query()
+    stream = qvp.Stream()
+    pools = []
+    for _ in range(max(1, args.pools)):
+        p = qvp.BlockPool(w.num_pool_blocks, w.block_bytes)
+        p.upload_all(image)
+        pools.append(p)
+    q = qvp.DeviceBuffer.from_array(query)
+    n_out = w.num_seqs * w.num_query_heads * w.head_dim
+    out = qvp.DeviceBuffer(n_out * 2)
+    batch = qvp.Batch()
+    view = batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, args.split, stream)
+    ws = qvp.DeviceBuffer(batch.workspace_bytes(w.num_query_heads, w.head_dim))
+    setup_s = time.perf_counter() - t_setup
+
+    def make_args(pool, ev=None):
+        return qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=pool.base, block_stride=pool.stride, batch=batch,
+                               kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_BF16, layer=w.layer,
+                               num_layers=w.num_layers, num_query_heads=w.num_query_heads,
+                               num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+                               tokens_per_block=w.tokens_per_block, scale=w.scale, strides=w.strides,
+                               workspace=ws.ptr, workspace_bytes=ws.nbytes, split_event=ev)
+
+    plain = [make_args(p) for p in pools]
+    for i in range(args.warmup):
+        qvp.paged_decode(plain[i % len(pools)], stream)
+    stream.synchronize()
+
+    # Timed region 1: K steps, nothing else on the stream.
+    qvp.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        qvp.paged_decode(plain[i % len(pools)], stream)
+    stream.synchronize()
+    qvp.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+
+    # Timed region 2: the same steps with HIP events around each kernel.
+    starts = [qvp.Event() for _ in range(args.steps)]
+    mids = [qvp.Event() for _ in range(args.steps)]
+    ends = [qvp.Event() for _ in range(args.steps)]
+    timed = [make_args(pools[i % len(pools)], mids[i]) for i in range(args.steps)]
+    qvp.synchronize()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        qvp.paged_decode(timed[i], stream)
+        ends[i].record(stream)
+    stream.synchronize()
+    split_ms = [starts[i].elapsed_ms(mids[i]) for i in range(args.steps)]
+    merge_ms = [mids[i].elapsed_ms(ends[i]) for i in range(args.steps)]
+
+    # Pack-inclusive step (host pack + pinned H2D of the tables + decode).
+    qvp.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, args.split, stream)
+        qvp.paged_decode(plain[i % len(pools)], stream)
+    stream.synchronize()
+    pack_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # Parity spot check of the last output against the CPU reference path is
+    # done by the test suite; here only make sure the output is finite.
+    res = out.download(np.uint16, n_out)
+    assert np.all(np.isfinite(W.bf16_bits_to_f32(res))), "non-finite decode output"
+
+    algo = w.algorithmic_bytes()
+    kernel_bytes = w.kv_bytes() + w.num_seqs * w.num_query_heads * w.head_dim * 2 + \
+        int(((w.context_lens.astype(np.int64) + 15) // 16).sum()) * 4 + w.num_seqs * 4
+    split_avg = statistics.mean(split_ms)
+    gbps = algo / (ms_per_step * 1e-3) / 1e9
+    achieved = kernel_bytes / (split_avg * 1e-3) / 1e9
+    traffic = load_traffic()
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q, N(0,0.5) K/V rounded to bf16; shuffled pool)",
+        "config": {
+            "workload": "config2: Qwen2-VL-7B single-layer paged decode, B=64, ctx U[512,4096], "
+                        "Hq28/Hkv4/D128, block 16, bf16 KV, pool +10% spare, 3 rotating pool copies",
+            "batch": w.num_seqs,
+            "cached_tokens": int(w.context_lens.sum()),
+            "split_tokens": view.split_tokens,
+            "num_splits": view.num_splits,
+            "parallelism": "single GPU",
+        },
+        "pct_of_peak_hbm": round(100.0 * gbps / PEAK_HBM_GBPS, 2),
+        "decode_tokens_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
+        "decode_tokens_per_s_28_layers_attention_only": round(w.num_seqs / (28 * ms_per_step * 1e-3), 1),
+        "algorithmic_bytes_per_step": algo,
+        "step_with_pack_ms": round(pack_ms, 5),
+        "step_with_pack_tokens_per_s": round(w.num_seqs / (pack_ms * 1e-3), 1),
+        "merge_kernel_avg_ms": round(statistics.mean(merge_ms), 5),
+        "roofline": {
+            "kernel": "decode_mfma_bf16_d128",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": traffic.get("bytes_per_launch") if traffic else None,
+            "kernel_avg_ms": round(split_avg, 5),
+            "kernel_bytes_per_launch": kernel_bytes,
+        },
+        "setup_s": round(setup_s, 2),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(w, image, query, args.cpu_reps)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -229,6 +229,9 @@ typedef struct qvp_decode_args {
     float scale;
     void* workspace;            /* device scratch for split partials, or NULL */
     uint64_t workspace_bytes;   /* size of workspace; ignored when it is NULL */
+    void* split_event;          /* optional hipEvent_t recorded on `stream` after the
+                                   split kernel and before the merge kernel (lets a
+                                   caller time the two kernels apart), or NULL */
 } qvp_decode_args;
 
 /* Bytes of workspace qvp_paged_decode needs for this batch and head shape. */

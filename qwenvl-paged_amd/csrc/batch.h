@@ -1,0 +1,59 @@
+// Internal definition of qvp_batch, shared by the packer and the decode
+// launcher (the decode caches its work schedule in the batch it runs on).
+#pragma once
+
+#include "common.h"
+
+#include <vector>
+
+// One contiguous run of 32-token tiles of one (sequence, kv head) segment that
+// a persistent decode workgroup processes: tiles [t0, t1) of segment (b, g),
+// whose sequence holds ctx tokens. A piece that is not the whole segment owns
+// workspace slot `slot`; the segment's slots are [seg_slot0, seg_slot0 +
+// seg_nslots) and counters[seg_slot0] counts the pieces that have finished.
+struct qvp_piece {
+    int32_t b, g, t0, t1, ctx, slot, seg_slot0, seg_nslots;
+};
+
+// Balanced schedule of the persistent MFMA decode for one packed batch and one
+// kv-head count. Device layout (int32 units, each array 256-byte aligned):
+//   wg_begin[num_wgs + 1]  CSR over pieces per workgroup
+//   pieces[num_pieces]     qvp_piece
+//   counters[num_slots]    completion counters (zero between launches)
+struct qvp_schedule {
+    bool valid{false};
+    uint64_t pack_generation{0};
+    uint32_t num_kv_heads{0};
+    uint32_t max_wgs{0};
+    uint32_t num_wgs{0};
+    uint32_t num_pieces{0};
+    uint32_t num_slots{0};
+    uint32_t max_partial_pieces_per_wg{0};
+    size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, total{0};  // int32 units
+    int32_t* staging{nullptr};
+    size_t staging_cap{0};
+    hipEvent_t staging_done{nullptr};
+    bool staging_pending{false};
+    int32_t* device{nullptr};
+    size_t device_cap{0};
+};
+
+struct qvp_batch {
+    int32_t* staging[2]{nullptr, nullptr};
+    size_t staging_cap[2]{0, 0};  // in int32 elements
+    hipEvent_t staging_done[2]{nullptr, nullptr};
+    bool staging_pending[2]{false, false};
+    int parity{0};
+    int32_t* device{nullptr};
+    size_t device_cap{0};
+    bool valid{false};
+    uint64_t generation{0};            // bumped by every successful pack
+    std::vector<int32_t> host_seq_lens;  // host copy of seq_lens for scheduling
+    qvp_packed_view view{};
+    qvp_schedule sched{};
+};
+
+namespace qvp {
+// Frees the schedule's buffers (called by qvp_batch_destroy).
+void destroy_schedule(qvp_schedule& s);
+}  // namespace qvp

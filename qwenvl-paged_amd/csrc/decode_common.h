@@ -1,0 +1,64 @@
+// Definitions shared by the paged-decode kernels and their launcher.
+#pragma once
+
+#include "batch.h"
+#include "common.h"
+
+namespace qvp {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Layout and batch arguments common to both decode paths (bytes unless noted).
+struct DecodeGeometry {
+    const uint8_t* kv_base;
+    uint64_t block_stride;
+    uint64_t k_off;         // frame start -> this layer's K half
+    uint64_t v_off;         // frame start -> this layer's V half
+    uint64_t token_stride;
+    uint64_t head_stride;
+    const int32_t* tables;  // [num_seqs][max_nb]
+    const int32_t* seq_lens;
+    const void* query;      // [num_seqs][Hq][D], cache element type
+    uint32_t max_nb;
+    uint32_t tpb;
+    uint32_t tpb_shift;     // log2(tpb) when tpb is a power of two
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t group;
+    uint32_t head_dim;
+    float scale_log2;       // scale * log2(e)
+};
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <typename T> __device__ inline float to_float(T v);
+template <> __device__ inline float to_float<float>(float v) { return v; }
+template <> __device__ inline float to_float<uint16_t>(uint16_t v) { return bf16_bits_to_float(v); }
+template <> __device__ inline float to_float<_Float16>(_Float16 v) { return static_cast<float>(v); }
+
+template <typename OutT> __device__ inline OutT from_float(float v);
+template <> __device__ inline float from_float<float>(float v) { return v; }
+template <> __device__ inline uint16_t from_float<uint16_t>(float v) { return float_to_bf16_bits(v); }
+template <> __device__ inline _Float16 from_float<_Float16>(float v) { return static_cast<_Float16>(v); }
+
+// Generic path: one workgroup per (split, query head), VALU only; splits are
+// the packer's fixed-size token partitions. Returns a qvp_status.
+int launch_generic_decode(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t kv_dtype,
+                          uint32_t out_dtype, void* out, void* workspace, hipEvent_t split_event,
+                          hipStream_t stream);
+uint64_t generic_workspace_bytes(const qvp_packed_view& v, uint32_t hq, uint32_t d);
+
+// MFMA path (bf16, head_dim 128, group <= 16, power-of-two tpb >= 16):
+// persistent workgroups over a balanced schedule built from the batch.
+bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr,
+                    uintptr_t kv_base_addr);
+int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t stream);
+uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim);
+int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t out_dtype, void* out,
+                       void* workspace, hipEvent_t split_event, hipStream_t stream);
+
+}  // namespace qvp

@@ -1,0 +1,189 @@
+// Generic paged decode: any element type, head_dim, GQA group and block size.
+//
+// One workgroup per (split, query head) over the packer's fixed token splits,
+// VALU arithmetic. Within a split it runs the reference's two passes
+// (include/qwenvl_paged/PagedAttention.h:98-118): scores and their maximum,
+// then weights, their sum and the value accumulator; a merge kernel then
+// combines the splits of each sequence. It serves fp32/fp16 caches and shapes
+// the MFMA kernel does not cover.
+#include "decode_common.h"
+
+namespace qvp {
+namespace {
+
+constexpr int kGenericThreads = 128;
+
+__device__ inline float block_reduce_max(float v, float* scratch) {
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+    __syncthreads();
+    float r = scratch[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x >> 6); ++w) r = fmaxf(r, scratch[w]);
+    __syncthreads();
+    return r;
+}
+
+__device__ inline float block_reduce_sum(float v, float* scratch) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) scratch[wave] = v;
+    __syncthreads();
+    float r = 0.f;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) r += scratch[w];
+    __syncthreads();
+    return r;
+}
+
+struct SplitArgs {
+    const int32_t* split_seq;
+    const int32_t* split_start;
+    uint32_t split_tokens;
+    float* ws_ml;   // [num_splits][Hq][2]
+    float* ws_acc;  // [num_splits][Hq][D]
+};
+
+template <typename T>
+__global__ __launch_bounds__(kGenericThreads) void decode_generic(DecodeGeometry p, SplitArgs sa) {
+    extern __shared__ float smem[];
+    float* q_s = smem;               // [head_dim]
+    float* s_s = smem + p.head_dim;  // [split_tokens]
+    __shared__ float red[kGenericThreads / 64];
+
+    const uint32_t split = blockIdx.x / p.num_q_heads;
+    const uint32_t h = blockIdx.x - split * p.num_q_heads;
+    const uint32_t g = h / p.group;
+    const int b = sa.split_seq[split];
+    const int start = sa.split_start[split];
+    const int ctx = p.seq_lens[b];
+    const int len = min(static_cast<int>(sa.split_tokens), ctx - start);
+    const int32_t* row = p.tables + static_cast<uint64_t>(b) * p.max_nb;
+    const uint32_t D = p.head_dim;
+
+    const T* q = static_cast<const T*>(p.query) + (static_cast<uint64_t>(b) * p.num_q_heads + h) * D;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) q_s[d] = to_float<T>(q[d]);
+    __syncthreads();
+
+    const uint64_t head_off = g * p.head_stride;
+    float mloc = -INFINITY;
+    for (int t = threadIdx.x; t < len; t += blockDim.x) {
+        const uint32_t tok = static_cast<uint32_t>(start + t);
+        const int32_t blk = row[tok / p.tpb];
+        const T* k = reinterpret_cast<const T*>(p.kv_base + static_cast<uint64_t>(blk) * p.block_stride + p.k_off +
+                                                (tok % p.tpb) * p.token_stride + head_off);
+        float dot = 0.f;
+        for (uint32_t d = 0; d < D; ++d) dot += q_s[d] * to_float<T>(k[d]);
+        const float sv = dot * p.scale_log2;
+        s_s[t] = sv;
+        mloc = fmaxf(mloc, sv);
+    }
+    const float m = block_reduce_max(mloc, red);
+    float lloc = 0.f;
+    for (int t = threadIdx.x; t < len; t += blockDim.x) {
+        const float w = fast_exp2(s_s[t] - m);
+        s_s[t] = w;
+        lloc += w;
+    }
+    const float l = block_reduce_sum(lloc, red);  // also orders the s_s writes before the reads below
+
+    float* acc_out = sa.ws_acc + (static_cast<uint64_t>(split) * p.num_q_heads + h) * D;
+    for (uint32_t d = threadIdx.x; d < D; d += blockDim.x) {
+        float acc = 0.f;
+        for (int t = 0; t < len; ++t) {
+            const uint32_t tok = static_cast<uint32_t>(start + t);
+            const int32_t blk = row[tok / p.tpb];
+            const T* v = reinterpret_cast<const T*>(p.kv_base + static_cast<uint64_t>(blk) * p.block_stride + p.v_off +
+                                                    (tok % p.tpb) * p.token_stride + head_off);
+            acc += s_s[t] * to_float<T>(v[d]);
+        }
+        acc_out[d] = acc;
+    }
+    if (threadIdx.x == 0) {
+        sa.ws_ml[(static_cast<uint64_t>(split) * p.num_q_heads + h) * 2 + 0] = m;
+        sa.ws_ml[(static_cast<uint64_t>(split) * p.num_q_heads + h) * 2 + 1] = l;
+    }
+}
+
+// out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) per (sequence, head).
+template <typename OutT>
+__global__ __launch_bounds__(128) void merge_splits(const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
+                                                    const int32_t* __restrict__ cu_splits, OutT* __restrict__ out,
+                                                    uint32_t num_q_heads, uint32_t head_dim) {
+    const uint32_t b = blockIdx.x / num_q_heads;
+    const uint32_t h = blockIdx.x - b * num_q_heads;
+    const int s0 = cu_splits[b];
+    const int s1 = cu_splits[b + 1];
+    float mmax = -INFINITY;
+    for (int s = s0; s < s1; ++s) mmax = fmaxf(mmax, ws_ml[(static_cast<uint64_t>(s) * num_q_heads + h) * 2]);
+    float lsum = 0.f;
+    for (int s = s0; s < s1; ++s) {
+        const uint64_t idx = static_cast<uint64_t>(s) * num_q_heads + h;
+        lsum += ws_ml[idx * 2 + 1] * fast_exp2(ws_ml[idx * 2] - mmax);
+    }
+    OutT* o = out + (static_cast<uint64_t>(b) * num_q_heads + h) * head_dim;
+    for (uint32_t d = threadIdx.x; d < head_dim; d += blockDim.x) {
+        float acc = 0.f;
+        for (int s = s0; s < s1; ++s) {
+            const uint64_t idx = static_cast<uint64_t>(s) * num_q_heads + h;
+            acc += ws_acc[idx * head_dim + d] * fast_exp2(ws_ml[idx * 2] - mmax);
+        }
+        o[d] = from_float<OutT>(acc / lsum);
+    }
+}
+
+}  // namespace
+
+uint64_t generic_workspace_bytes(const qvp_packed_view& v, uint32_t hq, uint32_t d) {
+    const uint64_t heads = static_cast<uint64_t>(v.num_splits) * hq;
+    return round_up(heads * 2 * sizeof(float), 256) + round_up(heads * d * sizeof(float), 256);
+}
+
+int launch_generic_decode(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t kv_dtype, uint32_t out_dtype,
+                          void* out, void* workspace, hipEvent_t split_event, hipStream_t stream) {
+    const uint64_t heads = static_cast<uint64_t>(v.num_splits) * g.num_q_heads;
+    SplitArgs sa{};
+    sa.split_seq = v.split_seq;
+    sa.split_start = v.split_start;
+    sa.split_tokens = v.split_tokens;
+    sa.ws_ml = static_cast<float*>(workspace);
+    sa.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + round_up(heads * 2 * sizeof(float), 256));
+    const size_t shmem = (static_cast<size_t>(g.head_dim) + v.split_tokens) * sizeof(float);
+    if (shmem > 64 * 1024) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "head_dim %u with split %u needs %zu bytes of LDS", g.head_dim,
+                    v.split_tokens, shmem);
+    }
+    const dim3 grid(static_cast<unsigned>(heads));
+    switch (kv_dtype) {
+        case QVP_DTYPE_F32:
+            hipLaunchKernelGGL(decode_generic<float>, grid, dim3(kGenericThreads), shmem, stream, g, sa);
+            break;
+        case QVP_DTYPE_BF16:
+            hipLaunchKernelGGL(decode_generic<uint16_t>, grid, dim3(kGenericThreads), shmem, stream, g, sa);
+            break;
+        default:
+            hipLaunchKernelGGL(decode_generic<_Float16>, grid, dim3(kGenericThreads), shmem, stream, g, sa);
+            break;
+    }
+    QVP_HIP(hipGetLastError());
+    if (split_event != nullptr) QVP_HIP(hipEventRecord(split_event, stream));
+
+    const dim3 mgrid(v.num_seqs * g.num_q_heads);
+    switch (out_dtype) {
+        case QVP_DTYPE_F32:
+            hipLaunchKernelGGL(merge_splits<float>, mgrid, dim3(128), 0, stream, sa.ws_ml, sa.ws_acc, v.cu_splits,
+                               static_cast<float*>(out), g.num_q_heads, g.head_dim);
+            break;
+        case QVP_DTYPE_BF16:
+            hipLaunchKernelGGL(merge_splits<uint16_t>, mgrid, dim3(128), 0, stream, sa.ws_ml, sa.ws_acc, v.cu_splits,
+                               static_cast<uint16_t*>(out), g.num_q_heads, g.head_dim);
+            break;
+        default:
+            hipLaunchKernelGGL(merge_splits<_Float16>, mgrid, dim3(128), 0, stream, sa.ws_ml, sa.ws_acc, v.cu_splits,
+                               static_cast<_Float16*>(out), g.num_q_heads, g.head_dim);
+            break;
+    }
+    QVP_HIP(hipGetLastError());
+    return QVP_OK;
+}
+
+}  // namespace qvp

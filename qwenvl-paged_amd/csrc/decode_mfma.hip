@@ -1,0 +1,642 @@
+// Persistent MFMA paged decode for bf16 caches with head_dim 128.
+//
+// Semantics: include/qwenvl_paged/PagedAttention.h:53-127 (softmax(scale q K^T) V
+// per query head, GQA head h reads kv head h / (Hq / Hkv), fp32 accumulation).
+//
+// Work decomposition. Every (sequence b, kv head g) pair is a segment of
+// ceil(len_b / 32) tiles of 32 tokens. The host lays all segments end to end
+// and cuts the sequence into one contiguous, equal-sized tile range per
+// workgroup (two resident workgroups per CU, launched once: no tail of
+// half-empty rounds, no per-item start-up cost). A range covers one or more
+// pieces (its intersection with segments). Inside a piece the four waves of the
+// workgroup take tiles round-robin, keep an online-softmax state (running max
+// m, running sum l, unnormalised accumulator O) and merge it through LDS when
+// the piece ends. A piece that is a whole segment writes the final output; the
+// other pieces write (m, l, O) to a workspace slot. When a workgroup has run
+// through its range it publishes its slots (one agent-scope release fence, then
+// one atomic increment of each segment's counter); the workgroup that completes
+// a segment's count merges its slots in place, out = sum_s O_s 2^(m_s - M) /
+// sum_s l_s 2^(m_s - M) with M = max_s m_s, and resets the counter for the next
+// launch. Publishing once at the end keeps the fence (which waits for every
+// outstanding memory operation of the wave) off the prefetch pipeline.
+// Each wave prefetches its next tile (possibly in the next piece) before it
+// computes the current one, so loads stay in flight across piece boundaries.
+//
+// MFMA mapping (v_mfma_f32_16x16x32_bf16; lane l = (c = l % 16, j = l / 16);
+// A[row][k] comes from lane (row, k / 8), B[k][col] from lane (col, k / 8), and
+// C[4j + r][c] lands in register r of lane (c, j)):
+//   QK^T is computed transposed, S^T = K Q^T, per 16-token half u of a tile.
+//   Row r of half u carries token (r / 4) + 16u + 4 (r % 4), so C register r of
+//   lane (c, j) is the score of token j + 4 (4u + r) for query head c. The
+//   query-head group of the kv head fills the 16 columns (up to 16 heads), so
+//   each K/V byte is read from HBM once for the whole group. The four k-groups
+//   of QK MFMA i cover head dims 32i .. 32i + 31.
+//   PV is computed as O^T = V^T P^T. Lane (c, j) holds P for tokens j + 4q,
+//   q = 0..7, which is the B operand as it stands (k slot q <-> token j + 4q).
+//   V is read with 16-byte coalesced loads, lane (c, j) of load q taking dims
+//   8c .. 8c + 7 of token 4q + j; with row x of PV MFMA n standing for dim
+//   8x + n, lane (c, j) already holds its A operand (element n of its 8 loads)
+//   and only an in-register 16-bit transpose is needed. P enters the bf16 MFMA
+//   as hi + lo (hi = P truncated to bf16, lo = P - hi rounded to bf16), which
+//   keeps the weights at about 2^-16 relative error. C register r of PV MFMA n
+//   in lane (c, j) is O[head c][dim 32j + 8r + n].
+#include "decode_common.h"
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+namespace qvp {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kTileTokens = 32;
+constexpr int kD = 128;
+constexpr int kRowPad = kD + 4;
+constexpr int kMinTilesPerWg = 4;
+constexpr int kWgsPerCu = 2;
+// A workgroup's range is contiguous, so only its first and last pieces can be
+// partial segments.
+constexpr int kMaxPartialPerWg = 2;
+// Slots combined per round of loads in the end-of-range merge.
+constexpr int kMergeChunk = 8;
+
+struct MfmaArgs {
+    const qvp_piece* pieces;
+    const int32_t* wg_begin;
+    int32_t* counters;
+    float* ws_ml;   // [slot][group][2] : running max (base 2), running sum
+    float* ws_acc;  // [slot][group][128]
+    void* out;      // [num_seqs][Hq][128]
+};
+
+struct KvTile {
+    u32x4 k[2][4];  // [half u][QK mfma i]
+    u32x4 v[8];     // [load q]
+};
+
+__device__ inline u32x4 load16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// A tile of one wave's sequence with its block ids already fetched, so its
+// loads can be issued without waiting on the block table.
+struct TileRef {
+    int b, g, t, ctx;
+    int32_t blk0, blk1;  // frames of tokens 32t .. 32t+15 and 32t+16 .. 32t+31
+};
+
+// Advances (pi, t) to this wave's next tile: t + 4 in the same piece, else the
+// first piece after it where the wave has a tile (round-robin start t0 + wave).
+// Starts from piece pi when t < 0. Returns false when the range is exhausted.
+__device__ inline bool next_tile(const MfmaArgs& a, int pe, int wave, int& pi, int& t) {
+    if (t >= 0) {
+        if (t + kWaves < a.pieces[pi].t1) {
+            t += kWaves;
+            return true;
+        }
+        ++pi;
+    }
+    for (; pi < pe; ++pi) {
+        const qvp_piece d = a.pieces[pi];
+        if (d.t0 + wave < d.t1) {
+            t = d.t0 + wave;
+            return true;
+        }
+    }
+    t = -1;
+    return false;
+}
+
+// Fetches the block ids of tile t of piece pi. A 16-token half never straddles
+// a block (tpb is a power of two >= 16); tokens past the context fall back to
+// the last valid block.
+__device__ inline TileRef resolve_tile(const DecodeGeometry& p, const MfmaArgs& a, int pi, int t) {
+    const qvp_piece d = a.pieces[pi];
+    TileRef r;
+    r.b = d.b;
+    r.g = d.g;
+    r.t = t;
+    r.ctx = d.ctx;
+    const int32_t* row = p.tables + static_cast<uint64_t>(d.b) * p.max_nb;
+    const int tok0 = t * kTileTokens;
+    r.blk0 = row[min(tok0, r.ctx - 1) >> p.tpb_shift];
+    r.blk1 = row[min(tok0 + 16, r.ctx - 1) >> p.tpb_shift];
+    return r;
+}
+
+// Issues the 16 loads of a tile. Tokens at or past ctx read in-frame bytes of
+// the last valid block; compute masks their scores and zeroes their values when
+// it consumes the tile (doing it here would make the wave wait for the loads it
+// is prefetching).
+__device__ inline void load_tile(const DecodeGeometry& p, const TileRef& r, int c, int j, KvTile& tile) {
+    const uint32_t tmask = p.tpb - 1;
+    const int tok0 = r.t * kTileTokens;
+    const uint8_t* head_base = p.kv_base + static_cast<uint64_t>(r.g) * p.head_stride;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const uint8_t* frame = head_base + static_cast<uint64_t>(u == 0 ? r.blk0 : r.blk1) * p.block_stride;
+        const int ktok = tok0 + 16 * u + (c >> 2) + 4 * (c & 3);
+        const uint8_t* kp = frame + p.k_off + static_cast<uint64_t>(ktok & tmask) * p.token_stride + 16u * j;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tile.k[u][i] = load16(kp + 64 * i);
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            const int q = 4 * u + qq;
+            const int vtok = tok0 + 4 * q + j;
+            const uint8_t* vp = frame + p.v_off + static_cast<uint64_t>(vtok & tmask) * p.token_stride + 16u * c;
+            tile.v[q] = load16(vp);
+        }
+    }
+}
+
+// Reductions over the four lanes (c, 0..3) of one query head: lanes l, l^16,
+// l^32, l^48, through the gfx950 row/half swaps (VALU only, so they never wait
+// on LDS or scalar-memory counters).
+__device__ inline float max_over_j(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ inline float sum_over_j(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroup barrier that orders LDS only: outstanding global loads (the next
+// tile) stay in flight across it.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One tile of online softmax + PV for the wave.
+__device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0, int ctx, float scale_log2,
+                                    int j, float& m_run, float& l_run, floatx4 (&o)[8]) {
+    float s[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[u][i]),
+                                                          __builtin_bit_cast(bf16x8_t, qop[i]), acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = tok0 + j + 16 * u + 4 * r;
+            s[u][r] = (tok < ctx) ? acc[r] * scale_log2 : -INFINITY;
+        }
+    }
+
+    // The four lanes (c, 0..3) of query head c share one running max.
+    float mt = s[0][0];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[u][r]);
+    mt = max_over_j(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+
+    float psum = 0.f;
+    uint32_t phi[4], plo[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+            const float p0 = fast_exp2(s[u][r] - m_new);
+            const float p1 = fast_exp2(s[u][r + 1] - m_new);
+            psum += p0 + p1;
+            const uint32_t h0 = __float_as_uint(p0) >> 16;
+            const uint32_t h1 = __float_as_uint(p1) >> 16;
+            const uint32_t l0 = float_to_bf16_bits(p0 - __uint_as_float(h0 << 16));
+            const uint32_t l1 = float_to_bf16_bits(p1 - __uint_as_float(h1 << 16));
+            phi[2 * u + r / 2] = h0 | (h1 << 16);
+            plo[2 * u + r / 2] = l0 | (l1 << 16);
+        }
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[n] *= alpha;
+
+    const u32x4 bhi = {phi[0], phi[1], phi[2], phi[3]};
+    const u32x4 blo = {plo[0], plo[1], plo[2], plo[3]};
+    // Values of tokens past the context are zeroed in place (their weights are
+    // 0, but the bytes read for them are not data and 0 * NaN would poison O).
+    // Only the last tile of a sequence has such tokens.
+    if (tok0 + kTileTokens > ctx) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (tok0 + 4 * q + j >= ctx) cur.v[q] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    const u32x4 (&v)[8] = cur.v;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const int w = n >> 1;
+        u32x4 a;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t x = v[2 * k][w];
+            const uint32_t y = v[2 * k + 1][w];
+            a[k] = (n & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
+        }
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bhi), o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, blo), o[n], 0, 0, 0);
+    }
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(DecodeGeometry p, MfmaArgs a) {
+    __shared__ float sm_m[kWaves][16];
+    __shared__ float sm_l[kWaves][16];
+    __shared__ float sm_o[kWaves][16][kRowPad];
+    __shared__ int sm_merge[kMaxPartialPerWg];
+
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15;
+    const int j = lane >> 4;
+    const int G = static_cast<int>(p.group);
+
+    const int pb = a.wg_begin[blockIdx.x];
+    const int pe = a.wg_begin[blockIdx.x + 1];
+
+    // Software pipeline per wave: while the current tile is computed, the next
+    // tile's loads are in flight (nxt) and the block ids of the tile after that
+    // are being fetched (r2), so no table lookup sits between a tile's arrival
+    // and the issue of the following loads. (pi2, t2) is the cursor of r2.
+    KvTile nxt;
+    int pi2 = pb;
+    int t2 = -1;
+    bool have_partial = false;
+    bool has2 = next_tile(a, pe, wave, pi2, t2);
+    if (has2) load_tile(p, resolve_tile(p, a, pi2, t2), c, j, nxt);
+    has2 = has2 && next_tile(a, pe, wave, pi2, t2);
+    TileRef r2{};
+    if (has2) r2 = resolve_tile(p, a, pi2, t2);
+
+    for (int pi = pb; pi < pe; ++pi) {
+        const qvp_piece d = a.pieces[pi];
+        const int ctx = d.ctx;
+
+        // Query B operand: lane (c, j), MFMA i -> Q[head g*G + c][dims 32i + 8j .. +8].
+        u32x4 qop[4];
+        {
+            const bool live = c < G;
+            const uint16_t* q = static_cast<const uint16_t*>(p.query) +
+                                (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + (live ? c : 0)) * kD;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
+                qop[i] = live ? v : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+
+        floatx4 o[8];
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY;
+        float l_run = 0.f;
+
+        for (int t = d.t0 + wave; t < d.t1; t += kWaves) {
+            KvTile cur = nxt;
+            if (has2) load_tile(p, r2, c, j, nxt);
+            has2 = has2 && next_tile(a, pe, wave, pi2, t2);
+            if (has2) r2 = resolve_tile(p, a, pi2, t2);
+            compute_tile(cur, qop, t * kTileTokens, ctx, p.scale_log2, j, m_run, l_run, o);
+        }
+
+        // Merge the four waves' states for this piece.
+        l_run = sum_over_j(l_run);
+        if (j == 0) {
+            sm_m[wave][c] = m_run;
+            sm_l[wave][c] = l_run;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int n = 0; n < 8; ++n) sm_o[wave][c][32 * j + 8 * r + n] = o[n][r];
+        lds_barrier();
+
+        const int slot = d.slot;
+        have_partial = have_partial || slot >= 0;
+        for (int e = threadIdx.x; e < G * kD; e += kThreads) {
+            const int hc = e >> 7;
+            const int dd = e & (kD - 1);
+            float mmax = sm_m[0][hc];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) mmax = fmaxf(mmax, sm_m[w][hc]);
+            float acc = 0.f;
+            float lsum = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const float f = fast_exp2(sm_m[w][hc] - mmax);
+                acc += sm_o[w][hc][dd] * f;
+                lsum += sm_l[w][hc] * f;
+            }
+            if (slot < 0) {
+                OutT* out = static_cast<OutT*>(a.out);
+                out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + hc) * kD + dd] =
+                    from_float<OutT>(acc / lsum);
+            } else {
+                // Agent-scope stores reach the point of coherence shared by
+                // all XCDs; no cache maintenance is needed to publish them.
+                const uint64_t row = static_cast<uint64_t>(slot) * G + hc;
+                __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (dd == 0) {
+                    __hip_atomic_store(&a.ws_ml[row * 2 + 0], mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&a.ws_ml[row * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        lds_barrier();
+    }
+
+    if (!have_partial) return;
+
+    // Count this workgroup's partial slots in; the workgroup whose increment
+    // completes a segment merges it. The barrier waits for every outstanding
+    // memory operation of the workgroup, so the slot stores above have
+    // completed at the point of coherence before any counter moves.
+    __syncthreads();
+    // One thread per partial piece (at most kMaxPartialPerWg of them) bumps
+    // that segment's counter; the increments run in parallel.
+    if (threadIdx.x < kMaxPartialPerWg) {
+        int found = -1;
+        int k = 0;
+        for (int pi = pb; pi < pe; ++pi) {
+            if (a.pieces[pi].slot < 0) continue;
+            if (k++ == static_cast<int>(threadIdx.x)) {
+                found = pi;
+                break;
+            }
+        }
+        int mine = -1;
+        if (found >= 0) {
+            const qvp_piece d = a.pieces[found];
+            const int done = __hip_atomic_fetch_add(&a.counters[d.seg_slot0], 1, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+            if (done == d.seg_nslots - 1) mine = found;
+        }
+        sm_merge[threadIdx.x] = mine;
+    }
+    __syncthreads();
+    OutT* out = static_cast<OutT*>(a.out);
+    for (int k = 0; k < kMaxPartialPerWg; ++k) {
+        const int pm = sm_merge[k];
+        if (pm < 0) continue;
+        const qvp_piece d = a.pieces[pm];
+        const int s0 = d.seg_slot0;
+        const int ns = d.seg_nslots;
+        for (int e = threadIdx.x; e < G * kD; e += kThreads) {
+            const int hc = e >> 7;
+            const int dd = e & (kD - 1);
+            // All slot values are loaded in one round (agent-scope loads read
+            // the slots of other workgroups, on other XCDs, from the point of
+            // coherence), then combined.
+            float mmax = -INFINITY;
+            float acc = 0.f;
+            float lsum = 0.f;
+            for (int c0 = 0; c0 < ns; c0 += kMergeChunk) {
+                float m[kMergeChunk], l[kMergeChunk], o[kMergeChunk];
+#pragma unroll
+                for (int x = 0; x < kMergeChunk; ++x) {
+                    m[x] = -INFINITY;
+                    l[x] = 0.f;
+                    o[x] = 0.f;
+                    if (c0 + x < ns) {
+                        const uint64_t row = static_cast<uint64_t>(s0 + c0 + x) * G + hc;
+                        m[x] = __hip_atomic_load(&a.ws_ml[row * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        l[x] = __hip_atomic_load(&a.ws_ml[row * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        o[x] = __hip_atomic_load(&a.ws_acc[row * kD + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+                float cm = mmax;
+#pragma unroll
+                for (int x = 0; x < kMergeChunk; ++x) cm = fmaxf(cm, m[x]);
+                const float rescale = fast_exp2(mmax - cm);
+                acc *= rescale;
+                lsum *= rescale;
+#pragma unroll
+                for (int x = 0; x < kMergeChunk; ++x) {
+                    const float f = fast_exp2(m[x] - cm);
+                    acc += o[x] * f;
+                    lsum += l[x] * f;
+                }
+                mmax = cm;
+            }
+            out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + hc) * kD + dd] = from_float<OutT>(acc / lsum);
+        }
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(&a.counters[s0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Resident workgroups per device (two per CU), cached per device ordinal.
+std::mutex g_dev_mutex;
+std::vector<uint32_t> g_dev_wgs;
+
+int device_max_wgs(uint32_t* wgs) {
+    int dev = 0;
+    QVP_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_dev_mutex);
+    if (g_dev_wgs.size() <= static_cast<size_t>(dev)) g_dev_wgs.resize(dev + 1, 0);
+    if (g_dev_wgs[dev] == 0) {
+        int cus = 0;
+        QVP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        g_dev_wgs[dev] = static_cast<uint32_t>(std::max(1, cus) * kWgsPerCu);
+    }
+    *wgs = g_dev_wgs[dev];
+    return QVP_OK;
+}
+
+size_t align_ints(size_t n) { return (n + 63) / 64 * 64; }
+
+}  // namespace
+
+void destroy_schedule(qvp_schedule& s) {
+    if (s.staging_pending) (void)hipEventSynchronize(s.staging_done);
+    if (s.staging != nullptr) (void)hipHostFree(s.staging);
+    if (s.staging_done != nullptr) (void)hipEventDestroy(s.staging_done);
+    if (s.device != nullptr) (void)hipFree(s.device);
+    s = qvp_schedule{};
+}
+
+bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr, uintptr_t kv_base_addr) {
+    const bool pow2 = g.tpb != 0 && (g.tpb & (g.tpb - 1)) == 0;
+    const bool aligned = (g.block_stride % 16 == 0) && (g.k_off % 16 == 0) && (g.v_off % 16 == 0) &&
+                         (g.token_stride % 16 == 0) && (g.head_stride % 16 == 0) && (kv_base_addr % 16 == 0) &&
+                         (query_addr % 16 == 0);
+    return kv_dtype == QVP_DTYPE_BF16 && g.head_dim == kD && g.group >= 1 && g.group <= 16 && pow2 && g.tpb >= 16 &&
+           aligned;
+}
+
+int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t stream) {
+    qvp_schedule& s = batch->sched;
+    uint32_t max_wgs = 0;
+    QVP_TRY(device_max_wgs(&max_wgs));
+    if (s.valid && s.pack_generation == batch->generation && s.num_kv_heads == num_kv_heads &&
+        s.max_wgs == max_wgs) {
+        return QVP_OK;
+    }
+    s.valid = false;
+
+    // Segments (b, g), b-major, and their tile counts.
+    const std::vector<int32_t>& lens = batch->host_seq_lens;
+    const size_t nseg = lens.size() * num_kv_heads;
+    std::vector<uint64_t> seg_cum(nseg + 1, 0);
+    for (size_t b = 0; b < lens.size(); ++b) {
+        const uint64_t tiles = (static_cast<uint64_t>(lens[b]) + kTileTokens - 1) / kTileTokens;
+        for (uint32_t g = 0; g < num_kv_heads; ++g) {
+            const size_t sidx = b * num_kv_heads + g;
+            seg_cum[sidx + 1] = seg_cum[sidx] + tiles;
+        }
+    }
+    const uint64_t total = seg_cum[nseg];
+    const uint64_t wgs64 =
+        std::min<uint64_t>(max_wgs, std::max<uint64_t>(1, (total + kMinTilesPerWg - 1) / kMinTilesPerWg));
+    const uint32_t W = static_cast<uint32_t>(wgs64);
+
+    // Equal contiguous tile ranges, cut at segment boundaries into pieces.
+    std::vector<int32_t> wg_begin(W + 1);
+    std::vector<qvp_piece> pieces;
+    pieces.reserve(W + nseg);
+    size_t seg = 0;
+    for (uint32_t w = 0; w < W; ++w) {
+        const uint64_t lo = total * w / W;
+        const uint64_t hi = total * (w + 1) / W;
+        wg_begin[w] = static_cast<int32_t>(pieces.size());
+        uint64_t pos = lo;
+        while (pos < hi) {
+            while (seg_cum[seg + 1] <= pos) ++seg;
+            const uint64_t end = std::min(hi, seg_cum[seg + 1]);
+            qvp_piece pc{};
+            pc.b = static_cast<int32_t>(seg / num_kv_heads);
+            pc.g = static_cast<int32_t>(seg % num_kv_heads);
+            pc.t0 = static_cast<int32_t>(pos - seg_cum[seg]);
+            pc.t1 = static_cast<int32_t>(end - seg_cum[seg]);
+            pc.ctx = lens[pc.b];
+            pc.slot = -1;
+            pc.seg_slot0 = -1;
+            pc.seg_nslots = 0;
+            pieces.push_back(pc);
+            pos = end;
+        }
+    }
+    wg_begin[W] = static_cast<int32_t>(pieces.size());
+
+    // Pieces of one segment are adjacent; whole-segment pieces need no slot.
+    int32_t next_slot = 0;
+    for (size_t i = 0; i < pieces.size();) {
+        size_t k = i + 1;
+        while (k < pieces.size() && pieces[k].b == pieces[i].b && pieces[k].g == pieces[i].g) ++k;
+        if (k - i > 1) {
+            const int32_t first = next_slot;
+            for (size_t x = i; x < k; ++x) {
+                pieces[x].slot = next_slot++;
+                pieces[x].seg_slot0 = first;
+                pieces[x].seg_nslots = static_cast<int32_t>(k - i);
+            }
+        }
+        i = k;
+    }
+    uint32_t max_partial = 0;
+    for (uint32_t w = 0; w < W; ++w) {
+        uint32_t n = 0;
+        for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) n += pieces[pi].slot >= 0 ? 1u : 0u;
+        max_partial = std::max(max_partial, n);
+    }
+    if (max_partial > static_cast<uint32_t>(kMaxPartialPerWg)) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "schedule gives a workgroup %u partial pieces (max %d)", max_partial,
+                    kMaxPartialPerWg);
+    }
+
+    s.off_wg_begin = 0;
+    s.off_pieces = align_ints(W + 1);
+    s.off_counters = s.off_pieces + align_ints(pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)));
+    s.total = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
+
+    if (s.staging_done == nullptr) QVP_HIP(hipEventCreateWithFlags(&s.staging_done, hipEventDisableTiming));
+    if (s.staging_pending) {
+        QVP_HIP(hipEventSynchronize(s.staging_done));
+        s.staging_pending = false;
+    }
+    if (s.staging_cap < s.total) {
+        if (s.staging != nullptr) QVP_HIP(hipHostFree(s.staging));
+        s.staging = nullptr;
+        s.staging_cap = 0;
+        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&s.staging), s.total * sizeof(int32_t), hipHostMallocDefault));
+        s.staging_cap = s.total;
+    }
+    if (s.device_cap < s.total) {
+        if (s.device != nullptr) QVP_HIP(hipFree(s.device));
+        s.device = nullptr;
+        s.device_cap = 0;
+        QVP_HIP(hipMalloc(reinterpret_cast<void**>(&s.device), s.total * sizeof(int32_t)));
+        s.device_cap = s.total;
+    }
+    int32_t* h = s.staging;
+    std::fill(h, h + s.total, 0);  // counters start at zero
+    std::copy(wg_begin.begin(), wg_begin.end(), h + s.off_wg_begin);
+    const int32_t* praw = reinterpret_cast<const int32_t*>(pieces.data());
+    std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
+    QVP_HIP(hipMemcpyAsync(s.device, h, s.total * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+    QVP_HIP(hipEventRecord(s.staging_done, stream));
+    s.staging_pending = true;
+
+    s.pack_generation = batch->generation;
+    s.num_kv_heads = num_kv_heads;
+    s.max_wgs = max_wgs;
+    s.num_wgs = W;
+    s.num_pieces = static_cast<uint32_t>(pieces.size());
+    s.num_slots = static_cast<uint32_t>(next_slot);
+    s.max_partial_pieces_per_wg = max_partial;
+    s.valid = true;
+    return QVP_OK;
+}
+
+uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim) {
+    const uint64_t rows = static_cast<uint64_t>(batch->sched.num_slots) * group;
+    return round_up(rows * 2 * sizeof(float), 256) + round_up(rows * head_dim * sizeof(float), 256);
+}
+
+int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t out_dtype, void* out,
+                       void* workspace, hipEvent_t split_event, hipStream_t stream) {
+    const qvp_schedule& s = batch->sched;
+    MfmaArgs a{};
+    a.wg_begin = s.device + s.off_wg_begin;
+    a.pieces = reinterpret_cast<const qvp_piece*>(s.device + s.off_pieces);
+    a.counters = s.device + s.off_counters;
+    const uint64_t rows = static_cast<uint64_t>(s.num_slots) * g.group;
+    a.ws_ml = static_cast<float*>(workspace);
+    a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + round_up(rows * 2 * sizeof(float), 256));
+    a.out = out;
+    const dim3 grid(s.num_wgs);
+    switch (out_dtype) {
+        case QVP_DTYPE_F32:
+            hipLaunchKernelGGL(decode_mfma_persistent<float>, grid, dim3(kThreads), 0, stream, g, a);
+            break;
+        case QVP_DTYPE_BF16:
+            hipLaunchKernelGGL(decode_mfma_persistent<uint16_t>, grid, dim3(kThreads), 0, stream, g, a);
+            break;
+        default:
+            hipLaunchKernelGGL(decode_mfma_persistent<_Float16>, grid, dim3(kThreads), 0, stream, g, a);
+            break;
+    }
+    QVP_HIP(hipGetLastError());
+    // The merge runs inside the kernel; the event still marks the split/merge
+    // boundary for callers that time the two phases.
+    if (split_event != nullptr) QVP_HIP(hipEventRecord(split_event, stream));
+    return QVP_OK;
+}
+
+}  // namespace qvp

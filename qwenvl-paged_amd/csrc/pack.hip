@@ -10,6 +10,7 @@
 // buffers alternate between two calls so the host can fill one while the DMA
 // engine still reads the other, and the device receives all arrays in a single
 // asynchronous copy.
+#include "batch.h"
 #include "common.h"
 
 #include <algorithm>
@@ -49,18 +50,6 @@ Layout make_layout(uint32_t num_seqs, uint32_t max_nb, uint32_t num_splits) {
 
 }  // namespace
 
-struct qvp_batch {
-    int32_t* staging[2]{nullptr, nullptr};
-    size_t staging_cap[2]{0, 0};  // in int32 elements
-    hipEvent_t staging_done[2]{nullptr, nullptr};
-    bool staging_pending[2]{false, false};
-    int parity{0};
-    int32_t* device{nullptr};
-    size_t device_cap{0};
-    bool valid{false};
-    qvp_packed_view view{};
-};
-
 using qvp::fail;
 
 extern "C" {
@@ -95,6 +84,7 @@ int qvp_batch_destroy(qvp_batch* batch) {
     if (batch->device != nullptr && hipFree(batch->device) != hipSuccess) {
         status = fail(QVP_ERR_DEVICE, "hipFree(batch)");
     }
+    qvp::destroy_schedule(batch->sched);
     delete batch;
     return status;
 }
@@ -253,6 +243,8 @@ int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
     v.num_pool_blocks = num_pool_blocks;
     v.max_seq_len = max_len;
     v.total_tokens = total_tokens;
+    batch->host_seq_lens.assign(seq_lens, seq_lens + num_seqs);
+    batch->generation += 1;
     batch->valid = true;
     return QVP_OK;
 }

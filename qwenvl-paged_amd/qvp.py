@@ -78,6 +78,7 @@ class DecodeArgs(ctypes.Structure):
         ("scale", c_float),
         ("workspace", c_void_p),
         ("workspace_bytes", c_uint64),
+        ("split_event", c_void_p),
     ]
 
 
@@ -457,12 +458,12 @@ def layout_strides(tokens_per_block: int, num_layers: int, num_kv_heads: int, he
 def decode_args(*, query: int, out: int, kv_base: int, block_stride: int, batch: Batch, kv_dtype: int,
                 out_dtype: int, layer: int, num_layers: int, num_query_heads: int, num_kv_heads: int,
                 head_dim: int, tokens_per_block: int, scale: float, strides: dict | None = None,
-                workspace: int = 0, workspace_bytes: int = 0) -> DecodeArgs:
+                workspace: int = 0, workspace_bytes: int = 0, split_event: "Event | None" = None) -> DecodeArgs:
     s = strides or layout_strides(tokens_per_block, num_layers, num_kv_heads, head_dim)
     return DecodeArgs(query, out, kv_base, block_stride, batch.handle, kv_dtype, out_dtype, layer, num_layers,
                       num_query_heads, num_kv_heads, head_dim, tokens_per_block, s["head_stride"],
                       s["token_stride"], s["stream_stride"], s["layer_stride"], scale, workspace or None,
-                      workspace_bytes)
+                      workspace_bytes, split_event.handle if split_event is not None else None)
 
 
 def paged_decode(args: DecodeArgs, stream=None) -> None:

@@ -74,6 +74,36 @@ def to_f32(arr: np.ndarray, dtype: int) -> np.ndarray:
     return arr.view(np.float16).astype(np.float32)
 
 
+def ulp16(x: np.ndarray, dtype: int) -> np.ndarray:
+    """Spacing of the 16-bit format at |x| (bf16: 8 significant bits, fp16: 11)."""
+    mant = 8 if dtype == qvp.DTYPE_BF16 else 11
+    e = np.floor(np.log2(np.maximum(np.abs(x), 1e-30)))
+    return np.exp2(e - (mant - 1))
+
+
+def round16(x: np.ndarray, dtype: int) -> np.ndarray:
+    """Round-to-nearest-even of fp32 values to the 16-bit format, as float32."""
+    if dtype == qvp.DTYPE_BF16:
+        return W.bf16_bits_to_f32(W.f32_to_bf16_bits(x))
+    return np.asarray(x, np.float32).astype(np.float16).astype(np.float32)
+
+
+def assert_close_16bit(got16: np.ndarray, ref32: np.ndarray, dtype: int, what: str = "") -> dict:
+    """A 16-bit output is the rounding of the kernel's fp32 result, so it is
+    compared with the oracle's fp32 result rounded the same way: equal, or one
+    unit in the last place apart where the two fp32 values straddle a rounding
+    boundary, and within the bf16 absolute tolerance otherwise."""
+    got = to_f32(got16, dtype).astype(np.float64)
+    exp = round16(ref32, dtype).astype(np.float64)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    diff = np.abs(got - exp)
+    allowed = np.maximum(BF16_ABS_TOL, ulp16(exp, dtype) * 1.0001)
+    worst = float((diff / allowed).max())
+    stats = {"max_abs": float(diff.max()), "exact_fraction": float((diff == 0).mean()), "worst_over_allowed": worst}
+    assert worst <= 1.0, f"{what}: 16-bit output off by more than max(2e-3, 1 ulp): {stats}"
+    return stats
+
+
 def assert_close_bf16(got: np.ndarray, ref: np.ndarray, what: str = "") -> dict:
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
