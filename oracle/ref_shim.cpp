@@ -17,6 +17,7 @@
 #include "qwenvl_paged/PagedAttention.h"
 #include "qwenvl_paged/Scheduler.h"
 #include "qwenvl_paged/SwapBackend.h"
+#include "trace_driver.h"
 
 #include <chrono>
 #include <cstring>
@@ -176,6 +177,37 @@ std::int64_t ref_element_offset(std::uint32_t tpb, std::uint32_t layers, std::ui
     layout.shape.bytes_per_element = 4;
     const auto off = layout.element_offset(layer, stream == 0 ? KVStream::Key : KVStream::Value, token, head);
     return off.has_value() ? static_cast<std::int64_t>(*off) : -1;
+}
+
+// Runs the continuous-batching trace of trace_driver.h on the reference's own
+// Scheduler / KVCacheManager / MemoryAllocator / HostSwapBackend and copies the
+// event log into `out` (NUL-terminated, truncated to `cap`). Returns the full
+// log length.
+std::uint64_t ref_scheduler_trace(std::uint32_t requests, std::uint64_t seed, std::uint32_t pool_percent,
+                                  std::uint32_t watermark_blocks, char* out, std::uint64_t cap) {
+    trace::Config c;
+    c.requests = requests;
+    c.seed = seed;
+    c.pool_percent = pool_percent;
+    c.watermark_blocks = watermark_blocks;
+    AllocatorConfig config;
+    config.block_shape.tokens_per_block = c.tokens_per_block;
+    config.block_shape.num_layers = 1;
+    config.block_shape.num_kv_heads = 1;
+    config.block_shape.head_dim = 8;
+    config.block_shape.bytes_per_element = 4;
+    config.max_blocks = trace::pool_blocks(c);
+    MemoryAllocator allocator(config);
+    HostSwapBackend swap(1u << 20);
+    allocator.set_swap_backend(&swap);
+    const std::string log =
+        trace::run<MemoryAllocator, KVCacheManager, Scheduler, SchedulerConfig, Request, RequestState>(c, allocator);
+    if (cap > 0) {
+        const std::size_t n = log.size() < cap - 1 ? log.size() : cap - 1;
+        std::memcpy(out, log.data(), n);
+        out[n] = '\0';
+    }
+    return log.size();
 }
 
 }  // extern "C"

@@ -1,0 +1,91 @@
+#pragma once
+// Paged-attention decode on the GPU behind the reference's interface
+// (include/qwenvl_paged/PagedAttention.h:23-127).
+//
+// paged_attention_decode<T> keeps the reference signature and refusal rules:
+// it returns false, leaving `out` untouched, for an invalid view, a null
+// pointer, sizeof(T) != bytes_per_element, context_len == 0, a layer outside
+// the shape, query heads that do not group onto the kv heads, or a needed block
+// that is unmapped or swapped out (PagedAttention.h:50-89). Otherwise the
+// computation runs on the GPU (libqvp: pack, then the split-K decode) and the
+// result is copied back. There is no CPU path: a view over host-placed frames
+// is refused. PagedAttentionBatch decodes many sequences in one launch from
+// device buffers; that is the engine's per-step entry point.
+
+#include "qwenvl_paged/CacheLayout.h"
+#include "qwenvl_paged/KVCacheManager.h"
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+struct qvp_batch;
+
+namespace qwenvl_paged {
+
+struct PagedAttentionParams {
+    std::uint32_t layer{0};
+    std::uint32_t num_query_heads{0};
+    std::uint32_t context_len{0};
+    float scale{1.0F};
+};
+
+// bfloat16 cache element: two bytes, explicit conversions (float -> bf16
+// rounds to nearest, ties to even; NaN stays NaN).
+struct bf16 {
+    std::uint16_t bits{0};
+    bf16() = default;
+    explicit bf16(float f) noexcept;
+    explicit operator float() const noexcept;
+};
+static_assert(sizeof(bf16) == 2, "bf16 must be two bytes");
+
+// Element type codes (values of qvp_dtype).
+enum class ElementType : int { F32 = 0, BF16 = 1, F16 = 2 };
+
+// Decodes one query token (query, out: host arrays of num_query_heads *
+// head_dim elements, head-major). T is float or bf16.
+template <typename T>
+[[nodiscard]] bool paged_attention_decode(const CacheView& view, const T* query, const PagedAttentionParams& params,
+                                          T* out);
+
+// The calling thread's message for the last refusal of paged_attention_decode.
+[[nodiscard]] const std::string& paged_attention_last_error();
+
+class PagedAttentionBatch {
+public:
+    PagedAttentionBatch();
+    ~PagedAttentionBatch();
+    PagedAttentionBatch(const PagedAttentionBatch&) = delete;
+    PagedAttentionBatch& operator=(const PagedAttentionBatch&) = delete;
+
+    // Packs the sequences of `views` (context_lens[b] committed tokens each,
+    // all views over the same device allocator), validates every argument and
+    // block, and enqueues the decode on the allocator's engine stream.
+    // device_query / device_out: [B][num_query_heads][head_dim], the cache
+    // element type for the query; out_type selects the output element type.
+    // Refused calls return false with nothing enqueued.
+    bool decode(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                std::uint32_t layer, std::uint32_t num_query_heads, float scale, const void* device_query,
+                void* device_out, ElementType out_type);
+    // Element type of the cache from its element size (4: F32, 2: BF16 unless
+    // set_cache_element_type(F16) was called).
+    void set_cache_element_type(ElementType type) noexcept;
+    [[nodiscard]] const std::string& last_error() const noexcept;
+    // The packed batch of the last successful decode (device arrays).
+    [[nodiscard]] qvp_batch* packed() const noexcept;
+    // Split-K partition in tokens (0: library default).
+    void set_split_tokens(std::uint32_t tokens) noexcept;
+
+private:
+    bool fail(std::string msg);
+
+    qvp_batch* batch_{nullptr};
+    std::vector<std::uint32_t> ids_;
+    std::vector<std::uint32_t> cu_;
+    std::string last_error_;
+    std::uint32_t split_tokens_{0};
+    int cache_type_override_{-1};
+};
+
+}  // namespace qwenvl_paged

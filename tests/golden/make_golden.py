@@ -1,0 +1,93 @@
+"""Writes the committed fixtures of this directory from the compiled reference
+(oracle/_ref/libqvp_ref.so, built by `make -C oracle` from the QwenVL-Paged
+sources where that tree is present). Run from the repository root:
+
+    python tests/golden/make_golden.py
+
+Fixtures (data only: inputs are regenerated from seeds, outputs stored):
+  decode_goldens.npz       paged_attention_decode<T> of the reference on
+                           config1 (fp32) and two bf16 workloads, with a SHA-256
+                           of each workload's pool image and query so that a
+                           drift of the input generators is caught
+  scheduler_trace_w4.txt   event log of the continuous-batching trace of
+  scheduler_trace_w0.txt   oracle/trace_driver.h on the reference's Scheduler /
+                           KVCacheManager / MemoryAllocator / HostSwapBackend
+                           (preemption watermark 4 and 0 blocks)
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import sys
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parents[2]
+sys.path[:0] = [str(ROOT / "qwenvl-paged_amd"), str(ROOT / "oracle")]
+
+import pyoracle as O  # noqa: E402
+import workloads as W  # noqa: E402
+
+HERE = Path(__file__).resolve().parent
+
+# Trace settings shared with tests/cpp/SchedulerTrace.test.cpp.
+TRACES = {"scheduler_trace_w4.txt": dict(requests=32, seed=5, pool_percent=30, watermark=4),
+          "scheduler_trace_w0.txt": dict(requests=32, seed=11, pool_percent=30, watermark=0)}
+
+
+def golden_workloads() -> dict[str, W.Workload]:
+    return {
+        "config1": W.config1(0),
+        "bf16_gqa7": W.custom([1, 17, 300, 64], 28, 4, 128, W.DTYPE_BF16, seed=21),
+        "bf16_tpb32": W.custom([33, 95, 700], 16, 2, 128, W.DTYPE_BF16, tokens_per_block=32, seed=22,
+                               num_layers=2, layer=1),
+    }
+
+
+def input_digest(w: W.Workload) -> str:
+    h = hashlib.sha256()
+    for a in (w.pool_image(), w.query(), w.ids, w.cu_blocks, w.context_lens):
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def reference_decode(w: W.Workload) -> np.ndarray:
+    dtype = O.ORC_F32 if w.kv_dtype == W.DTYPE_F32 else O.ORC_BF16
+    sess = O.RefSession(w.pool_image(), w.block_stride, w.num_pool_blocks, w.tokens_per_block, w.num_layers,
+                        w.num_kv_heads, w.head_dim, w.elem_bytes)
+    refused, out, _ = sess.decode(w.ids, w.cu_blocks, w.context_lens, dtype, w.query(), w.layer,
+                                  w.num_query_heads, w.head_dim, w.scale)
+    sess.close()
+    assert refused == 0
+    return out
+
+
+def reference_trace(requests: int, seed: int, pool_percent: int, watermark: int) -> str:
+    lib = O.reference()
+    lib.ref_scheduler_trace.restype = ctypes.c_uint64
+    lib.ref_scheduler_trace.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                                        ctypes.c_char_p, ctypes.c_uint64]
+    cap = 1 << 22
+    buf = ctypes.create_string_buffer(cap)
+    n = lib.ref_scheduler_trace(requests, seed, pool_percent, watermark, buf, cap)
+    assert n < cap
+    return buf.value.decode()
+
+
+def main() -> None:
+    if not O.reference_available():
+        raise SystemExit("oracle/_ref/libqvp_ref.so is missing: run `make -C oracle` with the reference tree present")
+    arrays = {}
+    for name, w in golden_workloads().items():
+        arrays[f"{name}_out"] = reference_decode(w)
+        arrays[f"{name}_digest"] = np.frombuffer(bytes.fromhex(input_digest(w)), dtype=np.uint8)
+    np.savez_compressed(HERE / "decode_goldens.npz", **arrays)
+    for fname, t in TRACES.items():
+        (HERE / fname).write_text(reference_trace(t["requests"], t["seed"], t["pool_percent"], t["watermark"]))
+    print("wrote", ", ".join(["decode_goldens.npz", *TRACES]))
+
+
+if __name__ == "__main__":
+    main()
