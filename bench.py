@@ -200,19 +200,17 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
 
-    # Timed region 2: the same steps with HIP events around each kernel.
+    # Timed region 2: the same steps with HIP events on the launch stream
+    # around each decode (one kernel: the split merge is fused into it).
     starts = [qvp.Event() for _ in range(args.steps)]
-    mids = [qvp.Event() for _ in range(args.steps)]
     ends = [qvp.Event() for _ in range(args.steps)]
-    timed = [make_args(pools[i % len(pools)], mids[i]) for i in range(args.steps)]
     qvp.synchronize()
     for i in range(args.steps):
         starts[i].record(stream)
-        qvp.paged_decode(timed[i], stream)
+        qvp.paged_decode(plain[i % len(pools)], stream)
         ends[i].record(stream)
     stream.synchronize()
-    split_ms = [starts[i].elapsed_ms(mids[i]) for i in range(args.steps)]
-    merge_ms = [mids[i].elapsed_ms(ends[i]) for i in range(args.steps)]
+    kernel_ms = [starts[i].elapsed_ms(ends[i]) for i in range(args.steps)]
 
     # Pack-inclusive step (host pack + pinned H2D of the tables + decode).
     qvp.synchronize()
@@ -231,9 +229,9 @@ def main() -> int:
     algo = w.algorithmic_bytes()
     kernel_bytes = w.kv_bytes() + w.num_seqs * w.num_query_heads * w.head_dim * 2 + \
         int(((w.context_lens.astype(np.int64) + 15) // 16).sum()) * 4 + w.num_seqs * 4
-    split_avg = statistics.mean(split_ms)
+    kernel_avg = statistics.mean(kernel_ms)
     gbps = algo / (ms_per_step * 1e-3) / 1e9
-    achieved = kernel_bytes / (split_avg * 1e-3) / 1e9
+    achieved = kernel_bytes / (kernel_avg * 1e-3) / 1e9
     traffic = load_traffic()
 
     line = {
@@ -264,7 +262,6 @@ def main() -> int:
         "algorithmic_bytes_per_step": algo,
         "step_with_pack_ms": round(pack_ms, 5),
         "step_with_pack_tokens_per_s": round(w.num_seqs / (pack_ms * 1e-3), 1),
-        "merge_kernel_avg_ms": round(statistics.mean(merge_ms), 5),
         "roofline": {
             "kernel": "decode_mfma_bf16_d128",
             "bound": "hbm",
@@ -273,7 +270,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic.get("bytes_per_launch") if traffic else None,
-            "kernel_avg_ms": round(split_avg, 5),
+            "kernel_avg_ms": round(kernel_avg, 5),
             "kernel_bytes_per_launch": kernel_bytes,
         },
         "setup_s": round(setup_s, 2),

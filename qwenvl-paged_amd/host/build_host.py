@@ -29,7 +29,6 @@ ROCM_LIB = "/opt/rocm/lib"
 CXXFLAGS = [
     "-std=c++17",
     "-O2",
-    "-g",
     "-fPIC",
     "-Wall",
     "-Wextra",
