@@ -12,13 +12,16 @@
 // workgroup take tiles round-robin, keep an online-softmax state (running max
 // m, running sum l, unnormalised accumulator O) and merge it through LDS when
 // the piece ends. A piece that is a whole segment writes the final output; the
-// other pieces write (m, l, O) to a workspace slot. When a workgroup has run
-// through its range it publishes its slots (one agent-scope release fence, then
-// one atomic increment of each segment's counter); the workgroup that completes
-// a segment's count merges its slots in place, out = sum_s O_s 2^(m_s - M) /
-// sum_s l_s 2^(m_s - M) with M = max_s m_s, and resets the counter for the next
-// launch. Publishing once at the end keeps the fence (which waits for every
-// outstanding memory operation of the wave) off the prefetch pipeline.
+// other pieces write (m, l, O) to a workspace slot with agent-scope stores,
+// which reach the point of coherence shared by all XCDs. When a workgroup has
+// run through its range, a workgroup barrier (which waits for every
+// outstanding memory operation) orders those stores before one agent-scope
+// atomic increment of each partial segment's counter; the workgroup that
+// completes a segment's count reads its slots with agent-scope loads, merges
+// them in one pass, out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) with
+// M = max_s m_s, and resets the counter for the next launch. Publishing once at
+// the end keeps that wait off the prefetch pipeline, and no cache write-back or
+// invalidate is needed.
 // Each wave prefetches its next tile (possibly in the next piece) before it
 // computes the current one, so loads stay in flight across piece boundaries.
 //
