@@ -38,6 +38,10 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # Keep single-lane atomics as written: the optimizer's wave-aggregated
+    # form reads the result back at once, which waits for every older load.
+    "-mllvm",
+    "-amdgpu-atomic-optimizer-strategy=None",
     f"-I{ROOT / 'include'}",
     f"-I{PKG / 'csrc'}",
 ]

@@ -62,8 +62,10 @@ constexpr int kWgsPerCu = 2;
 // A workgroup's range is contiguous, so only its first and last pieces can be
 // partial segments.
 constexpr int kMaxPartialPerWg = 2;
-// Slots combined per round of loads in the end-of-range merge.
+// Slots combined per round of loads in the end-of-range merge, and elements
+// per thread per round.
 constexpr int kMergeChunk = 8;
+constexpr int kMergeBatch = 4;
 
 struct MfmaArgs {
     const qvp_piece* pieces;
@@ -81,6 +83,28 @@ struct KvTile {
 
 __device__ inline u32x4 load16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+// The schedule and the block tables do not change while the kernel runs;
+// reading them through the constant address space lets the compiler use
+// scalar loads (which do not wait behind the wave's outstanding K/V loads)
+// although the kernel also performs atomics.
+template <typename T>
+__device__ inline const __attribute__((address_space(4))) T* as_const(const T* ptr) {
+    return (const __attribute__((address_space(4))) T*)(ptr);
+}
+__device__ inline qvp_piece piece_at(const qvp_piece* pieces, int i) {
+    const auto* q = as_const(pieces) + i;
+    qvp_piece d;
+    d.b = q->b;
+    d.g = q->g;
+    d.t0 = q->t0;
+    d.t1 = q->t1;
+    d.ctx = q->ctx;
+    d.slot = q->slot;
+    d.seg_slot0 = q->seg_slot0;
+    d.seg_nslots = q->seg_nslots;
+    return d;
+}
+
 // A tile of one wave's sequence with its block ids already fetched, so its
 // loads can be issued without waiting on the block table.
 struct TileRef {
@@ -93,14 +117,14 @@ struct TileRef {
 // Starts from piece pi when t < 0. Returns false when the range is exhausted.
 __device__ inline bool next_tile(const MfmaArgs& a, int pe, int wave, int& pi, int& t) {
     if (t >= 0) {
-        if (t + kWaves < a.pieces[pi].t1) {
+        if (t + kWaves < piece_at(a.pieces, pi).t1) {
             t += kWaves;
             return true;
         }
         ++pi;
     }
     for (; pi < pe; ++pi) {
-        const qvp_piece d = a.pieces[pi];
+        const qvp_piece d = piece_at(a.pieces, pi);
         if (d.t0 + wave < d.t1) {
             t = d.t0 + wave;
             return true;
@@ -114,13 +138,13 @@ __device__ inline bool next_tile(const MfmaArgs& a, int pe, int wave, int& pi, i
 // a block (tpb is a power of two >= 16); tokens past the context fall back to
 // the last valid block.
 __device__ inline TileRef resolve_tile(const DecodeGeometry& p, const MfmaArgs& a, int pi, int t) {
-    const qvp_piece d = a.pieces[pi];
+    const qvp_piece d = piece_at(a.pieces, pi);
     TileRef r;
     r.b = d.b;
     r.g = d.g;
     r.t = t;
     r.ctx = d.ctx;
-    const int32_t* row = p.tables + static_cast<uint64_t>(d.b) * p.max_nb;
+    const auto* row = as_const(p.tables) + static_cast<uint64_t>(d.b) * p.max_nb;
     const int tok0 = t * kTileTokens;
     r.blk0 = row[min(tok0, r.ctx - 1) >> p.tpb_shift];
     r.blk1 = row[min(tok0 + 16, r.ctx - 1) >> p.tpb_shift];
@@ -269,8 +293,8 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     const int j = lane >> 4;
     const int G = static_cast<int>(p.group);
 
-    const int pb = a.wg_begin[blockIdx.x];
-    const int pe = a.wg_begin[blockIdx.x + 1];
+    const int pb = as_const(a.wg_begin)[blockIdx.x];
+    const int pe = as_const(a.wg_begin)[blockIdx.x + 1];
 
     // Software pipeline per wave: while the current tile is computed, the next
     // tile's loads are in flight (nxt) and the block ids of the tile after that
@@ -287,20 +311,20 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     if (has2) r2 = resolve_tile(p, a, pi2, t2);
 
     for (int pi = pb; pi < pe; ++pi) {
-        const qvp_piece d = a.pieces[pi];
+        const qvp_piece d = piece_at(a.pieces, pi);
         const int ctx = d.ctx;
 
-        // Query B operand: lane (c, j), MFMA i -> Q[head g*G + c][dims 32i + 8j .. +8].
+        // Query B operand: lane (c, j), MFMA i -> Q[head g*G + c][dims 32i + 8j
+        // .. +8]. Columns past the group repeat the group's last head: their
+        // scores, weights and outputs stay in their own columns and are never
+        // written, and not masking leaves the loads' results unused until the
+        // first tile is computed (a select on them would wait at once).
         u32x4 qop[4];
         {
-            const bool live = c < G;
             const uint16_t* q = static_cast<const uint16_t*>(p.query) +
-                                (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + (live ? c : 0)) * kD;
+                                (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + min(c, G - 1)) * kD;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const u32x4 v = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
-                qop[i] = live ? v : u32x4{0u, 0u, 0u, 0u};
-            }
+            for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
         }
 
         floatx4 o[8];
@@ -376,7 +400,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         int found = -1;
         int k = 0;
         for (int pi = pb; pi < pe; ++pi) {
-            if (a.pieces[pi].slot < 0) continue;
+            if (piece_at(a.pieces, pi).slot < 0) continue;
             if (k++ == static_cast<int>(threadIdx.x)) {
                 found = pi;
                 break;
@@ -384,7 +408,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         }
         int mine = -1;
         if (found >= 0) {
-            const qvp_piece d = a.pieces[found];
+            const qvp_piece d = piece_at(a.pieces, found);
             const int done = __hip_atomic_fetch_add(&a.counters[d.seg_slot0], 1, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
             if (done == d.seg_nslots - 1) mine = found;
@@ -392,55 +416,95 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         sm_merge[threadIdx.x] = mine;
     }
     __syncthreads();
-    OutT* out = static_cast<OutT*>(a.out);
+    // Merge the segments this workgroup completed. All their elements are
+    // spread over the workgroup's threads, kMergeBatch per thread per round,
+    // and each round issues every slot load of its elements before combining
+    // (agent-scope loads read the slots of other workgroups, on other XCDs,
+    // from the point of coherence): the merge costs about one round trip.
+    int nm = 0;
+    int merge_piece[kMaxPartialPerWg] = {};
+    int max_ns = 0;
+#pragma unroll
     for (int k = 0; k < kMaxPartialPerWg; ++k) {
-        const int pm = sm_merge[k];
-        if (pm < 0) continue;
-        const qvp_piece d = a.pieces[pm];
-        const int s0 = d.seg_slot0;
-        const int ns = d.seg_nslots;
-        for (int e = threadIdx.x; e < G * kD; e += kThreads) {
-            const int hc = e >> 7;
-            const int dd = e & (kD - 1);
-            // All slot values are loaded in one round (agent-scope loads read
-            // the slots of other workgroups, on other XCDs, from the point of
-            // coherence), then combined.
-            float mmax = -INFINITY;
-            float acc = 0.f;
-            float lsum = 0.f;
-            for (int c0 = 0; c0 < ns; c0 += kMergeChunk) {
-                float m[kMergeChunk], l[kMergeChunk], o[kMergeChunk];
+        const int pm = __builtin_amdgcn_readfirstlane(sm_merge[k]);
+        if (pm >= 0) {
+            merge_piece[nm++] = pm;
+            max_ns = max(max_ns, static_cast<int>(piece_at(a.pieces, pm).seg_nslots));
+        }
+    }
+    if (nm == 0) return;
+    OutT* out = static_cast<OutT*>(a.out);
+    const int per_seg = G * kD;
+    const int total = nm * per_seg;
+    for (int f0 = threadIdx.x; f0 < total; f0 += kThreads * kMergeBatch) {
+        int hc[kMergeBatch], dd[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch], pb_of[kMergeBatch];
+        float mmax[kMergeBatch], acc[kMergeBatch], lsum[kMergeBatch];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const int f = f0 + i * kThreads;
+            const int seg = f < total ? f / per_seg : 0;
+            const int e = f < total ? f - seg * per_seg : 0;
+            const int pm = seg == 0 ? merge_piece[0] : merge_piece[kMaxPartialPerWg - 1];
+            const qvp_piece d = piece_at(a.pieces, pm);
+            hc[i] = e >> 7;
+            dd[i] = e & (kD - 1);
+            s0[i] = d.seg_slot0;
+            ns[i] = f < total ? d.seg_nslots : 0;
+            pb_of[i] = pm;
+            mmax[i] = -INFINITY;
+            acc[i] = 0.f;
+            lsum[i] = 0.f;
+        }
+        for (int c0 = 0; c0 < max_ns; c0 += kMergeChunk) {
+            float m[kMergeBatch][kMergeChunk], l[kMergeBatch][kMergeChunk], o[kMergeBatch][kMergeChunk];
+#pragma unroll
+            for (int i = 0; i < kMergeBatch; ++i) {
 #pragma unroll
                 for (int x = 0; x < kMergeChunk; ++x) {
-                    m[x] = -INFINITY;
-                    l[x] = 0.f;
-                    o[x] = 0.f;
-                    if (c0 + x < ns) {
-                        const uint64_t row = static_cast<uint64_t>(s0 + c0 + x) * G + hc;
-                        m[x] = __hip_atomic_load(&a.ws_ml[row * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        l[x] = __hip_atomic_load(&a.ws_ml[row * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        o[x] = __hip_atomic_load(&a.ws_acc[row * kD + dd], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    m[i][x] = -INFINITY;
+                    l[i][x] = 0.f;
+                    o[i][x] = 0.f;
+                    if (c0 + x < ns[i]) {
+                        const uint64_t row = static_cast<uint64_t>(s0[i] + c0 + x) * G + hc[i];
+                        m[i][x] = __hip_atomic_load(&a.ws_ml[row * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        l[i][x] =
+                            __hip_atomic_load(&a.ws_ml[row * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        o[i][x] = __hip_atomic_load(&a.ws_acc[row * kD + dd[i]], __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
-                float cm = mmax;
+            }
 #pragma unroll
-                for (int x = 0; x < kMergeChunk; ++x) cm = fmaxf(cm, m[x]);
-                const float rescale = fast_exp2(mmax - cm);
-                acc *= rescale;
-                lsum *= rescale;
+            for (int i = 0; i < kMergeBatch; ++i) {
+                float cm = mmax[i];
+#pragma unroll
+                for (int x = 0; x < kMergeChunk; ++x) cm = fmaxf(cm, m[i][x]);
+                // Elements past the end have no slot: keep them finite.
+                const float rescale = cm == -INFINITY ? 0.f : fast_exp2(mmax[i] - cm);
+                acc[i] *= rescale;
+                lsum[i] *= rescale;
 #pragma unroll
                 for (int x = 0; x < kMergeChunk; ++x) {
-                    const float f = fast_exp2(m[x] - cm);
-                    acc += o[x] * f;
-                    lsum += l[x] * f;
+                    const float f = c0 + x < ns[i] ? fast_exp2(m[i][x] - cm) : 0.f;
+                    acc[i] += o[i][x] * f;
+                    lsum[i] += l[i][x] * f;
                 }
-                mmax = cm;
+                mmax[i] = cm;
             }
-            out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + hc) * kD + dd] = from_float<OutT>(acc / lsum);
         }
-        if (threadIdx.x == 0) {
-            __hip_atomic_store(&a.counters[s0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            if (f0 + i * kThreads < total) {
+                const qvp_piece d = piece_at(a.pieces, pb_of[i]);
+                out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + hc[i]) * kD + dd[i]] =
+                    from_float<OutT>(acc[i] / lsum[i]);
+            }
         }
+    }
+    if (threadIdx.x < static_cast<unsigned>(nm)) {
+        const int s0 =
+            piece_at(a.pieces, threadIdx.x == 0 ? merge_piece[0] : merge_piece[kMaxPartialPerWg - 1]).seg_slot0;
+        __hip_atomic_store(&a.counters[s0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
