@@ -6,17 +6,21 @@ context lengths uniform on [512, 4096], block tables scattered over a shuffled
 pool holding 10% spare frames. Synthetic data (seeded N(0,1) queries, N(0,0.5)
 K/V, rounded to bf16).
 
-A step is one decode of the whole batch (the split-K kernel plus the split
-merge) with the packed batch and the cache already in HBM. Three independent
-copies of the pool rotate between steps so the 256 MB Infinity Cache cannot
-serve a step from the previous step's reads. `value` is algorithmic HBM bytes
-per step / step time. The pack-inclusive rate (host pack + pinned H2D + decode)
-is reported beside it as `step_with_pack_*`.
+A step is one decode of the whole batch (one persistent kernel; the merge of
+split segments is fused into it) with the packed batch and the cache already
+in HBM. Three independent copies of the pool rotate between steps so the 256 MB
+Infinity Cache cannot serve a step from the previous step's reads. `value` is
+algorithmic HBM bytes per step / step time. The pack-inclusive rate (host pack
++ pinned H2D + decode) is reported beside it as `step_with_pack_*`.
 
-`roofline` uses the split-K kernel's own average duration, measured with HIP
+`roofline` uses the decode kernel's own average duration, measured with HIP
 events recorded on the decode stream around it. `cpu_baseline` times the
 compiled reference paged_attention_decode<T> (oracle/_ref) on this host over
 the same batch, single-threaded like the reference engine loop.
+
+Other lines (not the headline): --workload config3 (Qwen2-VL-72B layer, B=32,
+ctx U[8192, 32768]), --cow (copy-on-write configuration, C++ driver) and
+--trace (continuous-batching trace, C++ driver) each print their own JSON line.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -109,6 +113,28 @@ def load_traffic() -> dict | None:
     return None
 
 
+def repeated_pool_image(w: W.Workload, chunk_bytes: int = 64 << 20) -> np.ndarray:
+    total = w.num_pool_blocks * w.block_stride
+    n = min(total, chunk_bytes) // 2
+    chunk = W.f32_to_bf16_bits(W.normal(w.seed ^ 0xCAC4E, n, w.kv_sigma)).view(np.uint8)
+    return np.resize(chunk, total)
+
+
+def run_driver(name: str) -> int:
+    """Runs a C++ configuration driver (build/bench/<name>) and relays its line."""
+    import subprocess
+
+    exe = ROOT / "build" / "bench" / name
+    if not exe.exists():
+        print(json.dumps({"error": f"{exe} is missing: run __graft_entry__.build() first"}))
+        return 2
+    proc = subprocess.run([str(exe)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=600)
+    sys.stderr.write(proc.stderr)
+    line = proc.stdout.strip().splitlines()[-1] if proc.stdout.strip() else "{}"
+    print(line)
+    return proc.returncode
+
+
 def copy_calibration(steps: int) -> int:
     """copy_blocks of 128 x 1 MiB frames onto 128 others in one launch:
     128 MiB read and 128 MiB written per launch, nothing else."""
@@ -145,12 +171,17 @@ def main() -> int:
     ap.add_argument("--pools", type=int, default=3, help="independent pool copies rotated between steps")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--workload", choices=["config2", "config3"], default="config2")
+    ap.add_argument("--cow", action="store_true", help="run the copy-on-write configuration driver")
+    ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
                          "used to scale rocprof FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.steps)
+    if args.cow or args.trace:
+        return run_driver("cow_bench" if args.cow else "trace_bench")
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -159,9 +190,11 @@ def main() -> int:
                           "n_gpus": args.gpus}))
         return 2
 
-    w = W.config2()
+    w = W.config2() if args.workload == "config2" else W.config3()
     t_setup = time.perf_counter()
-    image = w.pool_image()
+    # config3's pool (~3 GB) takes a repeated 64 MiB random chunk: contents do
+    # not change the traffic, and the parity tests cover the values.
+    image = w.pool_image() if args.workload == "config2" else repeated_pool_image(w)
     query = w.query()
     stream = qvp.Stream()
     pools = []
@@ -248,8 +281,12 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q, N(0,0.5) K/V rounded to bf16; shuffled pool)",
         "config": {
-            "workload": "config2: Qwen2-VL-7B single-layer paged decode, B=64, ctx U[512,4096], "
-                        "Hq28/Hkv4/D128, block 16, bf16 KV, pool +10% spare, 3 rotating pool copies",
+            "workload": (
+                f"config2: Qwen2-VL-7B single-layer paged decode, B=64, ctx U[512,4096], "
+                f"Hq28/Hkv4/D128, block 16, bf16 KV, pool +10% spare, {len(pools)} rotating pool copies"
+                if args.workload == "config2" else
+                f"config3: Qwen2-VL-72B single-layer paged decode, B=32, ctx U[8192,32768], "
+                f"Hq64/Hkv8/D128, block 16, bf16 KV, pool +10% spare, {len(pools)} pool copies"),
             "batch": w.num_seqs,
             "cached_tokens": int(w.context_lens.sum()),
             "split_tokens": view.split_tokens,
@@ -258,7 +295,8 @@ def main() -> int:
         },
         "pct_of_peak_hbm": round(100.0 * gbps / PEAK_HBM_GBPS, 2),
         "decode_tokens_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
-        "decode_tokens_per_s_28_layers_attention_only": round(w.num_seqs / (28 * ms_per_step * 1e-3), 1),
+        "decode_tokens_per_s_all_layers_attention_only": round(
+            w.num_seqs / ((28 if args.workload == "config2" else 80) * ms_per_step * 1e-3), 1),
         "algorithmic_bytes_per_step": algo,
         "step_with_pack_ms": round(pack_ms, 5),
         "step_with_pack_tokens_per_s": round(w.num_seqs / (pack_ms * 1e-3), 1),
@@ -269,13 +307,13 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": traffic.get("bytes_per_launch") if traffic else None,
+            "traffic": traffic.get("bytes_per_launch") if traffic and args.workload == "config2" else None,
             "kernel_avg_ms": round(kernel_avg, 5),
             "kernel_bytes_per_launch": kernel_bytes,
         },
         "setup_s": round(setup_s, 2),
     }
-    if not args.no_cpu:
+    if not args.no_cpu and args.workload == "config2":
         line["cpu_baseline"] = cpu_baseline(w, image, query, args.cpu_reps)
     print(json.dumps(line))
     return 0

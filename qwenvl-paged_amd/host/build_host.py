@@ -7,6 +7,8 @@ Outputs (git-ignored, shipped with the tree):
                                     Scheduler, PagedAttention (links libqvp.so)
   build/tests/host_tests            suites that run on host-placed frames (no GPU)
   build/tests/device_tests          suites that run on device-placed frames (GPU)
+  build/bench/cow_bench             copy-on-write configuration driver (GPU)
+  build/bench/trace_bench           continuous-batching trace driver (GPU)
 
 libqvp.so must be built first (qwenvl-paged_amd/build.py does both).
 """
@@ -57,6 +59,10 @@ TEST_BINARIES = {
 }
 
 
+# Benchmark drivers of the copy-on-write and continuous-batching configurations.
+BENCH_BINARIES = {"cow_bench": "cow_bench.cpp", "trace_bench": "trace_bench.cpp"}
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if proc.returncode != 0:
@@ -91,6 +97,12 @@ def build() -> None:
     _run([CXX, "-shared", "-o", str(tmp), *[str(obj_dir / (s.stem + ".o")) for s in SOURCES],
           f"-L{PKG}", "-lqvp", *rpath])
     os.replace(tmp, host_lib)
+
+    bench_rpath = [f"-Wl,-rpath,$ORIGIN/../../{PKG.name}", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,{ROCM_LIB}"]
+    (BUILD / "bench").mkdir(parents=True, exist_ok=True)
+    for binary, src in BENCH_BINARIES.items():
+        _run([CXX, *CXXFLAGS, "-o", str(BUILD / "bench" / binary), str(HOST / "bench" / src), f"-L{PKG}",
+              "-lqvp_host", "-lqvp", *bench_rpath])
 
     # Test binaries find both libraries through the package directory, given
     # both as an absolute path (this tree) and relative to the binary (a copy
