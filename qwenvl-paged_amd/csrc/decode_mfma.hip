@@ -13,15 +13,17 @@
 // m, running sum l, unnormalised accumulator O) and merge it through LDS when
 // the piece ends. A piece that is a whole segment writes the final output; the
 // other pieces write (m, l, O) to a workspace slot with agent-scope stores,
-// which reach the point of coherence shared by all XCDs. When a workgroup has
-// run through its range, a workgroup barrier (which waits for every
-// outstanding memory operation) orders those stores before one agent-scope
-// atomic increment of each partial segment's counter; the workgroup that
-// completes a segment's count reads its slots with agent-scope loads, merges
-// them in one pass, out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) with
-// M = max_s m_s, and resets the counter for the next launch. Publishing once at
-// the end keeps that wait off the prefetch pipeline, and no cache write-back or
-// invalidate is needed.
+// which are written through to the point of coherence shared by all XCDs.
+// When a workgroup has run through its range, each wave waits until its
+// stores have completed there (vmcnt(0)) and, after a workgroup barrier, one
+// thread per partial piece increments that segment's counter with an
+// agent-scope atomic; the workgroup that completes a segment's count reads the
+// slots with agent-scope loads (which read at that point of coherence),
+// merges them in one pass, out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M)
+// with M = max_s m_s, and resets the counter for the next launch. Publishing
+// once at the end keeps the store wait off the prefetch pipeline. (An
+// agent-scope release/acquire fence pair would also write back and invalidate
+// the XCD's L2; measured, that doubles the kernel's time.)
 // Each wave prefetches its next tile (possibly in the next piece) before it
 // computes the current one, so loads stay in flight across piece boundaries.
 //
@@ -376,8 +378,9 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
                 out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + hc) * kD + dd] =
                     from_float<OutT>(acc / lsum);
             } else {
-                // Agent-scope stores reach the point of coherence shared by
-                // all XCDs; no cache maintenance is needed to publish them.
+                // Agent-scope stores are written through to the point of
+                // coherence shared by all XCDs; the wait before the count-in
+                // makes sure they have arrived.
                 const uint64_t row = static_cast<uint64_t>(slot) * G + hc;
                 __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (dd == 0) {
@@ -392,28 +395,32 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     if (!have_partial) return;
 
     // Count this workgroup's partial slots in; the workgroup whose increment
-    // completes a segment merges it. The barrier waits for every outstanding
-    // memory operation of the workgroup, so the slot stores above have
-    // completed at the point of coherence before any counter moves.
+    // completes a segment merges it. A workgroup barrier alone does not wait
+    // for outstanding stores, so each wave first waits for all of its memory
+    // operations (the slot stores are agent-scope stores: they are complete
+    // once written through to the point of coherence), and the barrier then
+    // orders all four waves' stores before any counter moves. The asm's
+    // memory clobber keeps the compiler from moving memory accesses across
+    // the wait.
+    // Only the first and the last piece of a contiguous range can be partial
+    // segments; their descriptors are uniform (scalar loads).
+    const qvp_piece first_piece = piece_at(a.pieces, pb);
+    const qvp_piece last_piece = piece_at(a.pieces, pe - 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    // One thread per partial piece (at most kMaxPartialPerWg of them) bumps
-    // that segment's counter; the increments run in parallel.
+    // Thread 0 counts the first piece in, thread 1 the last one (when it is
+    // another piece); the two increments run in parallel.
     if (threadIdx.x < kMaxPartialPerWg) {
-        int found = -1;
-        int k = 0;
-        for (int pi = pb; pi < pe; ++pi) {
-            if (piece_at(a.pieces, pi).slot < 0) continue;
-            if (k++ == static_cast<int>(threadIdx.x)) {
-                found = pi;
-                break;
-            }
-        }
+        const bool is_first = threadIdx.x == 0;
+        const bool exists = is_first || pe - 1 > pb;
+        const int slot = is_first ? first_piece.slot : last_piece.slot;
+        const int seg_slot0 = is_first ? first_piece.seg_slot0 : last_piece.seg_slot0;
+        const int seg_nslots = is_first ? first_piece.seg_nslots : last_piece.seg_nslots;
         int mine = -1;
-        if (found >= 0) {
-            const qvp_piece d = piece_at(a.pieces, found);
-            const int done = __hip_atomic_fetch_add(&a.counters[d.seg_slot0], 1, __ATOMIC_RELAXED,
+        if (exists && slot >= 0) {
+            const int done = __hip_atomic_fetch_add(&a.counters[seg_slot0], 1, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
-            if (done == d.seg_nslots - 1) mine = found;
+            if (done == seg_nslots - 1) mine = is_first ? pb : pe - 1;
         }
         sm_merge[threadIdx.x] = mine;
     }
@@ -423,36 +430,35 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     // and each round issues every slot load of its elements before combining
     // (agent-scope loads read the slots of other workgroups, on other XCDs,
     // from the point of coherence): the merge costs about one round trip.
-    int nm = 0;
-    int merge_piece[kMaxPartialPerWg] = {};
-    int max_ns = 0;
-#pragma unroll
-    for (int k = 0; k < kMaxPartialPerWg; ++k) {
-        const int pm = __builtin_amdgcn_readfirstlane(sm_merge[k]);
-        if (pm >= 0) {
-            merge_piece[nm++] = pm;
-            max_ns = max(max_ns, static_cast<int>(piece_at(a.pieces, pm).seg_nslots));
-        }
-    }
-    if (nm == 0) return;
+    // The segments to merge (at most two) are uniform across the workgroup:
+    // their slot ranges and output rows are fetched once, with scalar loads,
+    // so the loops below issue no loads but the slot reads.
+    const int pm0 = __builtin_amdgcn_readfirstlane(sm_merge[0]);
+    const int pm1 = __builtin_amdgcn_readfirstlane(sm_merge[kMaxPartialPerWg - 1]);
+    if (pm0 < 0 && pm1 < 0) return;
+    const int nm = (pm0 >= 0) + (pm1 >= 0);
+    const qvp_piece m0 = piece_at(a.pieces, pm0 >= 0 ? pm0 : pm1);
+    const qvp_piece m1 = piece_at(a.pieces, pm1 >= 0 ? pm1 : pm0);
+    const int max_ns = max(m0.seg_nslots, m1.seg_nslots);
+    const uint64_t orow0 = (static_cast<uint64_t>(m0.b) * p.num_q_heads + m0.g * G) * kD;
+    const uint64_t orow1 = (static_cast<uint64_t>(m1.b) * p.num_q_heads + m1.g * G) * kD;
     OutT* out = static_cast<OutT*>(a.out);
     const int per_seg = G * kD;
     const int total = nm * per_seg;
     for (int f0 = threadIdx.x; f0 < total; f0 += kThreads * kMergeBatch) {
-        int hc[kMergeBatch], dd[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch], pb_of[kMergeBatch];
+        int hc[kMergeBatch], dd[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch];
+        uint64_t orow[kMergeBatch];
         float mmax[kMergeBatch], acc[kMergeBatch], lsum[kMergeBatch];
 #pragma unroll
         for (int i = 0; i < kMergeBatch; ++i) {
             const int f = f0 + i * kThreads;
-            const int seg = f < total ? f / per_seg : 0;
-            const int e = f < total ? f - seg * per_seg : 0;
-            const int pm = seg == 0 ? merge_piece[0] : merge_piece[kMaxPartialPerWg - 1];
-            const qvp_piece d = piece_at(a.pieces, pm);
+            const bool second = f >= per_seg;
+            const int e = f < total ? f - (second ? per_seg : 0) : 0;
             hc[i] = e >> 7;
             dd[i] = e & (kD - 1);
-            s0[i] = d.seg_slot0;
-            ns[i] = f < total ? d.seg_nslots : 0;
-            pb_of[i] = pm;
+            s0[i] = second ? m1.seg_slot0 : m0.seg_slot0;
+            ns[i] = f < total ? (second ? m1.seg_nslots : m0.seg_nslots) : 0;
+            orow[i] = second ? orow1 : orow0;
             mmax[i] = -INFINITY;
             acc[i] = 0.f;
             lsum[i] = 0.f;
@@ -496,16 +502,11 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         }
 #pragma unroll
         for (int i = 0; i < kMergeBatch; ++i) {
-            if (f0 + i * kThreads < total) {
-                const qvp_piece d = piece_at(a.pieces, pb_of[i]);
-                out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + hc[i]) * kD + dd[i]] =
-                    from_float<OutT>(acc[i] / lsum[i]);
-            }
+            if (f0 + i * kThreads < total) out[orow[i] + hc[i] * kD + dd[i]] = from_float<OutT>(acc[i] / lsum[i]);
         }
     }
     if (threadIdx.x < static_cast<unsigned>(nm)) {
-        const int s0 =
-            piece_at(a.pieces, threadIdx.x == 0 ? merge_piece[0] : merge_piece[kMaxPartialPerWg - 1]).seg_slot0;
+        const int s0 = threadIdx.x == 0 ? m0.seg_slot0 : m1.seg_slot0;
         __hip_atomic_store(&a.counters[s0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -633,15 +634,18 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
         }
         i = k;
     }
+    // The kernel counts in only the first and the last piece of a range.
     uint32_t max_partial = 0;
     for (uint32_t w = 0; w < W; ++w) {
         uint32_t n = 0;
-        for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) n += pieces[pi].slot >= 0 ? 1u : 0u;
+        for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
+            if (pieces[pi].slot < 0) continue;
+            ++n;
+            if (pi != wg_begin[w] && pi != wg_begin[w + 1] - 1) {
+                return fail(QVP_ERR_INVALID_ARGUMENT, "schedule puts a partial segment inside workgroup %u's range", w);
+            }
+        }
         max_partial = std::max(max_partial, n);
-    }
-    if (max_partial > static_cast<uint32_t>(kMaxPartialPerWg)) {
-        return fail(QVP_ERR_INVALID_ARGUMENT, "schedule gives a workgroup %u partial pieces (max %d)", max_partial,
-                    kMaxPartialPerWg);
     }
 
     s.off_wg_begin = 0;
