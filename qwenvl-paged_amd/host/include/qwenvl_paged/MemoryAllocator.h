@@ -21,6 +21,7 @@
 #include "qwenvl_paged/Block.h"
 #include "qwenvl_paged/SwapBackend.h"
 
+#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <functional>
@@ -137,11 +138,14 @@ private:
 
     bool fail(const std::string& what);
     bool run_batch(OpKind kind, const std::vector<DeviceOp>& ops);
+    void set_state(PhysicalBlockInfo& info, BlockState state) noexcept;
 
     AllocatorConfig config_{};
     std::vector<std::unique_ptr<PhysicalBlock>> blocks_;
     std::vector<PhysicalBlockInfo> infos_;
     std::vector<PhysicalBlockId> free_list_;
+    std::array<std::uint32_t, 4> state_counts_{};  // blocks per BlockState
+    std::size_t bytes_reserved_{0};
     SwapBackend* swap_backend_{nullptr};
     EvictionCandidateSelector eviction_selector_{};
 

@@ -54,6 +54,8 @@ MemoryAllocator::MemoryAllocator(AllocatorConfig config) : config_(config) {
         }
         PhysicalBlockInfo info;
         info.id = i;
+        ++state_counts_[static_cast<std::size_t>(info.state)];
+        bytes_reserved_ += blocks_.back()->size_bytes();
         infos_.push_back(info);
         // Free list 0..N-1, so allocate() pops N-1 first.
         free_list_.push_back(i);
@@ -73,6 +75,12 @@ MemoryAllocator::~MemoryAllocator() {
     (void)qvp_pool_destroy(pool_);
 }
 
+void MemoryAllocator::set_state(PhysicalBlockInfo& info, BlockState state) noexcept {
+    --state_counts_[static_cast<std::size_t>(info.state)];
+    ++state_counts_[static_cast<std::size_t>(state)];
+    info.state = state;
+}
+
 bool MemoryAllocator::fail(const std::string& what) {
     ok_ = false;
     last_error_ = what;
@@ -84,7 +92,7 @@ std::optional<PhysicalBlockId> MemoryAllocator::allocate() {
     const PhysicalBlockId id = free_list_.back();
     free_list_.pop_back();
     PhysicalBlockInfo& info = infos_[id];
-    info.state = BlockState::Active;
+    set_state(info, BlockState::Active);
     info.ref_count = 1;
     return id;
 }
@@ -95,11 +103,11 @@ void MemoryAllocator::release(PhysicalBlockId id) {
     if (info.ref_count == 0) return;
     --info.ref_count;
     if (info.ref_count == 0) {
-        info.state = BlockState::Free;
+        set_state(info, BlockState::Free);
         ++info.generation;
         free_list_.push_back(id);
     } else if (info.ref_count == 1) {
-        info.state = BlockState::Active;
+        set_state(info, BlockState::Active);
     }
 }
 
@@ -108,7 +116,7 @@ void MemoryAllocator::retain(PhysicalBlockId id) {
     PhysicalBlockInfo& info = infos_[id];
     if (info.ref_count == 0) return;
     ++info.ref_count;
-    info.state = BlockState::Shared;
+    set_state(info, BlockState::Shared);
 }
 
 void MemoryAllocator::copy_block(PhysicalBlockId source, PhysicalBlockId destination) {
@@ -152,7 +160,7 @@ std::optional<SwapSlotId> MemoryAllocator::swap_out(PhysicalBlockId id) {
     const std::optional<SwapSlotId> slot = swap_backend_->store(*frame);
     if (!slot) return std::nullopt;
     info.ref_count = 0;
-    info.state = BlockState::Free;
+    set_state(info, BlockState::Free);
     ++info.generation;
     free_list_.push_back(id);
     return slot;
@@ -184,19 +192,16 @@ std::optional<PhysicalBlockId> MemoryAllocator::select_eviction_candidate() cons
     return eviction_selector_(*this);
 }
 
+// Same figures as counting every block's state (src/MemoryAllocator.cpp:178-207),
+// kept as running counts so the scheduler's per-step calls cost O(1).
 AllocatorStats MemoryAllocator::stats() const noexcept {
     AllocatorStats s;
     s.total_blocks = static_cast<std::uint32_t>(infos_.size());
-    for (const PhysicalBlockInfo& info : infos_) {
-        switch (info.state) {
-            case BlockState::Free: ++s.free_blocks; break;
-            case BlockState::Active: ++s.active_blocks; break;
-            case BlockState::Shared: ++s.shared_blocks; break;
-            case BlockState::Swapped: break;
-        }
-    }
+    s.free_blocks = state_counts_[static_cast<std::size_t>(BlockState::Free)];
+    s.active_blocks = state_counts_[static_cast<std::size_t>(BlockState::Active)];
+    s.shared_blocks = state_counts_[static_cast<std::size_t>(BlockState::Shared)];
     if (swap_backend_ != nullptr) s.swapped_blocks = static_cast<std::uint32_t>(swap_backend_->resident_slots());
-    for (const auto& b : blocks_) s.bytes_reserved += b->size_bytes();
+    s.bytes_reserved = bytes_reserved_;
     return s;
 }
 

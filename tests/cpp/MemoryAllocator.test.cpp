@@ -138,6 +138,63 @@ TEST(MemoryAllocatorTest, StatsFollowAllocateAndRelease) {
     (void)y;
 }
 
+// stats() keeps running counts; a recount of every block's state after a
+// seeded mix of allocate / retain / release / swap must give the same figures.
+TEST(MemoryAllocatorTest, RunningStatsEqualARecount) {
+    MemoryAllocator a(config_with(24));
+    HostSwapBackend swap(64);
+    a.set_swap_backend(&swap);
+    std::vector<PhysicalBlockId> held;
+    std::vector<SwapSlotId> slots;
+    std::uint64_t rng = 12345;
+    auto next = [&rng](std::uint64_t n) {
+        rng = rng * 6364136223846793005ull + 1442695040888963407ull;
+        return (rng >> 33) % n;
+    };
+    for (int step = 0; step < 3000; ++step) {
+        const std::uint64_t op = next(6);
+        if (op == 0 || held.empty()) {
+            if (const auto id = a.allocate()) held.push_back(*id);
+        } else if (op == 1) {
+            const PhysicalBlockId id = held[next(held.size())];
+            a.retain(id);
+            held.push_back(id);
+        } else if (op == 2 || op == 3) {
+            const std::size_t k = next(held.size());
+            a.release(held[k]);
+            held.erase(held.begin() + static_cast<std::ptrdiff_t>(k));
+        } else if (op == 4) {
+            const std::size_t k = next(held.size());
+            if (const auto slot = a.swap_out(held[k])) {
+                slots.push_back(*slot);
+                held.erase(held.begin() + static_cast<std::ptrdiff_t>(k));
+            }
+        } else if (!slots.empty()) {
+            const std::size_t k = next(slots.size());
+            if (const auto id = a.swap_in(slots[k])) {
+                held.push_back(*id);
+                slots.erase(slots.begin() + static_cast<std::ptrdiff_t>(k));
+            }
+        }
+        std::uint32_t free_n = 0, active_n = 0, shared_n = 0;
+        for (PhysicalBlockId id = 0; id < 24; ++id) {
+            switch (a.info(id)->state) {
+                case BlockState::Free: ++free_n; break;
+                case BlockState::Active: ++active_n; break;
+                case BlockState::Shared: ++shared_n; break;
+                case BlockState::Swapped: break;
+            }
+        }
+        const AllocatorStats st = a.stats();
+        ASSERT_EQ(st.total_blocks, 24u);
+        ASSERT_EQ(st.free_blocks, free_n);
+        ASSERT_EQ(st.active_blocks, active_n);
+        ASSERT_EQ(st.shared_blocks, shared_n);
+        ASSERT_EQ(st.swapped_blocks, static_cast<std::uint32_t>(slots.size()));
+        ASSERT_EQ(st.bytes_reserved, 24u * a.block(0)->size_bytes());
+    }
+}
+
 TEST(MemoryAllocatorTest, CanAllocateComparesWithTheFreeCount) {
     MemoryAllocator a(config_with(2));
     EXPECT_TRUE(a.can_allocate(0));
