@@ -272,6 +272,46 @@ int qvp_swap_scatter(void* kv_base, uint64_t block_stride, uint32_t num_blocks,
                      const uint32_t* frame_ids, const uint64_t* arena_offsets, uint32_t count,
                      const void* arena, uint64_t arena_bytes, uint64_t copy_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* KV append (tests/PagedAttention.test.cpp:97-127,                         */
+/* tests/EndToEnd.test.cpp:157-179)                                         */
+/* ------------------------------------------------------------------------ */
+
+/* Pool geometry and source tensors of qvp_append_kv. */
+typedef struct qvp_append_args {
+    void* kv_base;              /* device address of frame 0 */
+    uint64_t block_stride;      /* bytes between frames */
+    uint32_t num_blocks;        /* frames in the pool */
+    uint32_t kv_dtype;          /* qvp_dtype of the cache and of k / v */
+    uint32_t num_layers;        /* layers per frame (BlockShape::num_layers) */
+    uint32_t first_layer;       /* layers [first_layer, first_layer + layer_count) */
+    uint32_t layer_count;       /*   are written */
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t tokens_per_block;
+    uint64_t head_stride;       /* elements, KVBlockLayout::head_stride() */
+    uint64_t token_stride;      /* elements, KVBlockLayout::token_stride() */
+    uint64_t stream_stride;     /* elements, KVBlockLayout::stream_stride() */
+    uint64_t layer_stride;      /* elements, KVBlockLayout::layer_stride() */
+    const void* k;              /* device, [count][layer_count][num_kv_heads][head_dim] */
+    const void* v;              /* device, same shape */
+} qvp_append_args;
+
+/* For every token i < count and every written layer l, stream s (0 = K from
+ * k, 1 = V from v) and kv head h, stores the head_dim elements of the source
+ * row at element offset (first_layer + l) * layer_stride + s * stream_stride +
+ * slots[i] * token_stride + h * head_stride of frame frames[i]
+ * (KVBlockLayout::element_offset, src/CacheLayout.cpp:25-38), which is what the
+ * reference's harnesses do element by element after
+ * KVCacheManager::ensure_token_writable returned the frame. frames / slots are
+ * host arrays (slot = token position % tokens_per_block). Refused before
+ * anything is enqueued: a frame >= num_blocks (QVP_ERR_UNMAPPED), a slot >=
+ * tokens_per_block, a (frame, slot) pair given twice, layers outside
+ * num_layers, strides under which two elements coincide or the layout
+ * exceeds block_stride (QVP_ERR_INVALID_ARGUMENT). */
+int qvp_append_kv(const qvp_append_args* args, const uint32_t* frames, const uint32_t* slots,
+                  uint32_t count, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -381,3 +381,33 @@ void orc_copy_block(uint8_t* pool, uint64_t block_stride, uint32_t num_pool_bloc
     if (src >= num_pool_blocks || dst >= num_pool_blocks) return;
     memmove(pool + (uint64_t)dst * block_stride, pool + (uint64_t)src * block_stride, copy_bytes);
 }
+
+/* ---------------------------------------------------------------- */
+/* K/V append (tests/PagedAttention.test.cpp:97-127,                */
+/* tests/EndToEnd.test.cpp:157-179)                                 */
+/* ---------------------------------------------------------------- */
+
+int orc_append_kv(uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks, uint32_t elem_bytes,
+                  uint32_t tpb, uint32_t num_layers, uint32_t num_kv_heads, uint32_t head_dim,
+                  uint32_t first_layer, uint32_t layer_count, const uint32_t* frames, const uint32_t* slots,
+                  uint32_t count, const uint8_t* k, const uint8_t* v) {
+    if ((uint64_t)first_layer + layer_count > num_layers) return -1;
+    for (uint32_t i = 0; i < count; ++i) {
+        if (frames[i] >= num_pool_blocks || slots[i] >= tpb) return -1;
+    }
+    const uint64_t row = (uint64_t)head_dim * elem_bytes;
+    for (uint32_t i = 0; i < count; ++i) {
+        uint8_t* frame = pool + (uint64_t)frames[i] * block_stride;
+        for (uint32_t l = 0; l < layer_count; ++l) {
+            for (uint32_t s = 0; s < 2; ++s) {
+                const uint8_t* src = (s == 0 ? k : v) + ((uint64_t)i * layer_count + l) * num_kv_heads * row;
+                for (uint32_t h = 0; h < num_kv_heads; ++h) {
+                    const int64_t off = orc_element_offset(tpb, num_layers, num_kv_heads, head_dim,
+                                                           first_layer + l, s, slots[i], h);
+                    memcpy(frame + (uint64_t)off * elem_bytes, src + (uint64_t)h * row, row);
+                }
+            }
+        }
+    }
+    return 0;
+}

@@ -12,7 +12,9 @@
  * under tests/golden/, and the closed-form cases of
  * tests/PagedAttention.test.cpp (uniform keys, one-hot selection, GQA, CoW
  * branches); the layout functions match CacheView.test.cpp's invariants; pack
- * and copy are checked against BlockTable entries and memcpy identity.
+ * and copy are checked against BlockTable entries and memcpy identity; the
+ * append is checked against the compiled reference's element_offset and a
+ * read-back of every written element (untouched bytes unchanged).
  */
 #ifndef QVP_ORACLE_H
 #define QVP_ORACLE_H
@@ -92,6 +94,20 @@ int orc_pack(uint32_t num_seqs, const uint32_t* ids, const uint32_t* cu_blocks,
  * outside the pool. */
 void orc_copy_block(uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks, uint32_t src,
                     uint32_t dst, uint64_t copy_bytes);
+
+/* The K/V writes of one decode step, as the reference's harnesses make them
+ * after KVCacheManager::ensure_token_writable returned the frame
+ * (tests/PagedAttention.test.cpp:97-127, tests/EndToEnd.test.cpp:157-179):
+ * for token i, layer first_layer + l, stream s (0 = K from k, 1 = V from v) and
+ * kv head h, head_dim elements of elem_bytes each go to element offset
+ * orc_element_offset(..., first_layer + l, s, slots[i], h) of frame frames[i].
+ * k / v are [count][layer_count][num_kv_heads][head_dim]. Tokens are applied in
+ * order. Returns -1 without writing when a frame, slot or layer is out of
+ * range, else 0. */
+int orc_append_kv(uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks, uint32_t elem_bytes,
+                  uint32_t tokens_per_block, uint32_t num_layers, uint32_t num_kv_heads, uint32_t head_dim,
+                  uint32_t first_layer, uint32_t layer_count, const uint32_t* frames, const uint32_t* slots,
+                  uint32_t count, const uint8_t* k, const uint8_t* v);
 
 #ifdef __cplusplus
 }

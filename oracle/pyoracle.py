@@ -66,6 +66,9 @@ def oracle() -> ctypes.CDLL:
             _i32p, _i32p, _i32p, _i32p, _i32p, _i32p,
         ]
         lib.orc_copy_block.argtypes = [c_void_p, c_uint64, c_uint32, c_uint32, c_uint32, c_uint64]
+        lib.orc_append_kv.restype = ctypes.c_int
+        lib.orc_append_kv.argtypes = [c_void_p, c_uint64] + [c_uint32] * 8 + [_u32p, _u32p, c_uint32, c_void_p,
+                                                                              c_void_p]
         _oracle = lib
     return _oracle
 
@@ -121,6 +124,20 @@ def decode_batch(pool: np.ndarray, block_stride: int, num_pool_blocks: int, ids,
         pool.ctypes.data, block_stride, num_pool_blocks, B, ids_p, cu_p, ctx_p, dtype, query.ctypes.data,
         layer, num_layers, hq, hkv, d, tpb, scale, out.ctypes.data, out_f32.ctypes.data, threads)
     return refused, out, out_f32
+
+
+def append_kv(pool: np.ndarray, block_stride: int, num_pool_blocks: int, elem_bytes: int, tpb: int,
+              num_layers: int, hkv: int, d: int, first_layer: int, layer_count: int, frames, slots,
+              k: np.ndarray, v: np.ndarray) -> int:
+    """Applies one step's K/V writes to a host pool image in place; -1 = refused."""
+    assert pool.flags["C_CONTIGUOUS"]
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    f_a, f_p = _u32(frames)
+    s_a, s_p = _u32(slots)
+    return oracle().orc_append_kv(pool.ctypes.data, block_stride, num_pool_blocks, elem_bytes, tpb, num_layers,
+                                  hkv, d, first_layer, layer_count, f_p, s_p, len(np.atleast_1d(frames)),
+                                  k.ctypes.data, v.ctypes.data)
 
 
 def pack(ids, cu_blocks, context_lens, tpb: int, num_pool_blocks: int, split_tokens: int = 0):

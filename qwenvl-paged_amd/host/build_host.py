@@ -55,6 +55,7 @@ TEST_BINARIES = {
         "DeviceAllocator.test.cpp",
         "PagedAttention.test.cpp",
         "EndToEnd.test.cpp",
+        "KVAppend.test.cpp",
     ],
 }
 

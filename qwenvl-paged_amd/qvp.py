@@ -82,6 +82,27 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class AppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("kv_base", c_void_p),
+        ("block_stride", c_uint64),
+        ("num_blocks", c_uint32),
+        ("kv_dtype", c_uint32),
+        ("num_layers", c_uint32),
+        ("first_layer", c_uint32),
+        ("layer_count", c_uint32),
+        ("num_kv_heads", c_uint32),
+        ("head_dim", c_uint32),
+        ("tokens_per_block", c_uint32),
+        ("head_stride", c_uint64),
+        ("token_stride", c_uint64),
+        ("stream_stride", c_uint64),
+        ("layer_stride", c_uint64),
+        ("k", c_void_p),
+        ("v", c_void_p),
+    ]
+
+
 _u32p = POINTER(c_uint32)
 _u64p = POINTER(c_uint64)
 
@@ -135,6 +156,7 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_uint64, c_uint32, _u32p, _u64p, c_uint32, c_void_p, c_uint64, c_uint64, c_void_p],
     ),
+    "qvp_append_kv": (c_int, [POINTER(AppendArgs), _u32p, _u32p, c_uint32, c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -492,3 +514,21 @@ def swap_scatter(kv_base: int, block_stride: int, num_blocks: int, frames, offse
     o_a, o_p = _u64(offsets)
     check(load().qvp_swap_scatter(kv_base, block_stride, num_blocks, f_p, o_p, len(f_a), arena.ptr, arena.nbytes,
                                   copy_bytes, _sp(stream)))
+
+
+def append_args(*, kv_base: int, block_stride: int, num_blocks: int, kv_dtype: int, num_layers: int,
+                first_layer: int, layer_count: int, num_kv_heads: int, head_dim: int, tokens_per_block: int,
+                k: int, v: int, strides: dict | None = None) -> AppendArgs:
+    s = strides or layout_strides(tokens_per_block, num_layers, num_kv_heads, head_dim)
+    return AppendArgs(kv_base, block_stride, num_blocks, kv_dtype, num_layers, first_layer, layer_count,
+                      num_kv_heads, head_dim, tokens_per_block, s["head_stride"], s["token_stride"],
+                      s["stream_stride"], s["layer_stride"], k, v)
+
+
+def append_kv(args: AppendArgs, frames, slots, stream=None) -> None:
+    """Writes count tokens' K/V rows (qvp_append_kv); frames and slots are host arrays."""
+    f_a, f_p = _u32(frames)
+    s_a, s_p = _u32(slots)
+    if len(f_a) != len(s_a):
+        raise ValueError("frames and slots differ in length")
+    check(load().qvp_append_kv(byref(args), f_p, s_p, len(f_a), _sp(stream)))

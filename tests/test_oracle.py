@@ -386,6 +386,85 @@ def test_copy_block_is_memcpy_identity():
     assert np.array_equal(view[others], orig[others])
 
 
+# K/V append: every written head row lands at the closed-form offset of the
+# layout ((layer * 2 + stream) * tpb + slot) * Hkv * D + h * D (pinned against
+# the compiled reference above), and no other byte of the pool changes.
+APPEND_CASES = [
+    # tpb, layers, hkv, d, bpe, first_layer, layer_count, tokens, frames
+    (16, 1, 2, 64, 4, 0, 1, 4, 8),
+    (16, 1, 4, 128, 2, 0, 1, 40, 64),
+    (16, 3, 3, 8, 2, 1, 2, 20, 6),
+    (4, 2, 1, 5, 4, 0, 2, 7, 3),
+]
+
+
+def _append_expected_rows(shape, frames, slots, first_layer, layer_count):
+    tpb, layers, hkv, d, bpe = shape
+    for i, (f, t) in enumerate(zip(frames, slots)):
+        for l in range(layer_count):
+            for s in range(2):
+                for h in range(hkv):
+                    off = (((first_layer + l) * 2 + s) * tpb + t) * hkv * d + h * d
+                    yield i, l, s, h, f, off * bpe
+
+
+def _append_case(case, seed):
+    tpb, layers, hkv, d, bpe, first_layer, layer_count, tokens, nframes = case
+    shape = (tpb, layers, hkv, d, bpe)
+    rng = np.random.default_rng(seed)
+    stride = O.oracle().orc_block_stride(O.oracle().orc_block_byte_size(*shape), 256)
+    pool = rng.integers(0, 256, nframes * stride, dtype=np.uint8)
+    pairs = rng.choice(nframes * tpb, size=tokens, replace=False)
+    frames, slots = (pairs // tpb).astype(np.uint32), (pairs % tpb).astype(np.uint32)
+    k = rng.integers(0, 256, tokens * layer_count * hkv * d * bpe, dtype=np.uint8)
+    v = rng.integers(0, 256, tokens * layer_count * hkv * d * bpe, dtype=np.uint8)
+    return shape, stride, pool, frames, slots, k, v
+
+
+def _check_append(case, stride, before, after, frames, slots, k, v):
+    tpb, layers, hkv, d, bpe, first_layer, layer_count, tokens, nframes = case
+    shape = (tpb, layers, hkv, d, bpe)
+    row = d * bpe
+    written = np.zeros(before.size, bool)
+    for i, l, s, h, f, off in _append_expected_rows(shape, frames, slots, first_layer, layer_count):
+        src = (k if s == 0 else v)[((i * layer_count + l) * hkv + h) * row:][:row]
+        at = f * stride + off
+        if not np.array_equal(after[at:at + row], src):
+            return False
+        written[at:at + row] = True
+    return np.array_equal(after[~written], before[~written])
+
+
+@pytest.mark.parametrize("case", APPEND_CASES)
+def test_append_writes_rows_at_the_layout_offsets(case):
+    shape, stride, pool, frames, slots, k, v = _append_case(case, seed=7)
+    before = pool.copy()
+    tpb, layers, hkv, d, bpe, first_layer, layer_count, tokens, nframes = case
+    assert O.append_kv(pool, stride, nframes, bpe, tpb, layers, hkv, d, first_layer, layer_count, frames, slots,
+                       k, v) == 0
+    assert _check_append(case, stride, before, pool, frames, slots, k, v)
+    # Refusals write nothing: a frame outside the pool, a slot past the block,
+    # layers past num_layers.
+    for f2, s2, fl, lc in ((nframes, 0, first_layer, layer_count), (0, tpb, first_layer, layer_count),
+                           (0, 0, layers - layer_count + 1, layer_count)):
+        img = before.copy()
+        bad_f, bad_s = frames.copy(), slots.copy()
+        bad_f[-1], bad_s[-1] = (f2, s2) if (f2, s2) != (0, 0) else (bad_f[-1], bad_s[-1])
+        assert O.append_kv(img, stride, nframes, bpe, tpb, layers, hkv, d, fl, lc, bad_f, bad_s, k, v) == -1
+        assert np.array_equal(img, before)
+
+
+def test_append_check_rejects_a_planted_mistake():
+    """The read-back check fails for an oracle call with K and V swapped."""
+    case = APPEND_CASES[1]
+    shape, stride, pool, frames, slots, k, v = _append_case(case, seed=8)
+    before = pool.copy()
+    tpb, layers, hkv, d, bpe, first_layer, layer_count, tokens, nframes = case
+    assert O.append_kv(pool, stride, nframes, bpe, tpb, layers, hkv, d, first_layer, layer_count, frames, slots,
+                       v, k) == 0
+    assert not _check_append(case, stride, before, pool, frames, slots, k, v)
+
+
 def test_bf16_conversion_rounds_to_nearest_even():
     lib = O.oracle()
     assert lib.orc_bf16_from_f32(1.0) == 0x3F80
