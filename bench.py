@@ -19,8 +19,10 @@ compiled reference paged_attention_decode<T> (oracle/_ref) on this host over
 the same batch, single-threaded like the reference engine loop.
 
 Other lines (not the headline): --workload config3 (Qwen2-VL-72B layer, B=32,
-ctx U[8192, 32768]), --cow (copy-on-write configuration, C++ driver) and
---trace (continuous-batching trace, C++ driver) each print their own JSON line.
+ctx U[8192, 32768]), --cow (copy-on-write configuration, C++ driver),
+--trace (continuous-batching trace, C++ driver) and --append (the K/V append
+of one config2 step, one layer and all 28 layers) each print their own JSON
+line.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -162,6 +164,63 @@ def copy_calibration(steps: int) -> int:
     return 0
 
 
+def append_case(name: str, w: W.Workload, num_layers: int, first_layer: int, layer_count: int, steps: int,
+                warmup: int) -> dict:
+    """Times qvp_append_kv for the next token of every sequence of `w` (its
+    frame from the sequence's table, or an unused frame at a block boundary),
+    with `num_layers`-layer frames."""
+    tpb, hkv, d = w.tokens_per_block, w.num_kv_heads, w.head_dim
+    block_bytes = tpb * num_layers * hkv * d * 2 * 2
+    # Only the frames the step writes need to exist: renumber them densely.
+    unused = iter(sorted(set(range(w.num_pool_blocks)) - set(int(x) for x in w.ids)))
+    frames, slots = [], []
+    for b in range(w.num_seqs):
+        row = w.ids[w.cu_blocks[b]:w.cu_blocks[b + 1]]
+        pos = int(w.context_lens[b])
+        frames.append(int(row[pos // tpb]) if pos // tpb < len(row) else next(unused))
+        slots.append(pos % tpb)
+    uniq = {f: i for i, f in enumerate(sorted(set(frames)))}
+    nframes = len(uniq) if num_layers > 1 else w.num_pool_blocks
+    frames = np.array([uniq[f] if num_layers > 1 else f for f in frames], np.uint32)
+    slots = np.array(slots, np.uint32)
+    pool = qvp.BlockPool(nframes, block_bytes)
+    pool.upload_all(np.zeros(nframes * pool.stride, np.uint8))
+    rng = np.random.default_rng(3)
+    n = w.num_seqs * layer_count * hkv * d
+    k = qvp.DeviceBuffer.from_array(W.f32_to_bf16_bits(rng.normal(0, 0.5, n).astype(np.float32)))
+    v = qvp.DeviceBuffer.from_array(W.f32_to_bf16_bits(rng.normal(0, 0.5, n).astype(np.float32)))
+    args = qvp.append_args(kv_base=pool.base, block_stride=pool.stride, num_blocks=nframes, kv_dtype=qvp.DTYPE_BF16,
+                           num_layers=num_layers, first_layer=first_layer, layer_count=layer_count,
+                           num_kv_heads=hkv, head_dim=d, tokens_per_block=tpb, k=k.ptr, v=v.ptr)
+    stream = qvp.Stream()
+    for _ in range(warmup):
+        qvp.append_kv(args, frames, slots, stream)
+    stream.synchronize()
+    e0, e1 = qvp.Event(), qvp.Event()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        qvp.append_kv(args, frames, slots, stream)
+    e1.record(stream)
+    stream.synchronize()
+    wall_us = (time.perf_counter() - t0) / steps * 1e6
+    gpu_us = e0.elapsed_ms(e1) / steps * 1e3
+    # Algorithmic bytes: the K and V rows read once and written once.
+    moved = 2 * 2 * w.num_seqs * layer_count * hkv * d * 2
+    return {"case": name, "tokens": w.num_seqs, "layers_written": layer_count, "frame_layers": num_layers,
+            "bytes_per_call": moved, "gpu_us_per_call": round(gpu_us, 3), "wall_us_per_call": round(wall_us, 3),
+            "GBps_gpu": round(moved / (gpu_us * 1e-6) / 1e9, 1)}
+
+
+def append_bench(steps: int, warmup: int) -> int:
+    w = W.config2()
+    cases = [append_case("config2 step, one layer", w, 1, 0, 1, steps, warmup),
+             append_case("config2 step, all 28 layers of a Qwen2-VL-7B frame", w, 28, 0, 28, steps, warmup)]
+    print(json.dumps({"mode": "append", "kernel": "append_rows", "data": "synthetic bf16 N(0,0.5) rows",
+                      "cases": cases}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -174,12 +233,15 @@ def main() -> int:
     ap.add_argument("--workload", choices=["config2", "config3"], default="config2")
     ap.add_argument("--cow", action="store_true", help="run the copy-on-write configuration driver")
     ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
+    ap.add_argument("--append", action="store_true", help="time the K/V append of one config2 step")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
                          "used to scale rocprof FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.steps)
+    if args.append:
+        return append_bench(args.steps, args.warmup)
     if args.cow or args.trace:
         return run_driver("cow_bench" if args.cow else "trace_bench")
 
