@@ -59,8 +59,10 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kTileTokens = 32;
 constexpr int kD = 128;
 constexpr int kRowPad = kD + 4;
-constexpr int kMinTilesPerWg = 4;
 constexpr int kWgsPerCu = 2;
+// Tiles per wave (whole batch over the resident waves) from which kv heads are
+// decoded four side by side.
+constexpr uint64_t kMinTilesPerWaveForHeadGroups = 32;
 // Share of a first-round workgroup's tiles given to a second-round one.
 constexpr double kSecondRoundShare = 0.72;
 // A workgroup's range is contiguous, so only its first and last pieces can be
@@ -75,9 +77,10 @@ struct MfmaArgs {
     const qvp_piece* pieces;
     const int32_t* wg_begin;
     int32_t* counters;
-    float* ws_ml;   // [slot][group][2] : running max (base 2), running sum
-    float* ws_acc;  // [slot][group][128]
+    float* ws_ml;   // [slot][hps][group][2] : running max (base 2), running sum
+    float* ws_acc;  // [slot][hps][group][128]
     void* out;      // [num_seqs][Hq][128]
+    int hps;        // kv heads per segment (4, 2 or 1)
 };
 
 struct KvTile {
@@ -116,21 +119,22 @@ struct TileRef {
     int32_t blk0, blk1;  // frames of tokens 32t .. 32t+15 and 32t+16 .. 32t+31
 };
 
-// Advances (pi, t) to this wave's next tile: t + 4 in the same piece, else the
-// first piece after it where the wave has a tile (round-robin start t0 + wave).
-// Starts from piece pi when t < 0. Returns false when the range is exhausted.
-__device__ inline bool next_tile(const MfmaArgs& a, int pe, int wave, int& pi, int& t) {
+// Advances (pi, t) to this wave's next tile: t + tl in the same piece, else
+// the first piece after it where the wave has a tile (start t0 + lane). The tl
+// tile lanes of a kv head take a piece's tiles round-robin. Starts from piece
+// pi when t < 0. Returns false when the range is exhausted.
+__device__ inline bool next_tile(const MfmaArgs& a, int pe, int lane, int tl, int& pi, int& t) {
     if (t >= 0) {
-        if (t + kWaves < piece_at(a.pieces, pi).t1) {
-            t += kWaves;
+        if (t + tl < piece_at(a.pieces, pi).t1) {
+            t += tl;
             return true;
         }
         ++pi;
     }
     for (; pi < pe; ++pi) {
         const qvp_piece d = piece_at(a.pieces, pi);
-        if (d.t0 + wave < d.t1) {
-            t = d.t0 + wave;
+        if (d.t0 + lane < d.t1) {
+            t = d.t0 + lane;
             return true;
         }
     }
@@ -138,14 +142,14 @@ __device__ inline bool next_tile(const MfmaArgs& a, int pe, int wave, int& pi, i
     return false;
 }
 
-// Fetches the block ids of tile t of piece pi. A 16-token half never straddles
-// a block (tpb is a power of two >= 16); tokens past the context fall back to
-// the last valid block.
-__device__ inline TileRef resolve_tile(const DecodeGeometry& p, const MfmaArgs& a, int pi, int t) {
+// Fetches the block ids of tile t of piece pi for kv head d.g * hps + hl. A
+// 16-token half never straddles a block (tpb is a power of two >= 16); tokens
+// past the context fall back to the last valid block.
+__device__ inline TileRef resolve_tile(const DecodeGeometry& p, const MfmaArgs& a, int pi, int t, int hl) {
     const qvp_piece d = piece_at(a.pieces, pi);
     TileRef r;
     r.b = d.b;
-    r.g = d.g;
+    r.g = d.g * a.hps + hl;
     r.t = t;
     r.ctx = d.ctx;
     const auto* row = as_const(p.tables) + static_cast<uint64_t>(d.b) * p.max_nb;
@@ -296,6 +300,12 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     const int c = lane & 15;
     const int j = lane >> 4;
     const int G = static_cast<int>(p.group);
+    // Wave w decodes kv head hl = w % hps of each segment, tile lane w / hps.
+    const int hps = a.hps;
+    const int tl = kWaves / hps;
+    const int hl = wave % hps;
+    const int tlane = wave / hps;
+    const int hpsG = hps * G;
 
     const int pb = as_const(a.wg_begin)[blockIdx.x];
     const int pe = as_const(a.wg_begin)[blockIdx.x + 1];
@@ -308,15 +318,16 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     int pi2 = pb;
     int t2 = -1;
     bool have_partial = false;
-    bool has2 = next_tile(a, pe, wave, pi2, t2);
-    if (has2) load_tile(p, resolve_tile(p, a, pi2, t2), c, j, nxt);
-    has2 = has2 && next_tile(a, pe, wave, pi2, t2);
+    bool has2 = next_tile(a, pe, tlane, tl, pi2, t2);
+    if (has2) load_tile(p, resolve_tile(p, a, pi2, t2, hl), c, j, nxt);
+    has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
     TileRef r2{};
-    if (has2) r2 = resolve_tile(p, a, pi2, t2);
+    if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
 
     for (int pi = pb; pi < pe; ++pi) {
         const qvp_piece d = piece_at(a.pieces, pi);
         const int ctx = d.ctx;
+        const int g = d.g * hps + hl;  // this wave's kv head
 
         // Query B operand: lane (c, j), MFMA i -> Q[head g*G + c][dims 32i + 8j
         // .. +8]. Columns past the group repeat the group's last head: their
@@ -326,7 +337,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         u32x4 qop[4];
         {
             const uint16_t* q = static_cast<const uint16_t*>(p.query) +
-                                (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + min(c, G - 1)) * kD;
+                                (static_cast<uint64_t>(d.b) * p.num_q_heads + g * G + min(c, G - 1)) * kD;
 #pragma unroll
             for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
         }
@@ -337,15 +348,15 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         float m_run = -INFINITY;
         float l_run = 0.f;
 
-        for (int t = d.t0 + wave; t < d.t1; t += kWaves) {
+        for (int t = d.t0 + tlane; t < d.t1; t += tl) {
             KvTile cur = nxt;
             if (has2) load_tile(p, r2, c, j, nxt);
-            has2 = has2 && next_tile(a, pe, wave, pi2, t2);
-            if (has2) r2 = resolve_tile(p, a, pi2, t2);
+            has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
+            if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
             compute_tile(cur, qop, t * kTileTokens, ctx, p.scale_log2, j, m_run, l_run, o);
         }
 
-        // Merge the four waves' states for this piece.
+        // This wave's state for (piece, head g) goes to LDS in row layout.
         l_run = sum_over_j(l_run);
         if (j == 0) {
             sm_m[wave][c] = m_run;
@@ -355,41 +366,99 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int n = 0; n < 8; ++n) sm_o[wave][c][32 * j + 8 * r + n] = o[n][r];
-        lds_barrier();
 
         const int slot = d.slot;
         have_partial = have_partial || slot >= 0;
-        for (int e = threadIdx.x; e < G * kD; e += kThreads) {
-            const int hc = e >> 7;
-            const int dd = e & (kD - 1);
-            float mmax = sm_m[0][hc];
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) mmax = fmaxf(mmax, sm_m[w][hc]);
-            float acc = 0.f;
-            float lsum = 0.f;
-#pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
-                const float f = fast_exp2(sm_m[w][hc] - mmax);
-                acc += sm_o[w][hc][dd] * f;
-                lsum += sm_l[w][hc] * f;
-            }
-            if (slot < 0) {
-                OutT* out = static_cast<OutT*>(a.out);
-                out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + hc) * kD + dd] =
-                    from_float<OutT>(acc / lsum);
-            } else {
-                // Agent-scope stores are written through to the point of
-                // coherence shared by all XCDs; the wait before the count-in
-                // makes sure they have arrived.
-                const uint64_t row = static_cast<uint64_t>(slot) * G + hc;
-                __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (dd == 0) {
-                    __hip_atomic_store(&a.ws_ml[row * 2 + 0], mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(&a.ws_ml[row * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        OutT* out = static_cast<OutT*>(a.out);
+        const uint64_t out_row0 = (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * hpsG) * kD;
+        if (tl == 1) {
+            // The wave holds the whole piece for its head: it writes its rows
+            // itself, with no workgroup barrier (its own LDS writes are visible
+            // to its own later reads).
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int e = lane; e < G * kD; e += 64) {
+                const int hc = e >> 7;
+                const int dd = e & (kD - 1);
+                const float acc = sm_o[wave][hc][dd];
+                if (slot < 0) {
+                    out[out_row0 + static_cast<uint64_t>(hl * G + hc) * kD + dd] = from_float<OutT>(acc / sm_l[wave][hc]);
+                } else {
+                    // Agent-scope stores are written through to the point of
+                    // coherence shared by all XCDs; the wait before the count-in
+                    // makes sure they have arrived.
+                    const uint64_t row = static_cast<uint64_t>(slot) * hpsG + hl * G + hc;
+                    __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (dd == 0) {
+                        __hip_atomic_store(&a.ws_ml[row * 2 + 0], sm_m[wave][hc], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(&a.ws_ml[row * 2 + 1], sm_l[wave][hc], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
             }
+            // Later writes of this wave's LDS rows come after these reads.
+            __builtin_amdgcn_wave_barrier();
+        } else if (hps == 1) {
+            // The four waves are tile lanes of one head: merge them through LDS.
+            lds_barrier();
+            for (int e = threadIdx.x; e < G * kD; e += kThreads) {
+                const int hc = e >> 7;
+                const int dd = e & (kD - 1);
+                float mmax = sm_m[0][hc];
+#pragma unroll
+                for (int w = 1; w < kWaves; ++w) mmax = fmaxf(mmax, sm_m[w][hc]);
+                float acc = 0.f;
+                float lsum = 0.f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) {
+                    const float f = fast_exp2(sm_m[w][hc] - mmax);
+                    acc += sm_o[w][hc][dd] * f;
+                    lsum += sm_l[w][hc] * f;
+                }
+                if (slot < 0) {
+                    out[out_row0 + e] = from_float<OutT>(acc / lsum);
+                } else {
+                    const uint64_t row = static_cast<uint64_t>(slot) * G + hc;
+                    __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (dd == 0) {
+                        __hip_atomic_store(&a.ws_ml[row * 2 + 0], mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(&a.ws_ml[row * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+            lds_barrier();
+        } else {
+            // Two heads of two tile lanes each: merge the lanes through LDS.
+            lds_barrier();
+            for (int e = threadIdx.x; e < hpsG * kD; e += kThreads) {
+                const int ri = e >> 7;  // row within the segment: head ri / G, query column ri % G
+                const int h2 = ri / G;
+                const int hc = ri - h2 * G;
+                const int dd = e & (kD - 1);
+                float mmax = sm_m[h2][hc];
+                for (int w = h2 + hps; w < kWaves; w += hps) mmax = fmaxf(mmax, sm_m[w][hc]);
+                float acc = 0.f;
+                float lsum = 0.f;
+                for (int w = h2; w < kWaves; w += hps) {
+                    const float f = fast_exp2(sm_m[w][hc] - mmax);
+                    acc += sm_o[w][hc][dd] * f;
+                    lsum += sm_l[w][hc] * f;
+                }
+                if (slot < 0) {
+                    out[out_row0 + e] = from_float<OutT>(acc / lsum);
+                } else {
+                    const uint64_t row = static_cast<uint64_t>(slot) * hpsG + ri;
+                    __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (dd == 0) {
+                        __hip_atomic_store(&a.ws_ml[row * 2 + 0], mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(&a.ws_ml[row * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                }
+            }
+            lds_barrier();
         }
-        lds_barrier();
     }
 
     if (!have_partial) return;
@@ -440,10 +509,10 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     const qvp_piece m0 = piece_at(a.pieces, pm0 >= 0 ? pm0 : pm1);
     const qvp_piece m1 = piece_at(a.pieces, pm1 >= 0 ? pm1 : pm0);
     const int max_ns = max(m0.seg_nslots, m1.seg_nslots);
-    const uint64_t orow0 = (static_cast<uint64_t>(m0.b) * p.num_q_heads + m0.g * G) * kD;
-    const uint64_t orow1 = (static_cast<uint64_t>(m1.b) * p.num_q_heads + m1.g * G) * kD;
+    const uint64_t orow0 = (static_cast<uint64_t>(m0.b) * p.num_q_heads + m0.g * hpsG) * kD;
+    const uint64_t orow1 = (static_cast<uint64_t>(m1.b) * p.num_q_heads + m1.g * hpsG) * kD;
     OutT* out = static_cast<OutT*>(a.out);
-    const int per_seg = G * kD;
+    const int per_seg = hpsG * kD;
     const int total = nm * per_seg;
     for (int f0 = threadIdx.x; f0 < total; f0 += kThreads * kMergeBatch) {
         int hc[kMergeBatch], dd[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch];
@@ -473,7 +542,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
                     l[i][x] = 0.f;
                     o[i][x] = 0.f;
                     if (c0 + x < ns[i]) {
-                        const uint64_t row = static_cast<uint64_t>(s0[i] + c0 + x) * G + hc[i];
+                        const uint64_t row = static_cast<uint64_t>(s0[i] + c0 + x) * hpsG + hc[i];
                         m[i][x] = __hip_atomic_load(&a.ws_ml[row * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         l[i][x] =
                             __hip_atomic_load(&a.ws_ml[row * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -531,6 +600,18 @@ int device_max_wgs(uint32_t* wgs) {
 
 size_t align_ints(size_t n) { return (n + 63) / 64 * 64; }
 
+// kv heads decoded side by side by one workgroup. Four (when they divide the
+// kv head count) lets each wave own one head of the same tiles: no per-piece
+// merge of the waves' states and whole token rows read together. But a
+// segment then spans four heads, so the batch is cut into 4x fewer, longer
+// segments and each split segment gathers more, larger slots in its final
+// merge; that pays only when every wave streams many tiles (long contexts).
+uint32_t head_group_size(uint32_t num_kv_heads, uint64_t tiles_per_head, uint32_t max_wgs) {
+    const uint64_t per_wave = tiles_per_head * num_kv_heads / (static_cast<uint64_t>(max_wgs) * kWaves);
+    if (per_wave < kMinTilesPerWaveForHeadGroups) return 1;
+    return num_kv_heads % 4 == 0 ? 4u : (num_kv_heads % 2 == 0 ? 2u : 1u);
+}
+
 }  // namespace
 
 void destroy_schedule(qvp_schedule& s) {
@@ -560,20 +641,27 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     }
     s.valid = false;
 
-    // Segments (b, g), b-major, and their tile counts.
+    // Segments (b, q), b-major: sequence b's kv heads q * hps .. q * hps + hps - 1,
+    // and their tile counts. With hps kv heads per segment the four waves of a
+    // workgroup split as hps heads x (4 / hps) tile lanes.
     const std::vector<int32_t>& lens = batch->host_seq_lens;
-    const size_t nseg = lens.size() * num_kv_heads;
+    uint64_t tiles_per_head = 0;
+    for (const int32_t len : lens) tiles_per_head += (static_cast<uint64_t>(len) + kTileTokens - 1) / kTileTokens;
+    const uint32_t hps = head_group_size(num_kv_heads, tiles_per_head, max_wgs);
+    const uint32_t nq = num_kv_heads / hps;
+    const uint64_t tl = kWaves / hps;
+    const size_t nseg = lens.size() * nq;
     std::vector<uint64_t> seg_cum(nseg + 1, 0);
     for (size_t b = 0; b < lens.size(); ++b) {
         const uint64_t tiles = (static_cast<uint64_t>(lens[b]) + kTileTokens - 1) / kTileTokens;
-        for (uint32_t g = 0; g < num_kv_heads; ++g) {
-            const size_t sidx = b * num_kv_heads + g;
+        for (uint32_t q = 0; q < nq; ++q) {
+            const size_t sidx = b * nq + q;
             seg_cum[sidx + 1] = seg_cum[sidx] + tiles;
         }
     }
     const uint64_t total = seg_cum[nseg];
-    const uint64_t wgs64 =
-        std::min<uint64_t>(max_wgs, std::max<uint64_t>(1, (total + kMinTilesPerWg - 1) / kMinTilesPerWg));
+    // At least one tile per tile lane.
+    const uint64_t wgs64 = std::min<uint64_t>(max_wgs, std::max<uint64_t>(1, (total + tl - 1) / tl));
     const uint32_t W = static_cast<uint32_t>(wgs64);
 
     // Contiguous tile ranges, cut at segment boundaries into pieces. The
@@ -605,8 +693,8 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
             while (seg_cum[seg + 1] <= pos) ++seg;
             const uint64_t end = std::min(hi, seg_cum[seg + 1]);
             qvp_piece pc{};
-            pc.b = static_cast<int32_t>(seg / num_kv_heads);
-            pc.g = static_cast<int32_t>(seg % num_kv_heads);
+            pc.b = static_cast<int32_t>(seg / nq);
+            pc.g = static_cast<int32_t>(seg % nq);
             pc.t0 = static_cast<int32_t>(pos - seg_cum[seg]);
             pc.t1 = static_cast<int32_t>(end - seg_cum[seg]);
             pc.ctx = lens[pc.b];
@@ -687,13 +775,14 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     s.num_wgs = W;
     s.num_pieces = static_cast<uint32_t>(pieces.size());
     s.num_slots = static_cast<uint32_t>(next_slot);
+    s.hps = hps;
     s.max_partial_pieces_per_wg = max_partial;
     s.valid = true;
     return QVP_OK;
 }
 
 uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim) {
-    const uint64_t rows = static_cast<uint64_t>(batch->sched.num_slots) * group;
+    const uint64_t rows = static_cast<uint64_t>(batch->sched.num_slots) * batch->sched.hps * group;
     return round_up(rows * 2 * sizeof(float), 256) + round_up(rows * head_dim * sizeof(float), 256);
 }
 
@@ -704,10 +793,11 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     a.wg_begin = s.device + s.off_wg_begin;
     a.pieces = reinterpret_cast<const qvp_piece*>(s.device + s.off_pieces);
     a.counters = s.device + s.off_counters;
-    const uint64_t rows = static_cast<uint64_t>(s.num_slots) * g.group;
+    const uint64_t rows = static_cast<uint64_t>(s.num_slots) * s.hps * g.group;
     a.ws_ml = static_cast<float*>(workspace);
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + round_up(rows * 2 * sizeof(float), 256));
     a.out = out;
+    a.hps = static_cast<int>(s.hps);
     const dim3 grid(s.num_wgs);
     switch (out_dtype) {
         case QVP_DTYPE_F32:

@@ -18,6 +18,17 @@ BF16_REL_TOL = 1e-2
 BF16_REL_FLOOR = 1e-3
 
 
+def tiled_pool_image(w: W.Workload, chunk_elems: int = 16_777_259) -> np.ndarray:
+    """A pool image for large workloads, quick to make: one seeded chunk of
+    N(0, kv_sigma^2) bf16 elements repeated over the frames. The chunk length is
+    odd, so no two frames see the same bytes at the same offsets."""
+    assert w.kv_dtype == qvp.DTYPE_BF16 and w.block_stride == w.block_bytes
+    total = w.num_pool_blocks * w.block_bytes // 2
+    chunk = W.f32_to_bf16_bits(np.random.default_rng(w.seed).normal(0.0, w.kv_sigma, chunk_elems).astype(np.float32))
+    reps = -(-total // chunk_elems)
+    return np.tile(chunk, reps)[:total].view(np.uint8)
+
+
 def oracle_dtype(kv_dtype: int) -> int:
     return {qvp.DTYPE_F32: O.ORC_F32, qvp.DTYPE_BF16: O.ORC_BF16, qvp.DTYPE_F16: O.ORC_F16}[kv_dtype]
 

@@ -13,7 +13,7 @@ import pytest
 
 import qvp
 import workloads as W
-from helpers import F32_ABS_TOL, GpuRun, assert_close_16bit, assert_close_bf16, oracle_decode, to_f32
+from helpers import F32_ABS_TOL, GpuRun, assert_close_16bit, assert_close_bf16, oracle_decode, tiled_pool_image, to_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -91,6 +91,25 @@ def test_balanced_schedule_shapes(lens):
 def test_config3_subset_72b_shape():
     print("case: config3 shape, 2 sequences", flush=True)
     _parity(W.config3(num_seqs=2), out_dtypes=(qvp.DTYPE_F32,))
+
+
+@pytest.mark.parametrize("hkv", [16, 6])
+def test_kv_heads_side_by_side_on_long_contexts(hkv):
+    """With >= 32 tiles per resident wave the schedule decodes kv heads side by
+    side (4 per workgroup for 16 kv heads, 2 per workgroup and two tile lanes
+    each for 6): every long sequence is cut into many pieces, and a short
+    sequence in the middle stays a whole segment written directly."""
+    total_tokens = 65536 * 32 // hkv + 8192
+    rng = np.random.default_rng(hkv)
+    cuts = np.sort(rng.choice(np.arange(1, total_tokens), size=5, replace=False))
+    lens = list(np.diff(np.concatenate([[0], cuts, [total_tokens]])))
+    lens.insert(3, 100)
+    print(f"case: head groups hkv={hkv} lens={lens}", flush=True)
+    w = W.custom(lens, hkv, hkv, 128, seed=hkv, spare=0.02)
+    run = GpuRun(w, image=tiled_pool_image(w))
+    ref_out, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    assert_close_bf16(got, ref32, f"head groups hkv={hkv}")
 
 
 def test_repeated_decodes_are_bitwise_identical():
