@@ -243,6 +243,47 @@ int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads,
 int qvp_paged_decode(const qvp_decode_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Causal paged prefill (PagedAttention.h:43-44: paged_attention_decode<T>  */
+/* applied per prompt position p with context_len = p + 1)                  */
+/* ------------------------------------------------------------------------ */
+
+/* The new tokens of sequence b are positions q_start[b] .. seq_lens[b] - 1 of
+ * the packed batch (their K/V already written, e.g. by qvp_append_kv); their
+ * queries and outputs are rows cu_q[b] .. cu_q[b + 1] - 1, with cu_q the
+ * exclusive prefix sum of seq_lens[b] - q_start[b]. For each such position p
+ * and query head h, with g = h / (num_query_heads / num_kv_heads):
+ *   out[row(p)][h][:] = sum_{t <= p} w_t V[b][t][g][:] / sum_{t <= p} w_t,
+ *   w_t = exp(s_t - max s),  s_t = scale * <query[row(p)][h][:], K[b][t][g][:]>,
+ * i.e. exactly the decode of that position with context p + 1. */
+typedef struct qvp_prefill_args {
+    const void* query;          /* device, [total_new][num_query_heads][head_dim], kv_dtype */
+    void* out;                  /* device, [total_new][num_query_heads][head_dim], out_dtype */
+    const void* kv_base;        /* device address of frame 0 */
+    uint64_t block_stride;      /* bytes between frames */
+    const qvp_batch* batch;     /* packed by qvp_pack with the full context lengths */
+    const uint32_t* q_start;    /* host, [num_seqs]: first new position, < seq_lens[b] */
+    uint32_t kv_dtype;
+    uint32_t out_dtype;
+    uint32_t layer;
+    uint32_t num_layers;
+    uint32_t num_query_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t tokens_per_block;
+    uint64_t head_stride;       /* elements, KVBlockLayout::head_stride() */
+    uint64_t token_stride;      /* elements */
+    uint64_t stream_stride;     /* elements */
+    uint64_t layer_stride;      /* elements */
+    float scale;
+} qvp_prefill_args;
+
+/* Validates everything on the host (the decode's rules, plus q_start[b] <
+ * seq_lens[b]), then enqueues the prefill on `stream`. bf16 caches with
+ * head_dim 128 run the MFMA prefill kernel; other shapes run the decode
+ * kernels over one virtual sequence per new position. */
+int qvp_paged_prefill(const qvp_prefill_args* args, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Copy-on-write (MemoryAllocator::copy_block, src/MemoryAllocator.cpp:76-85)*/
 /* ------------------------------------------------------------------------ */
 

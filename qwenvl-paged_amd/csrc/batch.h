@@ -39,6 +39,19 @@ struct qvp_schedule {
     size_t device_cap{0};
 };
 
+// Work list of a causal prefill over one packed batch (rebuilt per call: the
+// first new position of each sequence is a call argument), and the private
+// per-position batch of the prefill's decode-kernel path.
+struct qvp_prefill_plan {
+    int32_t* staging{nullptr};
+    size_t staging_cap{0};  // int32 elements
+    hipEvent_t staging_done{nullptr};
+    bool staging_pending{false};
+    int32_t* device{nullptr};
+    size_t device_cap{0};
+    qvp_batch* virt{nullptr};
+};
+
 struct qvp_batch {
     int32_t* staging[2]{nullptr, nullptr};
     size_t staging_cap[2]{0, 0};  // in int32 elements
@@ -50,11 +63,16 @@ struct qvp_batch {
     bool valid{false};
     uint64_t generation{0};            // bumped by every successful pack
     std::vector<int32_t> host_seq_lens;  // host copy of seq_lens for scheduling
+    std::vector<uint32_t> host_ids;      // host copy of the needed block ids, CSR over host_cu_blocks
+    std::vector<uint32_t> host_cu_blocks;
     qvp_packed_view view{};
     qvp_schedule sched{};
+    qvp_prefill_plan prefill{};
 };
 
 namespace qvp {
 // Frees the schedule's buffers (called by qvp_batch_destroy).
 void destroy_schedule(qvp_schedule& s);
+// Frees the prefill plan's buffers and its private batch.
+void destroy_prefill_plan(qvp_prefill_plan& p);
 }  // namespace qvp

@@ -45,7 +45,7 @@
 //   as hi + lo (hi = P truncated to bf16, lo = P - hi rounded to bf16), which
 //   keeps the weights at about 2^-16 relative error. C register r of PV MFMA n
 //   in lane (c, j) is O[head c][dim 32j + 8r + n].
-#include "decode_common.h"
+#include "mfma_tile.h"
 
 #include <algorithm>
 #include <mutex>
@@ -56,7 +56,6 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kTileTokens = 32;
 constexpr int kD = 128;
 constexpr int kRowPad = kD + 4;
 constexpr int kWgsPerCu = 2;
@@ -83,12 +82,6 @@ struct MfmaArgs {
     int hps;        // kv heads per segment (4, 2 or 1)
 };
 
-struct KvTile {
-    u32x4 k[2][4];  // [half u][QK mfma i]
-    u32x4 v[8];     // [load q]
-};
-
-__device__ inline u32x4 load16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // The schedule and the block tables do not change while the kernel runs;
 // reading them through the constant address space lets the compiler use
@@ -184,110 +177,6 @@ __device__ inline void load_tile(const DecodeGeometry& p, const TileRef& r, int 
     }
 }
 
-// Reductions over the four lanes (c, 0..3) of one query head: lanes l, l^16,
-// l^32, l^48, through the gfx950 row/half swaps (VALU only, so they never wait
-// on LDS or scalar-memory counters).
-__device__ inline float max_over_j(float v) {
-    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-__device__ inline float sum_over_j(float v) {
-    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-// Workgroup barrier that orders LDS only: outstanding global loads (the next
-// tile) stay in flight across it.
-__device__ inline void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// One tile of online softmax + PV for the wave.
-__device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0, int ctx, float scale_log2,
-                                    int j, float& m_run, float& l_run, floatx4 (&o)[8]) {
-    float s[2][4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[u][i]),
-                                                          __builtin_bit_cast(bf16x8_t, qop[i]), acc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tok = tok0 + j + 16 * u + 4 * r;
-            s[u][r] = (tok < ctx) ? acc[r] * scale_log2 : -INFINITY;
-        }
-    }
-
-    // The four lanes (c, 0..3) of query head c share one running max.
-    float mt = s[0][0];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[u][r]);
-    mt = max_over_j(mt);
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-
-    float psum = 0.f;
-    uint32_t phi[4], plo[4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int r = 0; r < 4; r += 2) {
-            const float p0 = fast_exp2(s[u][r] - m_new);
-            const float p1 = fast_exp2(s[u][r + 1] - m_new);
-            psum += p0 + p1;
-            const uint32_t h0 = __float_as_uint(p0) >> 16;
-            const uint32_t h1 = __float_as_uint(p1) >> 16;
-            const uint32_t l0 = float_to_bf16_bits(p0 - __uint_as_float(h0 << 16));
-            const uint32_t l1 = float_to_bf16_bits(p1 - __uint_as_float(h1 << 16));
-            phi[2 * u + r / 2] = h0 | (h1 << 16);
-            plo[2 * u + r / 2] = l0 | (l1 << 16);
-        }
-    }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) o[n] *= alpha;
-
-    const u32x4 bhi = {phi[0], phi[1], phi[2], phi[3]};
-    const u32x4 blo = {plo[0], plo[1], plo[2], plo[3]};
-    // Values of tokens past the context are zeroed in place (their weights are
-    // 0, but the bytes read for them are not data and 0 * NaN would poison O).
-    // Only the last tile of a sequence has such tokens.
-    if (tok0 + kTileTokens > ctx) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            if (tok0 + 4 * q + j >= ctx) cur.v[q] = u32x4{0u, 0u, 0u, 0u};
-        }
-    }
-    const u32x4 (&v)[8] = cur.v;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-        const int w = n >> 1;
-        u32x4 a;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t x = v[2 * k][w];
-            const uint32_t y = v[2 * k + 1][w];
-            a[k] = (n & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-        }
-        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bhi), o[n], 0, 0, 0);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, blo), o[n], 0, 0, 0);
-    }
-}
-
 template <typename OutT>
 __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(DecodeGeometry p, MfmaArgs a) {
     __shared__ float sm_m[kWaves][16];
@@ -353,7 +242,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
             if (has2) load_tile(p, r2, c, j, nxt);
             has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
             if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
-            compute_tile(cur, qop, t * kTileTokens, ctx, p.scale_log2, j, m_run, l_run, o);
+            compute_tile(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
         }
 
         // This wave's state for (piece, head g) goes to LDS in row layout.

@@ -1,0 +1,136 @@
+// MFMA tile math shared by the paged decode and the paged prefill (bf16 K/V,
+// head_dim 128, v_mfma_f32_16x16x32_bf16; lane l = (c = l % 16, j = l / 16)).
+//
+// One tile is 32 tokens of one kv head against 16 query columns (the query
+// heads of a group in the decode, 16 query positions of one head in the
+// prefill). S^T = K Q^T is computed per 16-token half u: row r of half u
+// carries token (r / 4) + 16u + 4 (r % 4), so C register r of lane (c, j) is
+// the score of token j + 4 (4u + r) for column c. PV is O^T = V^T P^T with V
+// loaded coalesced (lane (c, j) of load q holds dims 8c .. 8c + 7 of token
+// 4q + j) and transposed in registers; P enters the bf16 MFMA as hi + lo
+// (hi = P truncated to bf16, lo = P - hi rounded to bf16), which keeps the
+// weights at about 2^-16 relative error. C register r of PV MFMA n in lane
+// (c, j) is O[column c][dim 32j + 8r + n].
+#pragma once
+
+#include "decode_common.h"
+
+namespace qvp {
+
+constexpr int kTileTokens = 32;
+
+struct KvTile {
+    u32x4 k[2][4];  // [half u][QK mfma i]
+    u32x4 v[8];     // [load q]
+};
+
+__device__ inline u32x4 load16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// Reductions over the four lanes (c, 0..3) of one query head: lanes l, l^16,
+// l^32, l^48, through the gfx950 row/half swaps (VALU only, so they never wait
+// on LDS or scalar-memory counters).
+__device__ inline float max_over_j(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ inline float sum_over_j(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Workgroup barrier that orders LDS only: outstanding global loads (the next
+// tile) stay in flight across it.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One tile of online softmax + PV for the wave. Column c (this lane's c)
+// sees tokens t <= col_last; values of tokens at or past v_end are zeroed in
+// place (their weights are 0, but the bytes read for them are not data and
+// 0 * NaN would poison O).
+__device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0, int col_last, int v_end,
+                                    float scale_log2, int j, float& m_run, float& l_run, floatx4 (&o)[8]) {
+    float s[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[u][i]),
+                                                          __builtin_bit_cast(bf16x8_t, qop[i]), acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tok = tok0 + j + 16 * u + 4 * r;
+            s[u][r] = (tok <= col_last) ? acc[r] * scale_log2 : -INFINITY;
+        }
+    }
+
+    // The four lanes (c, 0..3) of query head c share one running max.
+    float mt = s[0][0];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[u][r]);
+    mt = max_over_j(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+
+    float psum = 0.f;
+    uint32_t phi[4], plo[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+            const float p0 = fast_exp2(s[u][r] - m_new);
+            const float p1 = fast_exp2(s[u][r + 1] - m_new);
+            psum += p0 + p1;
+            const uint32_t h0 = __float_as_uint(p0) >> 16;
+            const uint32_t h1 = __float_as_uint(p1) >> 16;
+            const uint32_t l0 = float_to_bf16_bits(p0 - __uint_as_float(h0 << 16));
+            const uint32_t l1 = float_to_bf16_bits(p1 - __uint_as_float(h1 << 16));
+            phi[2 * u + r / 2] = h0 | (h1 << 16);
+            plo[2 * u + r / 2] = l0 | (l1 << 16);
+        }
+    }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[n] *= alpha;
+
+    const u32x4 bhi = {phi[0], phi[1], phi[2], phi[3]};
+    const u32x4 blo = {plo[0], plo[1], plo[2], plo[3]};
+    // Values of tokens past the context are zeroed in place (their weights are
+    // 0, but the bytes read for them are not data and 0 * NaN would poison O).
+    // Only the last tile of a sequence has such tokens.
+    if (tok0 + kTileTokens > v_end) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (tok0 + 4 * q + j >= v_end) cur.v[q] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    const u32x4 (&v)[8] = cur.v;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const int w = n >> 1;
+        u32x4 a;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t x = v[2 * k][w];
+            const uint32_t y = v[2 * k + 1][w];
+            a[k] = (n & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
+        }
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bhi), o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, blo), o[n], 0, 0, 0);
+    }
+}
+
+}  // namespace qvp

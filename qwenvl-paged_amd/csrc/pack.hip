@@ -85,6 +85,7 @@ int qvp_batch_destroy(qvp_batch* batch) {
         status = fail(QVP_ERR_DEVICE, "hipFree(batch)");
     }
     qvp::destroy_schedule(batch->sched);
+    qvp::destroy_prefill_plan(batch->prefill);
     delete batch;
     return status;
 }
@@ -244,6 +245,13 @@ int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
     v.max_seq_len = max_len;
     v.total_tokens = total_tokens;
     batch->host_seq_lens.assign(seq_lens, seq_lens + num_seqs);
+    batch->host_ids.clear();
+    batch->host_cu_blocks.assign(1, 0);
+    for (uint32_t b = 0; b < num_seqs; ++b) {
+        const uint32_t needed = (context_lens[b] + tokens_per_block - 1) / tokens_per_block;
+        batch->host_ids.insert(batch->host_ids.end(), block_ids + cu_blocks[b], block_ids + cu_blocks[b] + needed);
+        batch->host_cu_blocks.push_back(static_cast<uint32_t>(batch->host_ids.size()));
+    }
     batch->generation += 1;
     batch->valid = true;
     return QVP_OK;

@@ -1,0 +1,375 @@
+// qvp_paged_prefill: causal attention of a step's new tokens over the paged
+// cache. The reference defines prefill as paged_attention_decode<T> applied per
+// prompt position p with context_len = p + 1 (include/qwenvl_paged/
+// PagedAttention.h:43-44; tests/EndToEnd.test.cpp:252-256), so every output
+// row here is the decode of its position.
+//
+// MFMA path (bf16 cache, head_dim 128, GQA group <= 16, power-of-two
+// tokens_per_block >= 16). A work item is (sequence b, kv head g, 16 new
+// positions p0 .. p0 + 15, up to 8 query heads of g's group). Its workgroup
+// streams tokens [0, p0 + 16) of kv head g in 32-token tiles: each tile is
+// loaded once, by all 256 threads, into an LDS double buffer (rows padded to
+// 272 bytes so the fragment reads spread over the banks), and every wave runs
+// the decode's tile math (mfma_tile.h) for its query heads with the 16
+// positions in the MFMA columns, column c seeing tokens t <= p0 + c. A wave
+// therefore covers the whole causal context of its queries: no split, no
+// merge. Items are launched longest context first so the short ones fill the
+// tail. Each K/V tile feeds 16 positions x up to 8 heads from LDS.
+//
+// Decode path (any other shape): one virtual sequence per new position (same
+// frames, context p + 1), packed into a private batch and run through
+// qvp_paged_decode, whose query and output rows are exactly the prefill's.
+#include "mfma_tile.h"
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+namespace qvp {
+namespace {
+
+constexpr int kPrefillWaves = 4;
+constexpr int kPrefillThreads = kPrefillWaves * 64;
+constexpr int kPrefillPositions = 16;     // MFMA columns
+constexpr int kPrefillHeadsPerItem = 8;   // two query heads per wave
+constexpr int kHeadBytes = 256;           // 128 bf16
+constexpr int kLdsRow = kHeadBytes + 16;  // padded LDS row of one token
+
+struct PrefillItem {
+    int32_t b;     // sequence
+    int32_t g;     // kv head
+    int32_t p0;    // first position of the block
+    int32_t np;    // positions in the block, 1 .. 16
+    int32_t row0;  // query / output row of p0
+    int32_t h0;    // first query head of the group handled by the item
+};
+static_assert(sizeof(PrefillItem) == 6 * sizeof(int32_t), "PrefillItem is six int32");
+
+template <typename T>
+__device__ inline const __attribute__((address_space(4))) T* as_const(const T* ptr) {
+    return (const __attribute__((address_space(4))) T*)(ptr);
+}
+
+__device__ inline u32x4 lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+template <typename OutT>
+__global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometry p, const PrefillItem* items,
+                                                                    void* out_ptr) {
+    __shared__ __attribute__((aligned(16))) uint8_t sm_kv[2][2][kTileTokens][kLdsRow];
+
+    const auto* itp = as_const(items) + blockIdx.x;
+    const int b = itp->b;
+    const int g = itp->g;
+    const int p0 = itp->p0;
+    const int np = itp->np;
+    const int row0 = itp->row0;
+    const int h0 = itp->h0;
+
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15;
+    const int j = lane >> 4;
+    const int G = static_cast<int>(p.group);
+    const int nh = min(G - h0, kPrefillHeadsPerItem);
+    // This wave's query heads (within the group): h0 + wave and h0 + wave + 4.
+    const bool has_a = wave < nh;
+    const bool has_b = wave + kPrefillWaves < nh;
+    const int ctx_end = p0 + np;
+    const int ntiles = (ctx_end + kTileTokens - 1) / kTileTokens;
+
+    // Column c is position p0 + c; columns past the block repeat its last
+    // position (valid data, never written).
+    const int cc = min(c, np - 1);
+    const int col_last = p0 + cc;
+    const uint16_t* qrow = static_cast<const uint16_t*>(p.query) +
+                           (static_cast<uint64_t>(row0 + cc) * p.num_q_heads + static_cast<uint64_t>(g) * G) * 128;
+    u32x4 qa[4], qb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        qa[i] = *reinterpret_cast<const u32x4*>(qrow + (h0 + min(wave, nh - 1)) * 128 + 32 * i + 8 * j);
+        qb[i] = *reinterpret_cast<const u32x4*>(qrow + (h0 + min(wave + kPrefillWaves, nh - 1)) * 128 + 32 * i + 8 * j);
+    }
+    floatx4 oa[8], ob[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        oa[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+        ob[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    float ma = -INFINITY, la = 0.f, mb = -INFINITY, lb = 0.f;
+
+    // Cooperative tile loads: thread t moves 16-byte chunks x and x + 8 (x =
+    // t % 8) of the K row and of the V row of token t / 8 of the tile.
+    const int lrow = threadIdx.x >> 3;
+    const int lx = threadIdx.x & 7;
+    const int32_t* table = p.tables + static_cast<uint64_t>(b) * p.max_nb;
+    auto load_regs = [&](int tile, u32x4 (&r)[4]) {
+        const int tok = tile * kTileTokens + lrow;
+        if (tok < ctx_end) {
+            const int32_t blk = table[tok >> p.tpb_shift];
+            const uint8_t* base = p.kv_base + static_cast<uint64_t>(blk) * p.block_stride +
+                                  static_cast<uint64_t>(tok & (p.tpb - 1)) * p.token_stride +
+                                  static_cast<uint64_t>(g) * p.head_stride;
+            r[0] = load16(base + p.k_off + 16 * lx);
+            r[1] = load16(base + p.k_off + 16 * (lx + 8));
+            r[2] = load16(base + p.v_off + 16 * lx);
+            r[3] = load16(base + p.v_off + 16 * (lx + 8));
+        } else {
+            // Rows past the context are zeros: their weights are 0 and 0 * 0
+            // keeps O clean.
+            r[0] = r[1] = r[2] = r[3] = u32x4{0u, 0u, 0u, 0u};
+        }
+    };
+    auto store_lds = [&](int buf, const u32x4 (&r)[4]) {
+        *reinterpret_cast<u32x4*>(&sm_kv[buf][0][lrow][16 * lx]) = r[0];
+        *reinterpret_cast<u32x4*>(&sm_kv[buf][0][lrow][16 * (lx + 8)]) = r[1];
+        *reinterpret_cast<u32x4*>(&sm_kv[buf][1][lrow][16 * lx]) = r[2];
+        *reinterpret_cast<u32x4*>(&sm_kv[buf][1][lrow][16 * (lx + 8)]) = r[3];
+    };
+
+    u32x4 regs[4];
+    load_regs(0, regs);
+    store_lds(0, regs);
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+        const int buf = t & 1;
+        const bool more = t + 1 < ntiles;
+        if (more) load_regs(t + 1, regs);  // in flight while this tile is computed
+        KvTile tile;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                tile.k[u][i] = lds16(&sm_kv[buf][0][16 * u + (c >> 2) + 4 * (c & 3)][16 * j + 64 * i]);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) tile.v[q] = lds16(&sm_kv[buf][1][4 * q + j][16 * c]);
+        if (has_a) compute_tile(tile, qa, t * kTileTokens, col_last, ctx_end, p.scale_log2, j, ma, la, oa);
+        if (has_b) compute_tile(tile, qb, t * kTileTokens, col_last, ctx_end, p.scale_log2, j, mb, lb, ob);
+        if (more) store_lds(buf ^ 1, regs);
+        // Tile t + 1 is visible, and every wave is done with buffer `buf`
+        // before the next iteration refills it.
+        __syncthreads();
+    }
+
+    OutT* out = static_cast<OutT*>(out_ptr);
+    auto write = [&](int hq, const floatx4 (&o)[8], float l) {
+        if (c >= np) return;
+        OutT* dst = out + (static_cast<uint64_t>(row0 + c) * p.num_q_heads + static_cast<uint64_t>(g) * G + hq) * 128;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int n = 0; n < 8; ++n) dst[32 * j + 8 * r + n] = from_float<OutT>(o[n][r] / l);
+    };
+    la = sum_over_j(la);
+    lb = sum_over_j(lb);
+    if (has_a) write(h0 + wave, oa, la);
+    if (has_b) write(h0 + wave + kPrefillWaves, ob, lb);
+}
+
+bool prefill_mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr, uintptr_t kv_base_addr) {
+    const bool pow2 = g.tpb != 0 && (g.tpb & (g.tpb - 1)) == 0;
+    const bool aligned = (g.block_stride % 16 == 0) && (g.k_off % 16 == 0) && (g.v_off % 16 == 0) &&
+                         (g.token_stride % 16 == 0) && (g.head_stride % 16 == 0) && (kv_base_addr % 16 == 0) &&
+                         (query_addr % 16 == 0);
+    return kv_dtype == QVP_DTYPE_BF16 && g.head_dim == 128 && g.group >= 1 && g.group <= 16 && pow2 && g.tpb >= 16 &&
+           aligned;
+}
+
+uint32_t log2_u32(uint32_t x) {
+    uint32_t r = 0;
+    while ((1u << r) < x) ++r;
+    return r;
+}
+
+}  // namespace
+
+void destroy_prefill_plan(qvp_prefill_plan& p) {
+    if (p.staging_pending) (void)hipEventSynchronize(p.staging_done);
+    if (p.staging != nullptr) (void)hipHostFree(p.staging);
+    if (p.staging_done != nullptr) (void)hipEventDestroy(p.staging_done);
+    if (p.device != nullptr) (void)hipFree(p.device);
+    if (p.virt != nullptr) (void)qvp_batch_destroy(p.virt);
+    p = qvp_prefill_plan{};
+}
+
+}  // namespace qvp
+
+extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
+    using qvp::fail;
+    if (a == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "args is NULL");
+    qvp_packed_view v{};
+    QVP_TRY(qvp_batch_view(a->batch, &v));
+    qvp_batch* batch = const_cast<qvp_batch*>(a->batch);
+    if (a->query == nullptr || a->out == nullptr || a->kv_base == nullptr) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "query, out or kv_base is NULL");
+    }
+    if (v.num_seqs > 0 && a->q_start == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "q_start is NULL");
+    const size_t esz = qvp::dtype_size(a->kv_dtype);
+    const size_t osz = qvp::dtype_size(a->out_dtype);
+    if (esz == 0 || osz == 0) return fail(QVP_ERR_INVALID_ARGUMENT, "unknown dtype");
+    if (a->num_query_heads == 0 || a->num_kv_heads == 0 || a->num_query_heads % a->num_kv_heads != 0) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "%u query heads do not group onto %u kv heads", a->num_query_heads,
+                    a->num_kv_heads);
+    }
+    if (a->layer >= a->num_layers) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "layer %u outside %u layers", a->layer, a->num_layers);
+    }
+    if (a->head_dim == 0) return fail(QVP_ERR_INVALID_ARGUMENT, "head_dim is 0");
+    if (a->tokens_per_block != v.tokens_per_block) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "batch packed for %u tokens per block, args say %u", v.tokens_per_block,
+                    a->tokens_per_block);
+    }
+    if (a->head_stride < a->head_dim || a->token_stride == 0) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "head vectors overlap");
+    }
+    const uint64_t last_elem = static_cast<uint64_t>(a->num_layers - 1) * a->layer_stride + a->stream_stride +
+                               static_cast<uint64_t>(a->tokens_per_block - 1) * a->token_stride +
+                               static_cast<uint64_t>(a->num_kv_heads - 1) * a->head_stride + a->head_dim;
+    if (last_elem * esz > a->block_stride) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "layout addresses %llu bytes but frames are %llu bytes",
+                    static_cast<unsigned long long>(last_elem * esz),
+                    static_cast<unsigned long long>(a->block_stride));
+    }
+    const std::vector<int32_t>& lens = batch->host_seq_lens;
+    uint64_t total_new = 0;
+    for (uint32_t s = 0; s < v.num_seqs; ++s) {
+        if (a->q_start[s] >= static_cast<uint32_t>(lens[s])) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "sequence %u: first new position %u is not below its context %d", s,
+                        a->q_start[s], lens[s]);
+        }
+        total_new += static_cast<uint32_t>(lens[s]) - a->q_start[s];
+    }
+    if (total_new > 0x7fffffffu) return fail(QVP_ERR_INVALID_ARGUMENT, "too many new tokens");
+    if (v.num_seqs == 0) return QVP_OK;
+
+    qvp::DecodeGeometry g{};
+    g.kv_base = static_cast<const uint8_t*>(a->kv_base);
+    g.block_stride = a->block_stride;
+    g.k_off = static_cast<uint64_t>(a->layer) * a->layer_stride * esz;
+    g.v_off = g.k_off + a->stream_stride * esz;
+    g.token_stride = a->token_stride * esz;
+    g.head_stride = a->head_stride * esz;
+    g.tables = v.block_tables;
+    g.seq_lens = v.seq_lens;
+    g.query = a->query;
+    g.max_nb = v.max_blocks_per_seq;
+    g.tpb = a->tokens_per_block;
+    g.tpb_shift = qvp::log2_u32(a->tokens_per_block);
+    g.num_q_heads = a->num_query_heads;
+    g.num_kv_heads = a->num_kv_heads;
+    g.group = a->num_query_heads / a->num_kv_heads;
+    g.head_dim = a->head_dim;
+    g.scale_log2 = a->scale * qvp::kLog2e;
+    hipStream_t s = qvp::as_stream(stream);
+    qvp_prefill_plan& plan = batch->prefill;
+
+    if (!qvp::prefill_mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
+                                     reinterpret_cast<uintptr_t>(a->kv_base))) {
+        // One virtual sequence per new position, over the same frames.
+        std::vector<uint32_t> ids, cu{0}, ctx;
+        ids.reserve(batch->host_ids.size());
+        for (uint32_t sq = 0; sq < v.num_seqs; ++sq) {
+            const uint32_t* row = batch->host_ids.data() + batch->host_cu_blocks[sq];
+            for (uint32_t pos = a->q_start[sq]; pos < static_cast<uint32_t>(lens[sq]); ++pos) {
+                const uint32_t nb = (pos + a->tokens_per_block) / a->tokens_per_block;
+                ids.insert(ids.end(), row, row + nb);
+                cu.push_back(static_cast<uint32_t>(ids.size()));
+                ctx.push_back(pos + 1);
+            }
+        }
+        if (plan.virt == nullptr) QVP_TRY(qvp_batch_create(&plan.virt));
+        QVP_TRY(qvp_pack(plan.virt, static_cast<uint32_t>(ctx.size()), ids.data(), cu.data(), ctx.data(),
+                         a->tokens_per_block, v.num_pool_blocks, v.split_tokens, stream));
+        qvp_decode_args d{};
+        d.query = a->query;
+        d.out = a->out;
+        d.kv_base = a->kv_base;
+        d.block_stride = a->block_stride;
+        d.batch = plan.virt;
+        d.kv_dtype = a->kv_dtype;
+        d.out_dtype = a->out_dtype;
+        d.layer = a->layer;
+        d.num_layers = a->num_layers;
+        d.num_query_heads = a->num_query_heads;
+        d.num_kv_heads = a->num_kv_heads;
+        d.head_dim = a->head_dim;
+        d.tokens_per_block = a->tokens_per_block;
+        d.head_stride = a->head_stride;
+        d.token_stride = a->token_stride;
+        d.stream_stride = a->stream_stride;
+        d.layer_stride = a->layer_stride;
+        d.scale = a->scale;
+        return qvp_paged_decode(&d, stream);
+    }
+
+    // Work items, longest context first.
+    const uint32_t G = g.group;
+    const uint32_t head_sets = (G + qvp::kPrefillHeadsPerItem - 1) / qvp::kPrefillHeadsPerItem;
+    std::vector<qvp::PrefillItem> items;
+    uint32_t row = 0;
+    for (uint32_t sq = 0; sq < v.num_seqs; ++sq) {
+        const uint32_t start = a->q_start[sq];
+        const uint32_t end = static_cast<uint32_t>(lens[sq]);
+        for (uint32_t p0 = start; p0 < end; p0 += qvp::kPrefillPositions) {
+            const uint32_t np = std::min<uint32_t>(qvp::kPrefillPositions, end - p0);
+            for (uint32_t kv = 0; kv < a->num_kv_heads; ++kv) {
+                for (uint32_t hs = 0; hs < head_sets; ++hs) {
+                    items.push_back(qvp::PrefillItem{static_cast<int32_t>(sq), static_cast<int32_t>(kv),
+                                                     static_cast<int32_t>(p0), static_cast<int32_t>(np),
+                                                     static_cast<int32_t>(row + (p0 - start)),
+                                                     static_cast<int32_t>(hs * qvp::kPrefillHeadsPerItem)});
+                }
+            }
+        }
+        row += end - start;
+    }
+    std::stable_sort(items.begin(), items.end(), [](const qvp::PrefillItem& x, const qvp::PrefillItem& y) {
+        return x.p0 + x.np > y.p0 + y.np;
+    });
+    if (items.size() > 0x7fffffffu) return fail(QVP_ERR_INVALID_ARGUMENT, "too many prefill items");
+    const size_t ints = items.size() * (sizeof(qvp::PrefillItem) / sizeof(int32_t));
+    if (plan.staging_done == nullptr) QVP_HIP(hipEventCreateWithFlags(&plan.staging_done, hipEventDisableTiming));
+    if (plan.staging_pending) {
+        QVP_HIP(hipEventSynchronize(plan.staging_done));
+        plan.staging_pending = false;
+    }
+    if (plan.staging_cap < ints) {
+        if (plan.staging != nullptr) QVP_HIP(hipHostFree(plan.staging));
+        plan.staging = nullptr;
+        plan.staging_cap = 0;
+        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&plan.staging), ints * sizeof(int32_t), hipHostMallocDefault));
+        plan.staging_cap = ints;
+    }
+    if (plan.device_cap < ints) {
+        // The device list may still be read by an earlier prefill on this batch.
+        if (plan.device != nullptr) {
+            QVP_HIP(hipStreamSynchronize(s));
+            QVP_HIP(hipFree(plan.device));
+        }
+        plan.device = nullptr;
+        plan.device_cap = 0;
+        QVP_HIP(hipMalloc(reinterpret_cast<void**>(&plan.device), ints * sizeof(int32_t)));
+        plan.device_cap = ints;
+    }
+    std::memcpy(plan.staging, items.data(), ints * sizeof(int32_t));
+    QVP_HIP(hipMemcpyAsync(plan.device, plan.staging, ints * sizeof(int32_t), hipMemcpyHostToDevice, s));
+    QVP_HIP(hipEventRecord(plan.staging_done, s));
+    plan.staging_pending = true;
+
+    const auto* dev_items = reinterpret_cast<const qvp::PrefillItem*>(plan.device);
+    const dim3 grid(static_cast<unsigned>(items.size()));
+    switch (a->out_dtype) {
+        case QVP_DTYPE_F32:
+            hipLaunchKernelGGL(qvp::prefill_mfma<float>, grid, dim3(qvp::kPrefillThreads), 0, s, g, dev_items, a->out);
+            break;
+        case QVP_DTYPE_BF16:
+            hipLaunchKernelGGL(qvp::prefill_mfma<uint16_t>, grid, dim3(qvp::kPrefillThreads), 0, s, g, dev_items,
+                               a->out);
+            break;
+        default:
+            hipLaunchKernelGGL(qvp::prefill_mfma<_Float16>, grid, dim3(qvp::kPrefillThreads), 0, s, g, dev_items,
+                               a->out);
+            break;
+    }
+    QVP_HIP(hipGetLastError());
+    return QVP_OK;
+}

@@ -82,6 +82,30 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("query", c_void_p),
+        ("out", c_void_p),
+        ("kv_base", c_void_p),
+        ("block_stride", c_uint64),
+        ("batch", c_void_p),
+        ("q_start", POINTER(c_uint32)),
+        ("kv_dtype", c_uint32),
+        ("out_dtype", c_uint32),
+        ("layer", c_uint32),
+        ("num_layers", c_uint32),
+        ("num_query_heads", c_uint32),
+        ("num_kv_heads", c_uint32),
+        ("head_dim", c_uint32),
+        ("tokens_per_block", c_uint32),
+        ("head_stride", c_uint64),
+        ("token_stride", c_uint64),
+        ("stream_stride", c_uint64),
+        ("layer_stride", c_uint64),
+        ("scale", c_float),
+    ]
+
+
 class AppendArgs(ctypes.Structure):
     _fields_ = [
         ("kv_base", c_void_p),
@@ -157,6 +181,7 @@ SIGNATURES = {
         [c_void_p, c_uint64, c_uint32, _u32p, _u64p, c_uint32, c_void_p, c_uint64, c_uint64, c_void_p],
     ),
     "qvp_append_kv": (c_int, [POINTER(AppendArgs), _u32p, _u32p, c_uint32, c_void_p]),
+    "qvp_paged_prefill": (c_int, [POINTER(PrefillArgs), c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -532,3 +557,20 @@ def append_kv(args: AppendArgs, frames, slots, stream=None) -> None:
     if len(f_a) != len(s_a):
         raise ValueError("frames and slots differ in length")
     check(load().qvp_append_kv(byref(args), f_p, s_p, len(f_a), _sp(stream)))
+
+
+def prefill_args(*, query: int, out: int, kv_base: int, block_stride: int, batch: "Batch", q_start, kv_dtype: int,
+                 out_dtype: int, layer: int, num_layers: int, num_query_heads: int, num_kv_heads: int, head_dim: int,
+                 tokens_per_block: int, scale: float, strides: dict | None = None) -> PrefillArgs:
+    """Arguments of qvp_paged_prefill; keeps the q_start array alive on the returned object."""
+    s = strides or layout_strides(tokens_per_block, num_layers, num_kv_heads, head_dim)
+    qs, qs_p = _u32(q_start)
+    a = PrefillArgs(query, out, kv_base, block_stride, batch.handle, qs_p, kv_dtype, out_dtype, layer, num_layers,
+                    num_query_heads, num_kv_heads, head_dim, tokens_per_block, s["head_stride"], s["token_stride"],
+                    s["stream_stride"], s["layer_stride"], scale)
+    a._q_start = qs
+    return a
+
+
+def paged_prefill(args: PrefillArgs, stream=None) -> None:
+    check(load().qvp_paged_prefill(byref(args), _sp(stream)))
