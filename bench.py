@@ -20,9 +20,10 @@ the same batch, single-threaded like the reference engine loop.
 
 Other lines (not the headline): --workload config3 (Qwen2-VL-72B layer, B=32,
 ctx U[8192, 32768]), --cow (copy-on-write configuration, C++ driver),
---trace (continuous-batching trace, C++ driver) and --append (the K/V append
-of one config2 step, one layer and all 28 layers) each print their own JSON
-line.
+--trace (continuous-batching trace, C++ driver), --append (the K/V append
+of one config2 step, one layer and all 28 layers) and --prefill (causal
+prefill of 4 x 2048-token prompts at the Qwen2-VL-7B shape, against the MFMA
+peak) each print their own JSON line.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -212,6 +213,49 @@ def append_case(name: str, w: W.Workload, num_layers: int, first_layer: int, lay
             "GBps_gpu": round(moved / (gpu_us * 1e-6) / 1e9, 1)}
 
 
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def prefill_bench(steps: int, warmup: int) -> int:
+    """Causal prefill of B prompts (all positions new) at the Qwen2-VL-7B layer
+    shape. Useful flops: 4 * Hq * D * sum over positions of (p + 1) (QK^T and
+    PV, causal)."""
+    lens = [2048, 2048, 2048, 2048]
+    w = W.custom(lens, 28, 4, 128, seed=5, spare=0.05)
+    pool = qvp.BlockPool(w.num_pool_blocks, w.block_bytes)
+    rng = np.random.default_rng(5)
+    chunk = W.f32_to_bf16_bits(rng.normal(0, 0.5, 1 << 22).astype(np.float32)).view(np.uint8)
+    pool.upload_all(np.resize(chunk, w.num_pool_blocks * pool.stride))
+    total = int(w.context_lens.sum())
+    q = qvp.DeviceBuffer.from_array(W.f32_to_bf16_bits(rng.normal(0, 1, (total, 28, 128)).astype(np.float32)))
+    out = qvp.DeviceBuffer(total * 28 * 128 * 2)
+    stream = qvp.Stream()
+    batch = qvp.Batch()
+    batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks, 512, stream)
+    args = qvp.prefill_args(query=q.ptr, out=out.ptr, kv_base=pool.base, block_stride=pool.stride, batch=batch,
+                            q_start=np.zeros(len(lens), np.uint32), kv_dtype=qvp.DTYPE_BF16,
+                            out_dtype=qvp.DTYPE_BF16, layer=0, num_layers=1, num_query_heads=28, num_kv_heads=4,
+                            head_dim=128, tokens_per_block=16, scale=w.scale)
+    for _ in range(warmup):
+        qvp.paged_prefill(args, stream)
+    stream.synchronize()
+    e0, e1 = qvp.Event(), qvp.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        qvp.paged_prefill(args, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    flops = 4.0 * 28 * 128 * sum(n * (n + 1) / 2 for n in lens)
+    tflops = flops / (ms * 1e-3) / 1e12
+    print(json.dumps({"mode": "prefill", "kernel": "prefill_mfma", "workload": "4 x 2048-token prompts, Hq28/Hkv4/D128 "
+                      "bf16, block 16, one layer", "steps": steps, "ms_per_prefill": round(ms, 4),
+                      "useful_flops": flops, "tokens_per_s": round(total / (ms * 1e-3), 1),
+                      "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}}))
+    return 0
+
+
 def append_bench(steps: int, warmup: int) -> int:
     w = W.config2()
     cases = [append_case("config2 step, one layer", w, 1, 0, 1, steps, warmup),
@@ -234,6 +278,7 @@ def main() -> int:
     ap.add_argument("--cow", action="store_true", help="run the copy-on-write configuration driver")
     ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
     ap.add_argument("--append", action="store_true", help="time the K/V append of one config2 step")
+    ap.add_argument("--prefill", action="store_true", help="time the causal prefill of 4 x 2048-token prompts")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
                          "used to scale rocprof FETCH_SIZE / WRITE_SIZE)")
@@ -242,6 +287,8 @@ def main() -> int:
         return copy_calibration(args.steps)
     if args.append:
         return append_bench(args.steps, args.warmup)
+    if args.prefill:
+        return prefill_bench(args.steps, args.warmup)
     if args.cow or args.trace:
         return run_driver("cow_bench" if args.cow else "trace_bench")
 

@@ -133,4 +133,81 @@ __device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0
     }
 }
 
+// Pieces of the tile step for callers that stage K and V themselves (the
+// prefill reads V already transposed from LDS and runs several query tiles
+// per K/V tile).
+
+// S^T of one tile per 16-token half u (C layout as above).
+__device__ inline void qk_tile(const u32x4 (&k)[2][4], const u32x4 (&qop)[4], floatx4 (&acc)[2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        floatx4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, k[u][i]),
+                                                        __builtin_bit_cast(bf16x8_t, qop[i]), a, 0, 0, 0);
+        }
+        acc[u] = a;
+    }
+}
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Online-softmax update of one tile for column c of this lane. Scores count
+// for tokens <= lim (pass INT_MAX when every token of the tile counts); the
+// running maximum m is kept in scaled base-2 units, so with scale_log2 > 0 the
+// maximum is taken on the raw scores and each weight is one fma and one exp2.
+// The running (l, O) are rescaled (skipped when no column's maximum moved: the
+// factor is then exactly 1), and P is returned as the hi and lo bf16 B
+// operands of the PV MFMAs (lo = P - hi, rounded to nearest even).
+__device__ inline void softmax_tile(const floatx4 (&acc)[2], int tok0, int lim, float scale_log2, int j,
+                                    float& m_run, float& l_run, floatx4 (&o)[8], u32x4& bhi, u32x4& blo) {
+    float s[2][4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[u][r] = (tok0 + j + 16 * u + 4 * r <= lim) ? acc[u][r] : -INFINITY;
+    float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    mt = max_over_j(mt) * scale_log2;
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    uint32_t phi[4], plo[4];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+            const float p0 = fast_exp2(fmaf(s[u][r], scale_log2, -m_new));
+            const float p1 = fast_exp2(fmaf(s[u][r + 1], scale_log2, -m_new));
+            psum += p0 + p1;
+            const uint32_t t0 = __float_as_uint(p0) & 0xffff0000u;
+            const uint32_t t1 = __float_as_uint(p1) & 0xffff0000u;
+            const bf16x2_t lo = {static_cast<__bf16>(p0 - __uint_as_float(t0)),
+                                 static_cast<__bf16>(p1 - __uint_as_float(t1))};
+            phi[2 * u + r / 2] = (t0 >> 16) | t1;
+            plo[2 * u + r / 2] = __builtin_bit_cast(uint32_t, lo);
+        }
+    }
+    l_run = l_run * alpha + psum;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[n] *= alpha;
+    }
+    bhi = u32x4{phi[0], phi[1], phi[2], phi[3]};
+    blo = u32x4{plo[0], plo[1], plo[2], plo[3]};
+}
+
+// O^T += V^T P^T, the A operand of MFMA n given: a[n] in lane (x, j) holds
+// V[tokens j + 4q, q = 0..7][dim 8x + n].
+__device__ inline void pv_tile(const u32x4 (&a)[8], const u32x4& bhi, const u32x4& blo, floatx4 (&o)[8]) {
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a[n]);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bhi), o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, blo), o[n], 0, 0, 0);
+    }
+}
+
 }  // namespace qvp

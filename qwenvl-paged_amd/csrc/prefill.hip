@@ -8,10 +8,12 @@
 // tokens_per_block >= 16). A work item is (sequence b, kv head g, 16 new
 // positions p0 .. p0 + 15, up to 8 query heads of g's group). Its workgroup
 // streams tokens [0, p0 + 16) of kv head g in 32-token tiles: each tile is
-// loaded once, by all 256 threads, into an LDS double buffer (rows padded to
-// 272 bytes so the fragment reads spread over the banks), and every wave runs
-// the decode's tile math (mfma_tile.h) for its query heads with the 16
-// positions in the MFMA columns, column c seeing tokens t <= p0 + c. A wave
+// loaded once, by all 256 threads, two tiles ahead of its use, into an LDS
+// double buffer holding K rows (padded to 272 bytes so the fragment reads
+// spread over the banks) and V transposed (so the PV operands need no
+// register transpose), and every wave runs the tile math of mfma_tile.h for
+// its query heads with the 16 positions in the MFMA columns, column c seeing
+// tokens t <= p0 + c (masks only on tiles that reach p0). A wave
 // therefore covers the whole causal context of its queries: no split, no
 // merge. Items are launched longest context first so the short ones fill the
 // tail. Each K/V tile feeds 16 positions x up to 8 heads from LDS.
@@ -22,6 +24,7 @@
 #include "mfma_tile.h"
 
 #include <algorithm>
+#include <climits>
 #include <cstring>
 #include <vector>
 
@@ -33,7 +36,17 @@ constexpr int kPrefillThreads = kPrefillWaves * 64;
 constexpr int kPrefillPositions = 16;     // MFMA columns
 constexpr int kPrefillHeadsPerItem = 8;   // two query heads per wave
 constexpr int kHeadBytes = 256;           // 128 bf16
-constexpr int kLdsRow = kHeadBytes + 16;  // padded LDS row of one token
+constexpr int kLdsRow = kHeadBytes + 16;  // padded LDS row of one token's K
+constexpr int kVtRow = 64 + 16;           // padded LDS row of one dim of V^T (32 tokens)
+
+// One K/V tile in LDS: K rows as in the frame (token-major), V transposed
+// (dim-major) so each PV operand is one 16-byte read. V^T row n * 16 + x
+// holds dim 8x + n; within a row, element 8 (t % 4) + t / 4 holds token t
+// (the k order of the PV MFMAs' P operand).
+struct PrefillTile {
+    uint8_t k[kTileTokens][kLdsRow];
+    uint8_t vt[128][kVtRow];
+};
 
 struct PrefillItem {
     int32_t b;     // sequence
@@ -55,7 +68,7 @@ __device__ inline u32x4 lds16(const uint8_t* p) { return *reinterpret_cast<const
 template <typename OutT>
 __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometry p, const PrefillItem* items,
                                                                     void* out_ptr) {
-    __shared__ __attribute__((aligned(16))) uint8_t sm_kv[2][2][kTileTokens][kLdsRow];
+    __shared__ __attribute__((aligned(16))) PrefillTile sm[2];
 
     const auto* itp = as_const(items) + blockIdx.x;
     const int b = itp->b;
@@ -97,56 +110,86 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     }
     float ma = -INFINITY, la = 0.f, mb = -INFINITY, lb = 0.f;
 
-    // Cooperative tile loads: thread t moves 16-byte chunks x and x + 8 (x =
-    // t % 8) of the K row and of the V row of token t / 8 of the tile.
-    const int lrow = threadIdx.x >> 3;
-    const int lx = threadIdx.x & 7;
+    // Cooperative tile loads: thread t moves 16-byte chunk x = t % 16 of the K
+    // and V rows of tokens r and r + 4, r = (t / 16) % 4 + 8 (t / 64), and
+    // writes the V pair transposed.
+    const int lx = threadIdx.x & 15;
+    const int lq = threadIdx.x >> 4;
+    const int lr = (lq & 3) + 8 * (lq >> 2);
     const int32_t* table = p.tables + static_cast<uint64_t>(b) * p.max_nb;
     auto load_regs = [&](int tile, u32x4 (&r)[4]) {
-        const int tok = tile * kTileTokens + lrow;
-        if (tok < ctx_end) {
-            const int32_t blk = table[tok >> p.tpb_shift];
-            const uint8_t* base = p.kv_base + static_cast<uint64_t>(blk) * p.block_stride +
-                                  static_cast<uint64_t>(tok & (p.tpb - 1)) * p.token_stride +
-                                  static_cast<uint64_t>(g) * p.head_stride;
-            r[0] = load16(base + p.k_off + 16 * lx);
-            r[1] = load16(base + p.k_off + 16 * (lx + 8));
-            r[2] = load16(base + p.v_off + 16 * lx);
-            r[3] = load16(base + p.v_off + 16 * (lx + 8));
-        } else {
-            // Rows past the context are zeros: their weights are 0 and 0 * 0
-            // keeps O clean.
-            r[0] = r[1] = r[2] = r[3] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int tok = tile * kTileTokens + lr + 4 * e;
+            if (tok < ctx_end) {
+                const int32_t blk = table[tok >> p.tpb_shift];
+                const uint8_t* base = p.kv_base + static_cast<uint64_t>(blk) * p.block_stride +
+                                      static_cast<uint64_t>(tok & (p.tpb - 1)) * p.token_stride +
+                                      static_cast<uint64_t>(g) * p.head_stride + 16 * lx;
+                r[e] = load16(base + p.k_off);
+                r[2 + e] = load16(base + p.v_off);
+            } else {
+                // Rows past the context are zeros: masked scores, zero values.
+                r[e] = u32x4{0u, 0u, 0u, 0u};
+                r[2 + e] = u32x4{0u, 0u, 0u, 0u};
+            }
         }
     };
+    const int vt_col = 2 * (8 * (lr & 3) + (lr >> 2));  // byte offset of token lr (lr + 4 follows it)
     auto store_lds = [&](int buf, const u32x4 (&r)[4]) {
-        *reinterpret_cast<u32x4*>(&sm_kv[buf][0][lrow][16 * lx]) = r[0];
-        *reinterpret_cast<u32x4*>(&sm_kv[buf][0][lrow][16 * (lx + 8)]) = r[1];
-        *reinterpret_cast<u32x4*>(&sm_kv[buf][1][lrow][16 * lx]) = r[2];
-        *reinterpret_cast<u32x4*>(&sm_kv[buf][1][lrow][16 * (lx + 8)]) = r[3];
+        *reinterpret_cast<u32x4*>(&sm[buf].k[lr][16 * lx]) = r[0];
+        *reinterpret_cast<u32x4*>(&sm[buf].k[lr + 4][16 * lx]) = r[1];
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+            const uint32_t x = r[2][n >> 1];
+            const uint32_t y = r[3][n >> 1];
+            const uint32_t pair = (n & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
+            *reinterpret_cast<uint32_t*>(&sm[buf].vt[n * 16 + lx][vt_col]) = pair;
+        }
     };
 
-    u32x4 regs[4];
-    load_regs(0, regs);
-    store_lds(0, regs);
-    __syncthreads();
-    for (int t = 0; t < ntiles; ++t) {
+    // Two register stages: the loads of tile t + 2 are issued while tile t is
+    // computed and land in LDS after tile t + 1 is computed, so each load has
+    // two tiles of compute to arrive. The loop is unrolled by two so each
+    // stage keeps its registers.
+    auto compute = [&](int t) {
         const int buf = t & 1;
-        const bool more = t + 1 < ntiles;
-        if (more) load_regs(t + 1, regs);  // in flight while this tile is computed
-        KvTile tile;
+        u32x4 kf[2][4], vf[8];
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                tile.k[u][i] = lds16(&sm_kv[buf][0][16 * u + (c >> 2) + 4 * (c & 3)][16 * j + 64 * i]);
+            for (int i = 0; i < 4; ++i) kf[u][i] = lds16(&sm[buf].k[16 * u + (c >> 2) + 4 * (c & 3)][16 * j + 64 * i]);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) tile.v[q] = lds16(&sm_kv[buf][1][4 * q + j][16 * c]);
-        if (has_a) compute_tile(tile, qa, t * kTileTokens, col_last, ctx_end, p.scale_log2, j, ma, la, oa);
-        if (has_b) compute_tile(tile, qb, t * kTileTokens, col_last, ctx_end, p.scale_log2, j, mb, lb, ob);
-        if (more) store_lds(buf ^ 1, regs);
-        // Tile t + 1 is visible, and every wave is done with buffer `buf`
-        // before the next iteration refills it.
+        for (int n = 0; n < 8; ++n) vf[n] = lds16(&sm[buf].vt[n * 16 + c][16 * j]);
+        // Only tiles reaching the block's first position need the causal mask.
+        const int lim = t * kTileTokens + kTileTokens - 1 > p0 ? col_last : INT_MAX;
+        // Both query heads in one block, so one head's softmax overlaps the
+        // other's MFMAs (a wave with one head computes it twice, writing once).
+        floatx4 acc_a[2], acc_b[2];
+        u32x4 ahi, alo, bhi, blo;
+        qk_tile(kf, qa, acc_a);
+        qk_tile(kf, qb, acc_b);
+        softmax_tile(acc_a, t * kTileTokens, lim, p.scale_log2, j, ma, la, oa, ahi, alo);
+        pv_tile(vf, ahi, alo, oa);
+        softmax_tile(acc_b, t * kTileTokens, lim, p.scale_log2, j, mb, lb, ob, bhi, blo);
+        pv_tile(vf, bhi, blo, ob);
+    };
+    u32x4 r0[4], r1[4];
+    load_regs(0, r0);
+    store_lds(0, r0);
+    if (ntiles > 1) load_regs(1, r0);
+    __syncthreads();
+    for (int t = 0; t < ntiles; t += 2) {
+        // LDS buffer 0 holds tile t; r0 carries tile t + 1.
+        if (t + 2 < ntiles) load_regs(t + 2, r1);
+        compute(t);
+        if (t + 1 < ntiles) store_lds(1, r0);
+        // Tile t + 1 is visible, and every wave is done with buffer 0.
+        __syncthreads();
+        if (t + 1 >= ntiles) break;
+        if (t + 3 < ntiles) load_regs(t + 3, r0);
+        compute(t + 1);
+        if (t + 2 < ntiles) store_lds(0, r1);
         __syncthreads();
     }
 
@@ -262,8 +305,9 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
     hipStream_t s = qvp::as_stream(stream);
     qvp_prefill_plan& plan = batch->prefill;
 
-    if (!qvp::prefill_mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
-                                     reinterpret_cast<uintptr_t>(a->kv_base))) {
+    // The MFMA kernel takes its running maximum on raw scores: scale > 0.
+    if (!(a->scale > 0.0f) || !qvp::prefill_mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
+                                                            reinterpret_cast<uintptr_t>(a->kv_base))) {
         // One virtual sequence per new position, over the same frames.
         std::vector<uint32_t> ids, cu{0}, ctx;
         ids.reserve(batch->host_ids.size());
