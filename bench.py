@@ -35,6 +35,7 @@ import json
 import os
 import platform
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -248,12 +249,53 @@ def prefill_bench(steps: int, warmup: int) -> int:
     ms = e0.elapsed_ms(e1) / steps
     flops = 4.0 * 28 * 128 * sum(n * (n + 1) / 2 for n in lens)
     tflops = flops / (ms * 1e-3) / 1e12
+    # torch carries its own HIP runtime, which does not open the device next
+    # to libqvp's in one process: the comparison runs in a child process.
+    child = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--torch-sdpa", "--steps", str(steps),
+                            "--warmup", str(warmup)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                           timeout=300)
+    results = [ln for ln in child.stdout.splitlines() if ln.startswith('{"ms"')]
+    sdpa_ms = json.loads(results[-1])["ms"] if child.returncode == 0 and results else None
+    if sdpa_ms is None:
+        print(f"torch sdpa child failed ({child.returncode}): {child.stderr[-400:]}", file=sys.stderr)
     print(json.dumps({"mode": "prefill", "kernel": "prefill_mfma", "workload": "4 x 2048-token prompts, Hq28/Hkv4/D128 "
                       "bf16, block 16, one layer", "steps": steps, "ms_per_prefill": round(ms, 4),
                       "useful_flops": flops, "tokens_per_s": round(total / (ms * 1e-3), 1),
                       "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_BF16_TFLOPS,
-                                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4)}}))
+                                   "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4)},
+                      "torch_sdpa_contiguous": None if sdpa_ms is None else {
+                          "ms": round(sdpa_ms, 4), "tflops": round(flops / (sdpa_ms * 1e-3) / 1e12, 1),
+                          "note": "torch fused causal attention on contiguous [B,H,S,D] tensors (no paging), "
+                                  "flash/efficient backends only"}}))
     return 0
+
+
+def torch_sdpa_ms(b: int, s: int, hq: int, hkv: int, d: int, steps: int, warmup: int):
+    """Same attention through torch's fused kernels over contiguous tensors: a
+    comparison point for the paged kernel, not a parity reference. None when
+    no fused backend accepts the shape (the math path is not allowed)."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(b, hq, s, d, device="cuda", dtype=torch.bfloat16, generator=g)
+    k = torch.randn(b, hkv, s, d, device="cuda", dtype=torch.bfloat16, generator=g)
+    v = torch.randn(b, hkv, s, d, device="cuda", dtype=torch.bfloat16, generator=g)
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            f = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
+            for _ in range(max(warmup, 1)):
+                f()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                f()
+            e1.record()
+            torch.cuda.synchronize()
+    except RuntimeError as e:
+        print(f"torch sdpa unavailable: {e}", file=sys.stderr)
+        return None
+    return e0.elapsed_time(e1) / steps
 
 
 def append_bench(steps: int, warmup: int) -> int:
@@ -279,6 +321,7 @@ def main() -> int:
     ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
     ap.add_argument("--append", action="store_true", help="time the K/V append of one config2 step")
     ap.add_argument("--prefill", action="store_true", help="time the causal prefill of 4 x 2048-token prompts")
+    ap.add_argument("--torch-sdpa", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
                          "used to scale rocprof FETCH_SIZE / WRITE_SIZE)")
@@ -289,6 +332,9 @@ def main() -> int:
         return append_bench(args.steps, args.warmup)
     if args.prefill:
         return prefill_bench(args.steps, args.warmup)
+    if args.torch_sdpa:
+        print(json.dumps({"ms": torch_sdpa_ms(4, 2048, 28, 4, 128, args.steps, args.warmup)}))
+        return 0
     if args.cow or args.trace:
         return run_driver("cow_bench" if args.cow else "trace_bench")
 

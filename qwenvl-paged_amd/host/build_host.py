@@ -56,6 +56,7 @@ TEST_BINARIES = {
         "PagedAttention.test.cpp",
         "EndToEnd.test.cpp",
         "KVAppend.test.cpp",
+        "Prefill.test.cpp",
     ],
 }
 

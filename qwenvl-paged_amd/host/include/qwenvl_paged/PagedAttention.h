@@ -68,17 +68,33 @@ public:
     bool decode(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
                 std::uint32_t layer, std::uint32_t num_query_heads, float scale, const void* device_query,
                 void* device_out, ElementType out_type);
+    // Causal prefill: for every sequence b the new positions p in
+    // [first_new[b], context_lens[b]) each attend to tokens [0, p] -- the
+    // reference's decode applied per position with context_len = p + 1
+    // (PagedAttention.h:43-44), in one enqueued call. The K/V of the new
+    // positions must already be in the cache (KVAppendBatch). device_query /
+    // device_out: [sum_b (context_lens[b] - first_new[b])][num_query_heads]
+    // [head_dim], sequence-major then position order. Refused like decode,
+    // and for first_new[b] >= context_lens[b].
+    bool prefill(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                 const std::vector<std::uint32_t>& first_new, std::uint32_t layer, std::uint32_t num_query_heads,
+                 float scale, const void* device_query, void* device_out, ElementType out_type);
     // Element type of the cache from its element size (4: F32, 2: BF16 unless
     // set_cache_element_type(F16) was called).
     void set_cache_element_type(ElementType type) noexcept;
     [[nodiscard]] const std::string& last_error() const noexcept;
-    // The packed batch of the last successful decode (device arrays).
+    // The packed batch of the last successful decode or prefill (device arrays).
     [[nodiscard]] qvp_batch* packed() const noexcept;
     // Split-K partition in tokens (0: library default).
     void set_split_tokens(std::uint32_t tokens) noexcept;
 
 private:
     bool fail(std::string msg);
+    // Checks shared by decode and prefill, then packs the batch on the
+    // allocator's stream; fills the pool geometry of the launch.
+    bool pack(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+              std::uint32_t layer, std::uint32_t num_query_heads, const void* device_query, void* device_out,
+              int& cache_type, void*& stream);
 
     qvp_batch* batch_{nullptr};
     std::vector<std::uint32_t> ids_;

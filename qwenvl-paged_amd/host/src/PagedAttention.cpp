@@ -141,9 +141,9 @@ void PagedAttentionBatch::set_cache_element_type(ElementType type) noexcept {
     cache_type_override_ = static_cast<int>(type);
 }
 
-bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
-                                 std::uint32_t layer, std::uint32_t num_query_heads, float scale,
-                                 const void* device_query, void* device_out, ElementType out_type) {
+bool PagedAttentionBatch::pack(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                               std::uint32_t layer, std::uint32_t num_query_heads, const void* device_query,
+                               void* device_out, int& cache_type, void*& stream) {
     if (batch_ == nullptr) return fail("no packed-batch object (device unavailable?)");
     if (views.empty() || views.size() != context_lens.size()) return fail("views and context_lens differ in size");
     if (device_query == nullptr || device_out == nullptr) return fail("null query or output buffer");
@@ -162,7 +162,7 @@ bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std:
     if (num_query_heads == 0 || shape.num_kv_heads == 0 || num_query_heads % shape.num_kv_heads != 0) {
         return fail("query heads do not group onto the kv heads");
     }
-    int cache_type = shape.bytes_per_element == 4 ? QVP_DTYPE_F32 : QVP_DTYPE_BF16;
+    cache_type = shape.bytes_per_element == 4 ? QVP_DTYPE_F32 : QVP_DTYPE_BF16;
     if (cache_type_override_ >= 0) cache_type = cache_type_override_;
     if (qvp_dtype(cache_type) == QVP_DTYPE_F32 ? shape.bytes_per_element != 4 : shape.bytes_per_element != 2) {
         return fail("element type does not match the cache's element size");
@@ -176,11 +176,11 @@ bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std:
         cu_.push_back(static_cast<std::uint32_t>(ids_.size()));
     }
 
-    // Queued copy-on-write copies and swap traffic land before the decode
-    // reads any frame.
+    // Queued copy-on-write copies and swap traffic land before the kernels
+    // read any frame.
     MemoryAllocator* mut = const_cast<MemoryAllocator*>(allocator);
     if (!mut->flush()) return fail("flush: " + mut->last_error());
-    void* stream = allocator->stream();
+    stream = allocator->stream();
     const PhysicalBlock* frame0 = allocator->block(0);
     const std::uint32_t num_blocks = static_cast<std::uint32_t>(allocator->stats().total_blocks);
     if (frame0 == nullptr) return fail("empty pool");
@@ -188,7 +188,18 @@ bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std:
                  context_lens.data(), shape.tokens_per_block, num_blocks, split_tokens_, stream) != QVP_OK) {
         return fail(std::string("pack: ") + qvp_last_error());
     }
+    return true;
+}
+
+bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                                 std::uint32_t layer, std::uint32_t num_query_heads, float scale,
+                                 const void* device_query, void* device_out, ElementType out_type) {
+    int cache_type = 0;
+    void* stream = nullptr;
+    if (!pack(views, context_lens, layer, num_query_heads, device_query, device_out, cache_type, stream)) return false;
     const KVBlockLayout& layout = views.front().layout;
+    const BlockShape& shape = layout.shape;
+    const MemoryAllocator* allocator = views.front().allocator;
     qvp_decode_args args{};
     args.query = device_query;
     args.out = device_out;
@@ -209,6 +220,44 @@ bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std:
     args.layer_stride = layout.layer_stride();
     args.scale = scale;
     if (qvp_paged_decode(&args, stream) != QVP_OK) return fail(std::string("decode: ") + qvp_last_error());
+    return true;
+}
+
+bool PagedAttentionBatch::prefill(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                                  const std::vector<std::uint32_t>& first_new, std::uint32_t layer,
+                                  std::uint32_t num_query_heads, float scale, const void* device_query,
+                                  void* device_out, ElementType out_type) {
+    if (first_new.size() != views.size()) return fail("views and first_new differ in size");
+    for (std::size_t b = 0; b < first_new.size() && b < context_lens.size(); ++b) {
+        if (first_new[b] >= context_lens[b]) return fail("first new position is not below the context length");
+    }
+    int cache_type = 0;
+    void* stream = nullptr;
+    if (!pack(views, context_lens, layer, num_query_heads, device_query, device_out, cache_type, stream)) return false;
+    const KVBlockLayout& layout = views.front().layout;
+    const BlockShape& shape = layout.shape;
+    const MemoryAllocator* allocator = views.front().allocator;
+    qvp_prefill_args args{};
+    args.query = device_query;
+    args.out = device_out;
+    args.kv_base = allocator->device_base();
+    args.block_stride = allocator->block_stride();
+    args.batch = batch_;
+    args.q_start = first_new.data();
+    args.kv_dtype = static_cast<std::uint32_t>(cache_type);
+    args.out_dtype = static_cast<std::uint32_t>(out_type);
+    args.layer = layer;
+    args.num_layers = shape.num_layers;
+    args.num_query_heads = num_query_heads;
+    args.num_kv_heads = shape.num_kv_heads;
+    args.head_dim = shape.head_dim;
+    args.tokens_per_block = shape.tokens_per_block;
+    args.head_stride = layout.head_stride();
+    args.token_stride = layout.token_stride();
+    args.stream_stride = layout.stream_stride();
+    args.layer_stride = layout.layer_stride();
+    args.scale = scale;
+    if (qvp_paged_prefill(&args, stream) != QVP_OK) return fail(std::string("prefill: ") + qvp_last_error());
     return true;
 }
 
