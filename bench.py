@@ -298,6 +298,75 @@ def torch_sdpa_ms(b: int, s: int, hq: int, hkv: int, d: int, steps: int, warmup:
     return e0.elapsed_time(e1) / steps
 
 
+def mrope_layout(num_seqs: int, prompt: int, seed: int):
+    """Qwen2-VL-style prompts: text runs and images / videos (spatial grids
+    4..40, up to 5 frames, temporal strides 1..8), laid out as get_rope_index
+    lays them out, filling `prompt` tokens."""
+    rng = np.random.default_rng(seed)
+    spans = []
+    for _ in range(num_seqs):
+        rows, tok, cur = [], 0, 0
+        while tok < prompt:
+            text = min(int(rng.integers(5, 200)), prompt - tok)
+            rows.append((tok, text, 0, 0, (cur,) * 3, (1, 1, 1), (0, 0, 0)))
+            tok, cur = tok + text, cur + text
+            gh, gw = int(rng.integers(4, 40)), int(rng.integers(4, 40))
+            gt = 1 if rng.integers(0, 2) == 0 else int(rng.integers(2, 6))
+            if tok + gt * gh * gw > prompt:
+                continue
+            rows.append((tok, gt * gh * gw, 2 if gt > 1 else 1, 0, (cur,) * 3, (int(rng.integers(1, 9)), 1, 1),
+                         (gt, gh, gw)))
+            tok, cur = tok + gt * gh * gw, cur + max(gh, gw)
+        spans.append(np.array(rows, qvp.MROPE_SPAN))
+    return spans
+
+
+def mrope_bench(steps: int, warmup: int, with_cpu: bool) -> int:
+    """M-RoPE positions of a prefill of 64 x 8192-token multimodal prompts
+    (524,288 rows) and of one decode step of the same 64 sequences."""
+    B, S = 64, 8192
+    spans = mrope_layout(B, S, 3)
+    cu = np.concatenate([[0], np.cumsum([len(x) for x in spans])]).astype(np.uint32)
+    flat = np.concatenate(spans)
+    stream = qvp.Stream()
+    mr = qvp.MRope()
+    cases = []
+    for name, begin, end in (("prefill 64 x 8192 tokens", [0] * B, [S] * B),
+                             ("decode step, 64 sequences", [S] * B, [S + 1] * B)):
+        rows = int(sum(e - b for b, e in zip(begin, end)))
+        out = qvp.DeviceBuffer(rows * 3 * 8)
+        for _ in range(warmup):
+            mr.positions(flat, cu, begin, end, out.ptr, rows, stream)
+        stream.synchronize()
+        e0, e1 = qvp.Event(), qvp.Event()
+        e0.record(stream)
+        for _ in range(steps):
+            mr.positions(flat, cu, begin, end, out.ptr, rows, stream)
+        e1.record(stream)
+        stream.synchronize()
+        us = e0.elapsed_ms(e1) * 1e3 / steps
+        written = rows * 24
+        case = {"case": name, "rows": rows, "us_per_call": round(us, 3),
+                "rows_per_s": round(rows / (us * 1e-6), 1),
+                "roofline": {"bound": "hbm", "achieved": round(written / (us * 1e-6) / 1e9, 1), "peak": PEAK_HBM_GBPS,
+                             "unit": "GB/s", "frac": round(written / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+                             "algorithmic_bytes": written}}
+        if with_cpu:
+            sys.path.insert(0, str(ROOT / "oracle"))
+            import pyoracle as O
+            t0 = time.perf_counter()
+            for x, b, e in zip(spans, begin, end):
+                O.mrope_positions(x, b, e)
+            cpu = time.perf_counter() - t0
+            case["cpu_baseline"] = {"value": round(rows / cpu, 1), "unit": "rows/s", "cores": 1, "kind": "port",
+                                    "sample": "the same call, oracle.c orc_mrope_positions per sequence "
+                                              "(walks tokens 0 .. end-1)"}
+        cases.append(case)
+    print(json.dumps({"mode": "mrope", "kernel": "mrope_rows", "data": "synthetic Qwen2-VL-style prompt layouts "
+                      "(text runs, images, videos)", "spans": int(len(flat)), "steps": steps, "cases": cases}))
+    return 0
+
+
 def append_bench(steps: int, warmup: int) -> int:
     w = W.config2()
     cases = [append_case("config2 step, one layer", w, 1, 0, 1, steps, warmup),
@@ -321,6 +390,7 @@ def main() -> int:
     ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
     ap.add_argument("--append", action="store_true", help="time the K/V append of one config2 step")
     ap.add_argument("--prefill", action="store_true", help="time the causal prefill of 4 x 2048-token prompts")
+    ap.add_argument("--mrope", action="store_true", help="time M-RoPE position materialisation")
     ap.add_argument("--torch-sdpa", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
@@ -332,6 +402,8 @@ def main() -> int:
         return append_bench(args.steps, args.warmup)
     if args.prefill:
         return prefill_bench(args.steps, args.warmup)
+    if args.mrope:
+        return mrope_bench(args.steps, args.warmup, not args.no_cpu)
     if args.torch_sdpa:
         print(json.dumps({"ms": torch_sdpa_ms(4, 2048, 28, 4, 128, args.steps, args.warmup)}))
         return 0

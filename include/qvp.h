@@ -21,6 +21,11 @@
  *                     src/MemoryAllocator.cpp:76-85 (copy_block)
  *   swap              include/qwenvl_paged/SwapBackend.h:27-57,
  *                     src/SwapBackend.cpp:10-43 (store/load of whole blocks)
+ *   K/V append        tests/PagedAttention.test.cpp:97-127, tests/EndToEnd.test.cpp:157-179
+ *   causal prefill    include/qwenvl_paged/PagedAttention.h:43-44 (decode per
+ *                     prompt position with context_len = p + 1)
+ *   M-RoPE positions  include/qwenvl_paged/KVCacheManager.h:23-78
+ *                     (PositionalEncodingSpan metadata)
  *
  * Conventions
  *   - Every entry point returns a qvp_status; QVP_OK is 0. On any other value
@@ -352,6 +357,45 @@ typedef struct qvp_append_args {
  * exceeds block_stride (QVP_ERR_INVALID_ARGUMENT). */
 int qvp_append_kv(const qvp_append_args* args, const uint32_t* frames, const uint32_t* slots,
                   uint32_t count, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* M-RoPE positions (PositionalEncodingSpan, KVCacheManager.h:23-78)        */
+/* ------------------------------------------------------------------------ */
+
+/* One PositionalEncodingSpan of a sequence. `grid` (the span's temporal,
+ * height and width extents) is this build's addition: the reference's span
+ * carries origin and stride only, which do not say where an image row ends. */
+typedef struct qvp_mrope_span {
+    uint32_t start_token;
+    uint32_t token_count;
+    uint32_t kind;              /* 0 Text1D, 1 Image2D, 2 Video3D */
+    uint32_t reserved;          /* 0 */
+    int64_t origin[3];          /* temporal, height, width */
+    int64_t stride[3];
+    int64_t grid[3];            /* extents; Image2D / Video3D only */
+} qvp_mrope_span;
+
+/* Host staging and device buffers of the position materialisation. */
+typedef struct qvp_mrope qvp_mrope;
+int qvp_mrope_create(qvp_mrope** out);
+int qvp_mrope_destroy(qvp_mrope* m);
+
+/* Writes the (temporal, height, width) position of tokens [begin[b], end[b])
+ * of every sequence b to out (device, int64, [3][total_rows], rows in sequence
+ * order, axis-major as a model's position_ids). Token i of a Text1D span is
+ * origin + i * stride on each axis; token i of an Image2D / Video3D span with
+ * grid (T, H, W) is origin + (i / (H W), (i / W) % H, i % W) * stride per
+ * axis; a token no span covers takes 1 + the largest position of any axis of
+ * the tokens before it on all three axes (0 for the first token), which is
+ * the text / decode continuation of Qwen2-VL's get_rope_index. spans: host,
+ * CSR over cu_spans[num_seqs + 1], sorted by start_token within a sequence.
+ * Refused before anything is enqueued: overlapping or unsorted spans, an
+ * empty span, an unknown kind, a grid whose product is not token_count (or
+ * an Image2D grid with T != 1), |origin| or |stride| above 2^24, more than
+ * 2^24 sequences, begin[b] > end[b], total_rows != sum(end - begin). */
+int qvp_mrope_positions(qvp_mrope* m, const qvp_mrope_span* spans, const uint32_t* cu_spans,
+                        const uint32_t* begin, const uint32_t* end, uint32_t num_seqs, int64_t* out,
+                        uint64_t total_rows, void* stream);
 
 #ifdef __cplusplus
 }

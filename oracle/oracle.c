@@ -411,3 +411,60 @@ int orc_append_kv(uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks
     }
     return 0;
 }
+
+/* ---------------------------------------------------------------- */
+/* M-RoPE positions (see oracle.h)                                  */
+/* ---------------------------------------------------------------- */
+
+static int mrope_span_ok(const orc_mrope_span* s) {
+    const int64_t lim = (int64_t)1 << 24;
+    if (s->token_count == 0 || s->kind > 2) return 0;
+    for (int a = 0; a < 3; ++a) {
+        if (s->origin[a] > lim || s->origin[a] < -lim || s->stride[a] > lim || s->stride[a] < -lim) return 0;
+    }
+    if (s->kind == 0) return 1;
+    for (int a = 0; a < 3; ++a) {
+        if (s->grid[a] < 1 || s->grid[a] > (int64_t)s->token_count) return 0;
+    }
+    if (s->kind == 1 && s->grid[0] != 1) return 0;
+    return s->grid[0] * s->grid[1] * s->grid[2] == (int64_t)s->token_count;
+}
+
+int orc_mrope_positions(const orc_mrope_span* spans, uint32_t num_spans, uint32_t begin, uint32_t end,
+                        int64_t* out) {
+    if (begin > end) return -1;
+    uint64_t prev_end = 0;
+    for (uint32_t k = 0; k < num_spans; ++k) {
+        if (!mrope_span_ok(&spans[k]) || spans[k].start_token < prev_end) return -1;
+        prev_end = (uint64_t)spans[k].start_token + spans[k].token_count;
+    }
+    const uint32_t n = end - begin;
+    int64_t running_max = -1;
+    uint32_t k = 0;
+    for (uint64_t p = 0; p < end; ++p) {
+        while (k < num_spans && (uint64_t)spans[k].start_token + spans[k].token_count <= p) ++k;
+        int64_t pos[3];
+        if (k < num_spans && spans[k].start_token <= p) {
+            const orc_mrope_span* s = &spans[k];
+            const int64_t i = (int64_t)(p - s->start_token);
+            int64_t coord[3];
+            if (s->kind == 0) {
+                coord[0] = coord[1] = coord[2] = i;
+            } else {
+                coord[0] = i / (s->grid[1] * s->grid[2]);
+                coord[1] = (i / s->grid[2]) % s->grid[1];
+                coord[2] = i % s->grid[2];
+            }
+            for (int a = 0; a < 3; ++a) pos[a] = s->origin[a] + coord[a] * s->stride[a];
+        } else {
+            pos[0] = pos[1] = pos[2] = running_max + 1;
+        }
+        for (int a = 0; a < 3; ++a) {
+            if (pos[a] > running_max) running_max = pos[a];
+        }
+        if (p >= begin) {
+            for (int a = 0; a < 3; ++a) out[(uint64_t)a * n + (p - begin)] = pos[a];
+        }
+    }
+    return 0;
+}

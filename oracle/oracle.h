@@ -14,7 +14,10 @@
  * branches); the layout functions match CacheView.test.cpp's invariants; pack
  * and copy are checked against BlockTable entries and memcpy identity; the
  * append is checked against the compiled reference's element_offset and a
- * read-back of every written element (untouched bytes unchanged).
+ * read-back of every written element (untouched bytes unchanged); the M-RoPE
+ * positions match position ids written by Hugging Face transformers 5.15.0's
+ * Qwen2-VL / Qwen2.5-VL get_rope_index (tests/golden/mrope_positions.json),
+ * the reference itself having no materialisation.
  */
 #ifndef QVP_ORACLE_H
 #define QVP_ORACLE_H
@@ -108,6 +111,32 @@ int orc_append_kv(uint8_t* pool, uint64_t block_stride, uint32_t num_pool_blocks
                   uint32_t tokens_per_block, uint32_t num_layers, uint32_t num_kv_heads, uint32_t head_dim,
                   uint32_t first_layer, uint32_t layer_count, const uint32_t* frames, const uint32_t* slots,
                   uint32_t count, const uint8_t* k, const uint8_t* v);
+
+/* One positional span (PositionalEncodingSpan, include/qwenvl_paged/
+ * KVCacheManager.h:41-60, plus grid extents for image / video spans). */
+typedef struct orc_mrope_span {
+    uint32_t start_token;
+    uint32_t token_count;
+    uint32_t kind; /* 0 Text1D, 1 Image2D, 2 Video3D */
+    uint32_t reserved;
+    int64_t origin[3];
+    int64_t stride[3];
+    int64_t grid[3];
+} orc_mrope_span;
+
+/* M-RoPE (temporal, height, width) positions of tokens [begin, end) of one
+ * sequence into out[3][end - begin]. Restates the position rule of Qwen2-VL's
+ * get_rope_index (transformers 5.15.0, models/qwen2_vl/modeling_qwen2_vl.py,
+ * Qwen2VLModel.get_vision_position_ids / get_rope_index; Qwen2.5-VL's adds a
+ * temporal stride): a span's token i sits at origin + its grid coordinates x
+ * stride (Text1D: i on every axis); a token outside every span continues
+ * 1D from 1 + the largest position of any earlier token (the decode rule
+ * position = p + rope_delta). Walks tokens 0 .. end-1 in order keeping that
+ * running maximum. Returns -1 without writing for spans the library refuses
+ * (unsorted or overlapping, empty, unknown kind, grid product != count, an
+ * Image2D grid with T != 1, |origin| or |stride| > 2^24) or begin > end. */
+int orc_mrope_positions(const orc_mrope_span* spans, uint32_t num_spans, uint32_t begin, uint32_t end,
+                        int64_t* out);
 
 #ifdef __cplusplus
 }

@@ -69,6 +69,8 @@ def oracle() -> ctypes.CDLL:
         lib.orc_append_kv.restype = ctypes.c_int
         lib.orc_append_kv.argtypes = [c_void_p, c_uint64] + [c_uint32] * 8 + [_u32p, _u32p, c_uint32, c_void_p,
                                                                               c_void_p]
+        lib.orc_mrope_positions.restype = ctypes.c_int
+        lib.orc_mrope_positions.argtypes = [c_void_p, c_uint32, c_uint32, c_uint32, c_void_p]
         _oracle = lib
     return _oracle
 
@@ -138,6 +140,21 @@ def append_kv(pool: np.ndarray, block_stride: int, num_pool_blocks: int, elem_by
     return oracle().orc_append_kv(pool.ctypes.data, block_stride, num_pool_blocks, elem_bytes, tpb, num_layers,
                                   hkv, d, first_layer, layer_count, f_p, s_p, len(np.atleast_1d(frames)),
                                   k.ctypes.data, v.ctypes.data)
+
+
+# orc_mrope_span (oracle.h): PositionalEncodingSpan plus grid extents.
+MROPE_SPAN = np.dtype([("start_token", "<u4"), ("token_count", "<u4"), ("kind", "<u4"), ("reserved", "<u4"),
+                       ("origin", "<i8", 3), ("stride", "<i8", 3), ("grid", "<i8", 3)])
+assert MROPE_SPAN.itemsize == 88
+
+
+def mrope_positions(spans: np.ndarray, begin: int, end: int):
+    """Positions [3][end - begin] (int64) of one sequence, or None when refused."""
+    spans = np.ascontiguousarray(spans, dtype=MROPE_SPAN)
+    out = np.zeros((3, max(end - begin, 0)), np.int64)
+    rc = oracle().orc_mrope_positions(spans.ctypes.data if len(spans) else None, len(spans), begin, end,
+                                      out.ctypes.data)
+    return None if rc != 0 else out
 
 
 def pack(ids, cu_blocks, context_lens, tpb: int, num_pool_blocks: int, split_tokens: int = 0):

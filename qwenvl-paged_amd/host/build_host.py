@@ -57,6 +57,7 @@ TEST_BINARIES = {
         "EndToEnd.test.cpp",
         "KVAppend.test.cpp",
         "Prefill.test.cpp",
+        "MRope.test.cpp",
     ],
 }
 

@@ -36,6 +36,11 @@ struct PositionalEncodingSpan {
     PositionEncodingKind kind{PositionEncodingKind::Text1D};
     Position3D origin{};
     Position3D stride{};
+    // Addition (trailing, defaulted, so the reference's aggregate
+    // initialisations still compile): the temporal, height and width extents
+    // of an Image2D / Video3D span, needed to place its token i (row-major
+    // over the grid); unused for Text1D.
+    Position3D grid{};
 };
 
 struct PositionalEncodingMetadata {

@@ -182,6 +182,10 @@ SIGNATURES = {
     ),
     "qvp_append_kv": (c_int, [POINTER(AppendArgs), _u32p, _u32p, c_uint32, c_void_p]),
     "qvp_paged_prefill": (c_int, [POINTER(PrefillArgs), c_void_p]),
+    "qvp_mrope_create": (c_int, [POINTER(c_void_p)]),
+    "qvp_mrope_destroy": (c_int, [c_void_p]),
+    "qvp_mrope_positions": (c_int, [c_void_p, c_void_p, _u32p, _u32p, _u32p, c_uint32, c_void_p, c_uint64,
+                                    c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None
@@ -484,6 +488,40 @@ class Batch:
     def destroy(self) -> None:
         if self.handle:
             check(load().qvp_batch_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+# qvp_mrope_span: PositionalEncodingSpan with grid extents.
+MROPE_SPAN = np.dtype([("start_token", "<u4"), ("token_count", "<u4"), ("kind", "<u4"), ("reserved", "<u4"),
+                       ("origin", "<i8", 3), ("stride", "<i8", 3), ("grid", "<i8", 3)])
+
+
+class MRope:
+    """M-RoPE position materialisation (qvp_mrope_*)."""
+
+    def __init__(self):
+        p = c_void_p()
+        check(load().qvp_mrope_create(byref(p)))
+        self.handle = p.value
+
+    def positions(self, spans, cu_spans, begin, end, out: int, total_rows: int, stream=None) -> None:
+        """Writes int64 [3][total_rows] positions to device address `out`."""
+        spans = np.ascontiguousarray(spans, dtype=MROPE_SPAN)
+        cu_a, cu_p = _u32(cu_spans)
+        b_a, b_p = _u32(begin)
+        e_a, e_p = _u32(end)
+        check(load().qvp_mrope_positions(self.handle, spans.ctypes.data if len(spans) else None, cu_p, b_p, e_p,
+                                         len(b_a), out, total_rows, _sp(stream)))
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(load().qvp_mrope_destroy(self.handle))
             self.handle = None
 
     def __del__(self):

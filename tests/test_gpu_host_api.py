@@ -13,7 +13,7 @@ import pytest
 ROOT = Path(__file__).resolve().parents[1]
 BINARY = ROOT / "build" / "tests" / "device_tests"
 
-SUITES = ["DeviceAllocatorTest", "PagedAttentionTest", "PagedAttentionBatchTest", "EngineTest", "KVAppendTest", "PrefillTest"]
+SUITES = ["DeviceAllocatorTest", "PagedAttentionTest", "PagedAttentionBatchTest", "EngineTest", "KVAppendTest", "PrefillTest", "MRopeTest"]
 
 
 @pytest.mark.gpu
