@@ -237,6 +237,9 @@ def prefill_bench(steps: int, warmup: int) -> int:
                             q_start=np.zeros(len(lens), np.uint32), kv_dtype=qvp.DTYPE_BF16,
                             out_dtype=qvp.DTYPE_BF16, layer=0, num_layers=1, num_query_heads=28, num_kv_heads=4,
                             head_dim=128, tokens_per_block=16, scale=w.scale)
+    # At least 30 warm-up launches (~10 ms) on both sides: GPU clocks ramp
+    # over the first milliseconds of sustained MFMA work.
+    warmup = max(warmup, 30)
     for _ in range(warmup):
         qvp.paged_prefill(args, stream)
     stream.synchronize()
@@ -283,7 +286,7 @@ def torch_sdpa_ms(b: int, s: int, hq: int, hkv: int, d: int, steps: int, warmup:
     try:
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             f = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=True)
-            for _ in range(max(warmup, 1)):
+            for _ in range(max(warmup, 30)):
                 f()
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

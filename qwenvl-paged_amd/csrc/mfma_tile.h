@@ -153,25 +153,20 @@ __device__ inline void qk_tile(const u32x4 (&k)[2][4], const u32x4 (&qop)[4], fl
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
-// Online-softmax update of one tile for column c of this lane. Scores count
-// for tokens <= lim (pass INT_MAX when every token of the tile counts); the
-// running maximum m is kept in scaled base-2 units, so with scale_log2 > 0 the
+// Online-softmax step of one tile for column c of this lane. The running
+// maximum m is kept in scaled base-2 units, so with scale_log2 > 0 the
 // maximum is taken on the raw scores and each weight is one fma and one exp2.
-// The running (l, O) are rescaled (skipped when no column's maximum moved: the
-// factor is then exactly 1), and P is returned as the hi and lo bf16 B
-// operands of the PV MFMAs (lo = P - hi, rounded to nearest even).
-__device__ inline void softmax_tile(const floatx4 (&acc)[2], int tok0, int lim, float scale_log2, int j,
-                                    float& m_run, float& l_run, floatx4 (&o)[8], u32x4& bhi, u32x4& blo) {
-    float s[2][4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) s[u][r] = (tok0 + j + 16 * u + 4 * r <= lim) ? acc[u][r] : -INFINITY;
+// l is rescaled here; O must be scaled by the returned alpha by the caller
+// (alpha is exactly 1 when no column's maximum moved). P is returned as the
+// hi and lo bf16 B operands of the PV MFMAs (hi = P truncated to bf16, lo =
+// P - hi rounded to nearest even).
+__device__ inline void softmax_p(const floatx4 (&s)[2], float scale_log2, float& m_run, float& l_run, u32x4& bhi,
+                                 u32x4& blo, float& alpha) {
     float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     mt = max_over_j(mt) * scale_log2;
     const float m_new = fmaxf(m_run, mt);
-    const float alpha = fast_exp2(m_run - m_new);
+    alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
     float psum = 0.f;
     uint32_t phi[4], plo[4];
@@ -182,25 +177,22 @@ __device__ inline void softmax_tile(const floatx4 (&acc)[2], int tok0, int lim, 
             const float p0 = fast_exp2(fmaf(s[u][r], scale_log2, -m_new));
             const float p1 = fast_exp2(fmaf(s[u][r + 1], scale_log2, -m_new));
             psum += p0 + p1;
-            const uint32_t t0 = __float_as_uint(p0) & 0xffff0000u;
-            const uint32_t t1 = __float_as_uint(p1) & 0xffff0000u;
-            const bf16x2_t lo = {static_cast<__bf16>(p0 - __uint_as_float(t0)),
-                                 static_cast<__bf16>(p1 - __uint_as_float(t1))};
-            phi[2 * u + r / 2] = (t0 >> 16) | t1;
+            const uint32_t b0 = __float_as_uint(p0);
+            const uint32_t b1 = __float_as_uint(p1);
+            const bf16x2_t lo = {static_cast<__bf16>(p0 - __uint_as_float(b0 & 0xffff0000u)),
+                                 static_cast<__bf16>(p1 - __uint_as_float(b1 & 0xffff0000u))};
+            // High halves of p0 (low word) and p1 (high word) in one byte permute.
+            phi[2 * u + r / 2] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
             plo[2 * u + r / 2] = __builtin_bit_cast(uint32_t, lo);
         }
     }
     l_run = l_run * alpha + psum;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
-#pragma unroll
-        for (int n = 0; n < 8; ++n) o[n] *= alpha;
-    }
     bhi = u32x4{phi[0], phi[1], phi[2], phi[3]};
     blo = u32x4{plo[0], plo[1], plo[2], plo[3]};
 }
 
-// O^T += V^T P^T, the A operand of MFMA n given: a[n] in lane (x, j) holds
-// V[tokens j + 4q, q = 0..7][dim 8x + n].
+// O^T += V^T P^T for one tile: `a` holds V^T operands (lane (c, j) of MFMA n:
+// dims 16n + c, the tile's tokens in the P operand's k order).
 __device__ inline void pv_tile(const u32x4 (&a)[8], const u32x4& bhi, const u32x4& blo, floatx4 (&o)[8]) {
 #pragma unroll
     for (int n = 0; n < 8; ++n) {

@@ -8,15 +8,17 @@
 // tokens_per_block >= 16). A work item is (sequence b, kv head g, 16 new
 // positions p0 .. p0 + 15, up to 8 query heads of g's group). Its workgroup
 // streams tokens [0, p0 + 16) of kv head g in 32-token tiles: each tile is
-// loaded once, by all 256 threads, two tiles ahead of its use, into an LDS
-// double buffer holding K rows (padded to 272 bytes so the fragment reads
-// spread over the banks) and V transposed (so the PV operands need no
+// loaded once, by all 256 threads, one tile of compute ahead of its use, into
+// an LDS double buffer holding K rows (padded to 272 bytes so the fragment
+// reads spread over the banks) and V transposed (so the PV operands need no
 // register transpose), and every wave runs the tile math of mfma_tile.h for
-// its query heads with the 16 positions in the MFMA columns, column c seeing
-// tokens t <= p0 + c (masks only on tiles that reach p0). A wave
-// therefore covers the whole causal context of its queries: no split, no
-// merge. Items are launched longest context first so the short ones fill the
-// tail. Each K/V tile feeds 16 positions x up to 8 heads from LDS.
+// its two query heads with the 16 positions in the MFMA columns, column c
+// seeing tokens t <= p0 + c (masks only on tiles that reach p0). The tile
+// loop is software-pipelined: PV of tile t runs beside QK and the softmax of
+// tile t + 1. A wave therefore covers the whole causal context of its
+// queries: no split, no merge. Items are launched longest context first so
+// the short ones fill the tail. Each K/V tile feeds 16 positions x up to 8
+// heads from LDS.
 //
 // Decode path (any other shape): one virtual sequence per new position (same
 // frames, context p + 1), packed into a private batch and run through
@@ -25,6 +27,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <type_traits>
 #include <cstring>
 #include <vector>
 
@@ -111,30 +114,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     float ma = -INFINITY, la = 0.f, mb = -INFINITY, lb = 0.f;
 
     // Cooperative tile loads: thread t moves 16-byte chunk x = t % 16 of the K
-    // and V rows of tokens r and r + 4, r = (t / 16) % 4 + 8 (t / 64), and
-    // writes the V pair transposed.
+    // and V rows of tokens r and r + 4, r = t / 64 + 8 ((t / 16) % 4), and
+    // writes the V pair transposed. Wave w thus writes V^T chunk w of every
+    // row, each lane group its own dword of the chunk: the 64 lanes of a
+    // transposed store hit 64 distinct LDS banks.
     const int lx = threadIdx.x & 15;
-    const int lq = threadIdx.x >> 4;
-    const int lr = (lq & 3) + 8 * (lq >> 2);
-    const int32_t* table = p.tables + static_cast<uint64_t>(b) * p.max_nb;
-    auto load_regs = [&](int tile, u32x4 (&r)[4]) {
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int tok = tile * kTileTokens + lr + 4 * e;
-            if (tok < ctx_end) {
-                const int32_t blk = table[tok >> p.tpb_shift];
-                const uint8_t* base = p.kv_base + static_cast<uint64_t>(blk) * p.block_stride +
-                                      static_cast<uint64_t>(tok & (p.tpb - 1)) * p.token_stride +
-                                      static_cast<uint64_t>(g) * p.head_stride + 16 * lx;
-                r[e] = load16(base + p.k_off);
-                r[2 + e] = load16(base + p.v_off);
-            } else {
-                // Rows past the context are zeros: masked scores, zero values.
-                r[e] = u32x4{0u, 0u, 0u, 0u};
-                r[2 + e] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
+    const int lr = (threadIdx.x >> 6) + 8 * ((threadIdx.x >> 4) & 3);
     const int vt_col = 2 * (8 * (lr & 3) + (lr >> 2));  // byte offset of token lr (lr + 4 follows it)
     auto store_lds = [&](int buf, const u32x4 (&r)[4]) {
         *reinterpret_cast<u32x4*>(&sm[buf].k[lr][16 * lx]) = r[0];
@@ -148,50 +133,144 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
         }
     };
 
-    // Two register stages: the loads of tile t + 2 are issued while tile t is
-    // computed and land in LDS after tile t + 1 is computed, so each load has
-    // two tiles of compute to arrive. The loop is unrolled by two so each
-    // stage keeps its registers.
-    auto compute = [&](int t) {
-        const int buf = t & 1;
-        u32x4 kf[2][4], vf[8];
+    // Addressing: a tile's two 16-token halves lie in one block each
+    // (tokens_per_block is a power of two >= 16), so their frame offsets are
+    // uniform values computed once per tile and each lane adds a constant for
+    // its token rows (tokens lr and lr + 4 share a half). Halves past the
+    // context's last block re-read that block: their scores are masked and
+    // their V rows zeroed, so every address stays inside a mapped frame.
+    const auto* trow = as_const(p.tables) + static_cast<uint64_t>(b) * p.max_nb;
+    const int last_tok = ctx_end - 1;
+    const int last_blk = last_tok >> p.tpb_shift;
+    const int lane_half = lr >> 4;
+    uint64_t lane_off[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        lane_off[e] = static_cast<uint64_t>((lr + 4 * e) & 15) * p.token_stride +
+                      static_cast<uint64_t>(g) * p.head_stride + 16 * lx;
+    }
+    const uint8_t* kbase = p.kv_base + p.k_off;
+    const uint8_t* vbase = p.kv_base + p.v_off;
+    auto load_tile_regs = [&](int tile, u32x4 (&r)[4]) {
+        uint64_t half_off[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int tok0 = tile * kTileTokens + 16 * h;
+            const int blk = min(tok0 >> p.tpb_shift, last_blk);
+            half_off[h] = static_cast<uint64_t>(trow[blk]) * p.block_stride +
+                          static_cast<uint64_t>(tok0 & (p.tpb - 1) & ~15) * p.token_stride;
+        }
+        const uint64_t off = lane_half ? half_off[1] : half_off[0];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            r[e] = load16(kbase + off + lane_off[e]);
+            r[2 + e] = load16(vbase + off + lane_off[e]);
+        }
+    };
+    // V rows past the context are not data (0 * NaN would poison O): they are
+    // zeroed when the tile goes to LDS, a tile of compute after their loads.
+    auto store_tile = [&](int buf, u32x4 (&r)[4], int tile) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            if (tile * kTileTokens + lr + 4 * e > last_tok) r[2 + e] = u32x4{0u, 0u, 0u, 0u};
+        }
+        store_lds(buf, r);
+    };
+    auto read_k = [&](int buf, u32x4 (&kf)[2][4]) {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int i = 0; i < 4; ++i) kf[u][i] = lds16(&sm[buf].k[16 * u + (c >> 2) + 4 * (c & 3)][16 * j + 64 * i]);
+    };
+    auto read_v = [&](int buf, u32x4 (&vf)[8]) {
 #pragma unroll
         for (int n = 0; n < 8; ++n) vf[n] = lds16(&sm[buf].vt[n * 16 + c][16 * j]);
-        // Only tiles reaching the block's first position need the causal mask.
-        const int lim = t * kTileTokens + kTileTokens - 1 > p0 ? col_last : INT_MAX;
-        // Both query heads in one block, so one head's softmax overlaps the
-        // other's MFMAs (a wave with one head computes it twice, writing once).
-        floatx4 acc_a[2], acc_b[2];
-        u32x4 ahi, alo, bhi, blo;
-        qk_tile(kf, qa, acc_a);
-        qk_tile(kf, qb, acc_b);
-        softmax_tile(acc_a, t * kTileTokens, lim, p.scale_log2, j, ma, la, oa, ahi, alo);
-        pv_tile(vf, ahi, alo, oa);
-        softmax_tile(acc_b, t * kTileTokens, lim, p.scale_log2, j, mb, lb, ob, bhi, blo);
-        pv_tile(vf, bhi, blo, ob);
     };
-    u32x4 r0[4], r1[4];
-    load_regs(0, r0);
-    store_lds(0, r0);
-    if (ntiles > 1) load_regs(1, r0);
+    // Causal mask of tile t for both heads: column c sees tokens <= col_last.
+    auto mask2 = [&](floatx4 (&sa)[2], floatx4 (&sb)[2], int t) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool out = t * kTileTokens + j + 16 * u + 4 * r > col_last;
+                sa[u][r] = out ? -INFINITY : sa[u][r];
+                sb[u][r] = out ? -INFINITY : sb[u][r];
+            }
+    };
+
+    // Software pipeline over tiles. Iteration t issues PV(t) (P and V of tile
+    // t already in registers) in one basic block with QK and the softmax of
+    // tile t + 1, which do not depend on it, so the MFMAs of one overlap the
+    // VALU work of the other; tile t + 2 travels from registers to the LDS
+    // buffer tile t used. Tiles from t_diag on reach the block's first
+    // position and take the causal mask; the loop is split there so the
+    // others carry no mask code. Both query heads run in one block (a wave
+    // with one head computes it twice, writing once).
+    const int t_diag = (p0 + 1) / kTileTokens;
+    const int last_tile = ntiles - 1;
+    u32x4 r0[4];
+    u32x4 kf[2][4], vf[8];
+    floatx4 sa[2], sb[2];
+    u32x4 ahi, alo, bhi, blo;
+    float alpha_a, alpha_b;
+    load_tile_regs(0, r0);
+    store_tile(0, r0, 0);
+    load_tile_regs(min(1, last_tile), r0);
     __syncthreads();
-    for (int t = 0; t < ntiles; t += 2) {
-        // LDS buffer 0 holds tile t; r0 carries tile t + 1.
-        if (t + 2 < ntiles) load_regs(t + 2, r1);
-        compute(t);
-        if (t + 1 < ntiles) store_lds(1, r0);
-        // Tile t + 1 is visible, and every wave is done with buffer 0.
+    read_k(0, kf);
+    read_v(0, vf);
+    qk_tile(kf, qa, sa);
+    qk_tile(kf, qb, sb);
+    if (t_diag == 0) mask2(sa, sb, 0);
+    softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
+    softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
+    store_tile(1, r0, min(1, last_tile));
+    __syncthreads();
+    // O is rescaled for tile t's maximum just before PV(t) accumulates into
+    // it, skipped when no column's maximum moved (the factor is then exactly
+    // 1); the branch sits at the top of the iteration, outside the block above.
+    auto rescale = [&]() {
+        if (__builtin_amdgcn_ballot_w64(alpha_a != 1.0f || alpha_b != 1.0f) != 0) {
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                oa[n] *= alpha_a;
+                ob[n] *= alpha_b;
+            }
+        }
+    };
+    auto step = [&](int t, auto masked) {
+        const int nb = (t + 1) & 1;
+        rescale();
+        // Tile t + 2; near the end the last tile again, which lands in a
+        // buffer no later iteration reads.
+        load_tile_regs(min(t + 2, last_tile), r0);
+        read_k(nb, kf);
+        qk_tile(kf, qa, sa);
+        qk_tile(kf, qb, sb);
+        pv_tile(vf, ahi, alo, oa);
+        pv_tile(vf, bhi, blo, ob);
+        read_v(nb, vf);
+        if constexpr (decltype(masked)::value) mask2(sa, sb, t + 1);
+        softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
+        softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
+        // Schedule: the QK MFMAs first, then the PV MFMAs spread over the
+        // softmax's VALU work.
+#pragma unroll
+        for (int k = 0; k < 16; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+        for (int k = 0; k < 32; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        store_tile(t & 1, r0, min(t + 2, last_tile));
         __syncthreads();
-        if (t + 1 >= ntiles) break;
-        if (t + 3 < ntiles) load_regs(t + 3, r0);
-        compute(t + 1);
-        if (t + 2 < ntiles) store_lds(0, r1);
-        __syncthreads();
-    }
+    };
+    int t = 0;
+    for (; t + 1 < min(t_diag, ntiles); ++t) step(t, std::false_type{});
+    for (; t + 1 < ntiles; ++t) step(t, std::true_type{});
+    rescale();
+    pv_tile(vf, ahi, alo, oa);
+    pv_tile(vf, bhi, blo, ob);
 
     OutT* out = static_cast<OutT*>(out_ptr);
     auto write = [&](int hq, const floatx4 (&o)[8], float l) {
