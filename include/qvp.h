@@ -118,6 +118,21 @@ int qvp_event_synchronize(void* event);
 int qvp_stream_wait_event(void* stream, void* event);
 int qvp_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/* HIP graph capture of a stream (thread-local mode). Between begin and end,
+ * enqueue only calls that touch nothing on the host per call: qvp_paged_decode
+ * on a batch that was already decoded once since its last qvp_pack (its
+ * schedule is then cached on the device) with a caller workspace,
+ * qvp_append_kv, qvp_copy_blocks, qvp_swap_gather / qvp_swap_scatter,
+ * qvp_fill_bytes and device-to-device copies. qvp_pack, qvp_paged_prefill and
+ * qvp_mrope_positions upload host-built lists on every call and are not
+ * captured. The kernels reset their own merge counters, so a graph may be
+ * replayed any number of times; it reads and writes the buffers it was
+ * captured with. */
+int qvp_graph_begin_capture(void* stream);
+int qvp_graph_end_capture(void* stream, void** graph_exec);
+int qvp_graph_launch(void* graph_exec, void* stream);
+int qvp_graph_destroy(void* graph_exec);
+
 /* ------------------------------------------------------------------------ */
 /* Block pool: the physical KV frames in HBM                                */
 /* Replaces per-block std::aligned_alloc storage (Block.h:99-166,           */

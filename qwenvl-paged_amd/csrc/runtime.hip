@@ -178,6 +178,37 @@ int qvp_event_elapsed_ms(float* ms, void* start, void* stop) {
     return QVP_OK;
 }
 
+int qvp_graph_begin_capture(void* stream) {
+    if (stream == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "capture needs a created stream, not the default one");
+    QVP_HIP(hipStreamBeginCapture(qvp::as_stream(stream), hipStreamCaptureModeThreadLocal));
+    return QVP_OK;
+}
+
+int qvp_graph_end_capture(void* stream, void** graph_exec) {
+    if (stream == nullptr || graph_exec == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "stream or graph_exec is NULL");
+    *graph_exec = nullptr;
+    hipGraph_t graph = nullptr;
+    QVP_HIP(hipStreamEndCapture(qvp::as_stream(stream), &graph));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (err != hipSuccess) return qvp::hip_fail(err, "hipGraphInstantiate");
+    *graph_exec = exec;
+    return QVP_OK;
+}
+
+int qvp_graph_launch(void* graph_exec, void* stream) {
+    if (graph_exec == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "graph_exec is NULL");
+    QVP_HIP(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), qvp::as_stream(stream)));
+    return QVP_OK;
+}
+
+int qvp_graph_destroy(void* graph_exec) {
+    if (graph_exec == nullptr) return QVP_OK;
+    QVP_HIP(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)));
+    return QVP_OK;
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------------------

@@ -182,6 +182,10 @@ SIGNATURES = {
     ),
     "qvp_append_kv": (c_int, [POINTER(AppendArgs), _u32p, _u32p, c_uint32, c_void_p]),
     "qvp_paged_prefill": (c_int, [POINTER(PrefillArgs), c_void_p]),
+    "qvp_graph_begin_capture": (c_int, [c_void_p]),
+    "qvp_graph_end_capture": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "qvp_graph_launch": (c_int, [c_void_p, c_void_p]),
+    "qvp_graph_destroy": (c_int, [c_void_p]),
     "qvp_mrope_create": (c_int, [POINTER(c_void_p)]),
     "qvp_mrope_destroy": (c_int, [c_void_p]),
     "qvp_mrope_positions": (c_int, [c_void_p, c_void_p, _u32p, _u32p, _u32p, c_uint32, c_void_p, c_uint64,
@@ -495,6 +499,49 @@ class Batch:
             self.destroy()
         except Exception:
             pass
+
+
+class Graph:
+    """A captured stream (qvp_graph_*): `with Graph.capture(stream) as g:` then g.launch(stream)."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+
+    @staticmethod
+    def capture(stream: "Stream"):
+        return _Capture(stream)
+
+    def launch(self, stream=None) -> None:
+        check(load().qvp_graph_launch(self.handle, _sp(stream)))
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(load().qvp_graph_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+
+class _Capture:
+    def __init__(self, stream):
+        self.stream = stream
+        self.graph = Graph(None)
+
+    def __enter__(self) -> Graph:
+        check(load().qvp_graph_begin_capture(_sp(self.stream)))
+        return self.graph
+
+    def __exit__(self, exc_type, exc, tb):
+        h = c_void_p()
+        rc = load().qvp_graph_end_capture(_sp(self.stream), byref(h))
+        if exc_type is None:
+            check(rc)
+            self.graph.handle = h.value
+        return False
 
 
 # qvp_mrope_span: PositionalEncodingSpan with grid extents.
