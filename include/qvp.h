@@ -300,7 +300,8 @@ typedef struct qvp_prefill_args {
 /* Validates everything on the host (the decode's rules, plus q_start[b] <
  * seq_lens[b]), then enqueues the prefill on `stream`. bf16 caches with
  * head_dim 128 and a positive scale run the MFMA prefill kernel; other shapes
- * run the decode kernels over one virtual sequence per new position. */
+ * run the decode kernels over one virtual sequence per new position (packed
+ * in chunks of at most 2^20 block ids, decoded in order on `stream`). */
 int qvp_paged_prefill(const qvp_prefill_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */

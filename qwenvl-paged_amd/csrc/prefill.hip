@@ -41,6 +41,8 @@ constexpr int kPrefillHeadsPerItem = 8;   // two query heads per wave
 constexpr int kHeadBytes = 256;           // 128 bf16
 constexpr int kLdsRow = kHeadBytes + 16;  // padded LDS row of one token's K
 constexpr int kVtRow = 64 + 16;           // padded LDS row of one dim of V^T (32 tokens)
+// Block ids per virtual batch of the decode-kernel path.
+constexpr size_t kMaxVirtualIds = size_t{1} << 20;
 
 // One K/V tile in LDS: K rows as in the frame (token-major), V transposed
 // (dim-major) so each PV operand is one 16-byte read. V^T row n * 16 + x
@@ -387,24 +389,13 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
     // The MFMA kernel takes its running maximum on raw scores: scale > 0.
     if (!(a->scale > 0.0f) || !qvp::prefill_mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
                                                             reinterpret_cast<uintptr_t>(a->kv_base))) {
-        // One virtual sequence per new position, over the same frames.
-        std::vector<uint32_t> ids, cu{0}, ctx;
-        ids.reserve(batch->host_ids.size());
-        for (uint32_t sq = 0; sq < v.num_seqs; ++sq) {
-            const uint32_t* row = batch->host_ids.data() + batch->host_cu_blocks[sq];
-            for (uint32_t pos = a->q_start[sq]; pos < static_cast<uint32_t>(lens[sq]); ++pos) {
-                const uint32_t nb = (pos + a->tokens_per_block) / a->tokens_per_block;
-                ids.insert(ids.end(), row, row + nb);
-                cu.push_back(static_cast<uint32_t>(ids.size()));
-                ctx.push_back(pos + 1);
-            }
-        }
+        // One virtual sequence per new position, over the same frames, run in
+        // chunks of at most kMaxVirtualIds block ids (a long prompt needs
+        // about n^2 / (2 tokens_per_block) of them). Chunks are packed and
+        // decoded in order on the stream; the query and output rows of a
+        // chunk start at its first position's row.
         if (plan.virt == nullptr) QVP_TRY(qvp_batch_create(&plan.virt));
-        QVP_TRY(qvp_pack(plan.virt, static_cast<uint32_t>(ctx.size()), ids.data(), cu.data(), ctx.data(),
-                         a->tokens_per_block, v.num_pool_blocks, v.split_tokens, stream));
         qvp_decode_args d{};
-        d.query = a->query;
-        d.out = a->out;
         d.kv_base = a->kv_base;
         d.block_stride = a->block_stride;
         d.batch = plan.virt;
@@ -421,7 +412,33 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
         d.stream_stride = a->stream_stride;
         d.layer_stride = a->layer_stride;
         d.scale = a->scale;
-        return qvp_paged_decode(&d, stream);
+        const uint64_t row_elems = static_cast<uint64_t>(a->num_query_heads) * a->head_dim;
+        std::vector<uint32_t> ids, cu{0}, ctx;
+        uint64_t first_row = 0;
+        auto flush = [&]() -> int {
+            if (ctx.empty()) return QVP_OK;
+            QVP_TRY(qvp_pack(plan.virt, static_cast<uint32_t>(ctx.size()), ids.data(), cu.data(), ctx.data(),
+                             a->tokens_per_block, v.num_pool_blocks, v.split_tokens, stream));
+            d.query = static_cast<const uint8_t*>(a->query) + first_row * row_elems * esz;
+            d.out = static_cast<uint8_t*>(a->out) + first_row * row_elems * osz;
+            QVP_TRY(qvp_paged_decode(&d, stream));
+            first_row += ctx.size();
+            ids.clear();
+            cu.assign(1, 0);
+            ctx.clear();
+            return QVP_OK;
+        };
+        for (uint32_t sq = 0; sq < v.num_seqs; ++sq) {
+            const uint32_t* row = batch->host_ids.data() + batch->host_cu_blocks[sq];
+            for (uint32_t pos = a->q_start[sq]; pos < static_cast<uint32_t>(lens[sq]); ++pos) {
+                const uint32_t nb = (pos + a->tokens_per_block) / a->tokens_per_block;
+                if (ids.size() + nb > qvp::kMaxVirtualIds) QVP_TRY(flush());
+                ids.insert(ids.end(), row, row + nb);
+                cu.push_back(static_cast<uint32_t>(ids.size()));
+                ctx.push_back(pos + 1);
+            }
+        }
+        return flush();
     }
 
     // Work items, longest context first.

@@ -114,6 +114,17 @@ def test_other_shapes_use_the_decode_path(shape):
     _check(w, got, ref_out, ref32, qvp.DTYPE_F32, f"fallback {shape}")
 
 
+def test_decode_path_runs_long_prompts_in_chunks():
+    # The decode-kernel path packs one virtual sequence per position, at most
+    # 2^20 block ids per pack: a 6000-token prompt (about 1.1M ids) and a
+    # second sequence starting at position 1000 take two chunks, the second
+    # starting mid-sequence, and every row must land in its own place.
+    print("case: prefill decode path, chunked virtual batches", flush=True)
+    w = W.custom([6000, 3000], 4, 2, 64, kv_dtype=qvp.DTYPE_F32, seed=12)
+    got, ref_out, ref32, _ = _run(w, [0, 1000], qvp.DTYPE_F32)
+    _check(w, got, ref_out, ref32, qvp.DTYPE_F32, "chunked decode path")
+
+
 def test_refused_prefill_writes_nothing():
     print("case: prefill refusals", flush=True)
     w = W.custom([40, 20], 28, 4, 128, seed=9)
