@@ -370,6 +370,53 @@ def mrope_bench(steps: int, warmup: int, with_cpu: bool) -> int:
     return 0
 
 
+def swap_bench(steps: int, warmup: int) -> int:
+    """Swap-out (gather) and swap-in (scatter) of whole Qwen2-VL-7B frames
+    (28 layers x K/V x 16 tokens x 4 kv heads x 128 x bf16 = 917,504 B)
+    between a shuffled HBM pool and a pinned host arena, beside a plain
+    contiguous copy of the same bytes through the runtime (the host-link
+    ceiling the swap kernels are bound by)."""
+    frame = 28 * 2 * 16 * 4 * 128 * 2
+    nframes = 1024
+    pool = qvp.BlockPool(nframes, frame)
+    stride = pool.stride
+    cases = []
+    stream = qvp.Stream()
+    for count in (64, 512):
+        total = count * frame
+        arena = qvp.PinnedBuffer(total)
+        frames = W.permutation(count, nframes)[:count].astype(np.uint32)
+        offsets = (np.arange(count, dtype=np.uint64) * frame)
+        dev = qvp.DeviceBuffer(total)
+
+        def timed(fn):
+            for _ in range(max(warmup, 2)):
+                fn()
+            stream.synchronize()
+            e0, e1 = qvp.Event(), qvp.Event()
+            e0.record(stream)
+            for _ in range(steps):
+                fn()
+            e1.record(stream)
+            stream.synchronize()
+            return e0.elapsed_ms(e1) / steps
+
+        g = timed(lambda: qvp.swap_gather(pool.base, stride, nframes, frames, offsets, arena, frame, stream))
+        sc = timed(lambda: qvp.swap_scatter(pool.base, stride, nframes, frames, offsets, arena, frame, stream))
+        d2h = timed(lambda: qvp.check(qvp.load().qvp_memcpy_dtoh(arena.ptr, dev.ptr, total, stream.handle)))
+        h2d = timed(lambda: qvp.check(qvp.load().qvp_memcpy_htod(dev.ptr, arena.ptr, total, stream.handle)))
+        gbs = lambda ms: round(total / (ms * 1e-3) / 1e9, 2)
+        cases.append({"frames": count, "bytes": total, "swap_out_gather_ms": round(g, 4), "swap_out_GBps": gbs(g),
+                      "swap_in_scatter_ms": round(sc, 4), "swap_in_GBps": gbs(sc),
+                      "contiguous_d2h_GBps": gbs(d2h), "contiguous_h2d_GBps": gbs(h2d),
+                      "roofline": {"bound": "host link", "out_frac_of_contiguous": round(d2h / g, 3),
+                                   "in_frac_of_contiguous": round(h2d / sc, 3)}})
+        arena.free()
+    print(json.dumps({"mode": "swap", "kernel": "copy_segments (swap gather/scatter)", "frame_bytes": frame,
+                      "data": "uninitialised HBM frames, shuffled frame ids", "steps": steps, "cases": cases}))
+    return 0
+
+
 def append_bench(steps: int, warmup: int) -> int:
     w = W.config2()
     cases = [append_case("config2 step, one layer", w, 1, 0, 1, steps, warmup),
@@ -394,6 +441,7 @@ def main() -> int:
     ap.add_argument("--append", action="store_true", help="time the K/V append of one config2 step")
     ap.add_argument("--prefill", action="store_true", help="time the causal prefill of 4 x 2048-token prompts")
     ap.add_argument("--mrope", action="store_true", help="time M-RoPE position materialisation")
+    ap.add_argument("--swap", action="store_true", help="time swap-out / swap-in of whole 7B frames")
     ap.add_argument("--torch-sdpa", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
@@ -407,6 +455,8 @@ def main() -> int:
         return prefill_bench(args.steps, args.warmup)
     if args.mrope:
         return mrope_bench(args.steps, args.warmup, not args.no_cpu)
+    if args.swap:
+        return swap_bench(args.steps, args.warmup)
     if args.torch_sdpa:
         print(json.dumps({"ms": torch_sdpa_ms(4, 2048, 28, 4, 128, args.steps, args.warmup)}))
         return 0
