@@ -213,23 +213,29 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     TileRef r2{};
     if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
 
+    // Query B operand: lane (c, j), MFMA i -> Q[head g*G + c][dims 32i + 8j
+    // .. +8]. Columns past the group repeat the group's last head: their
+    // scores, weights and outputs stay in their own columns and are never
+    // written, and not masking leaves the loads' results unused until the
+    // first tile is computed (a select on them would wait at once). The next
+    // piece's query is loaded when a piece starts, so it has arrived when
+    // that piece's first tile is computed.
+    auto load_query = [&](int pi, u32x4 (&qo)[4]) {
+        const qvp_piece d = piece_at(a.pieces, pi);
+        const uint16_t* q = static_cast<const uint16_t*>(p.query) +
+                            (static_cast<uint64_t>(d.b) * p.num_q_heads + (d.g * hps + hl) * G + min(c, G - 1)) * kD;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qo[i] = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
+    };
+    u32x4 qnext[4];
+    if (pb < pe) load_query(pb, qnext);
     for (int pi = pb; pi < pe; ++pi) {
         const qvp_piece d = piece_at(a.pieces, pi);
         const int ctx = d.ctx;
-        const int g = d.g * hps + hl;  // this wave's kv head
-
-        // Query B operand: lane (c, j), MFMA i -> Q[head g*G + c][dims 32i + 8j
-        // .. +8]. Columns past the group repeat the group's last head: their
-        // scores, weights and outputs stay in their own columns and are never
-        // written, and not masking leaves the loads' results unused until the
-        // first tile is computed (a select on them would wait at once).
         u32x4 qop[4];
-        {
-            const uint16_t* q = static_cast<const uint16_t*>(p.query) +
-                                (static_cast<uint64_t>(d.b) * p.num_q_heads + g * G + min(c, G - 1)) * kD;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
-        }
+        for (int i = 0; i < 4; ++i) qop[i] = qnext[i];
+        if (pi + 1 < pe) load_query(pi + 1, qnext);
 
         floatx4 o[8];
 #pragma unroll
