@@ -20,6 +20,9 @@ struct qvp_piece {
 //   wg_begin[num_wgs + 1]  CSR over pieces per workgroup
 //   pieces[num_pieces]     qvp_piece
 //   counters[num_slots]    completion counters (zero between launches)
+//   first[num_wgs][4][8]   per wave: its first tile (piece, tile, kv head, the
+//                          two block ids; piece -1 when it has none) and the
+//                          workgroup's piece range (begin, end)
 struct qvp_schedule {
     bool valid{false};
     uint64_t pack_generation{0};
@@ -30,7 +33,7 @@ struct qvp_schedule {
     uint32_t num_slots{0};
     uint32_t max_partial_pieces_per_wg{0};
     uint32_t hps{1};  // kv heads per segment
-    size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, total{0};  // int32 units
+    size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, off_first{0}, total{0};  // int32 units
     int32_t* staging{nullptr};
     size_t staging_cap{0};
     hipEvent_t staging_done{nullptr};

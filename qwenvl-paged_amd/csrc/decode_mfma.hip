@@ -72,9 +72,13 @@ constexpr int kMaxPartialPerWg = 2;
 constexpr int kMergeChunk = 8;
 constexpr int kMergeBatch = 4;
 
+// Words per wave of the schedule's first-tile table.
+constexpr int kFirstWords = 8;
+
 struct MfmaArgs {
     const qvp_piece* pieces;
     const int32_t* wg_begin;
+    const int32_t* first;  // [wg][wave][kFirstWords]: piece, tile, kv head, blk0, blk1, range begin, end
     int32_t* counters;
     float* ws_ml;   // [slot][hps][group][2] : running max (base 2), running sum
     float* ws_acc;  // [slot][hps][group][128]
@@ -196,19 +200,31 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     const int tlane = wave / hps;
     const int hpsG = hps * G;
 
-    const int pb = as_const(a.wg_begin)[blockIdx.x];
-    const int pe = as_const(a.wg_begin)[blockIdx.x + 1];
+    // The wave's first tile (already resolved to frames by the host) and the
+    // range come in one scalar load, so its first K/V loads issue without a
+    // chain of dependent reads of the schedule and the block table (which
+    // every wave of the grid would make at once at start-up).
+    const auto* fd = as_const(a.first) + (static_cast<int>(blockIdx.x) * kWaves + wave) * kFirstWords;
+    const int pb = fd[5];
+    const int pe = fd[6];
 
     // Software pipeline per wave: while the current tile is computed, the next
     // tile's loads are in flight (nxt) and the block ids of the tile after that
     // are being fetched (r2), so no table lookup sits between a tile's arrival
     // and the issue of the following loads. (pi2, t2) is the cursor of r2.
     KvTile nxt;
-    int pi2 = pb;
-    int t2 = -1;
+    int pi2 = fd[0];
+    int t2 = fd[1];
     bool have_partial = false;
-    bool has2 = next_tile(a, pe, tlane, tl, pi2, t2);
-    if (has2) load_tile(p, resolve_tile(p, a, pi2, t2, hl), c, j, nxt);
+    bool has2 = pi2 >= 0;
+    if (has2) {
+        TileRef r0{};
+        r0.g = fd[2];
+        r0.t = t2;
+        r0.blk0 = fd[3];
+        r0.blk1 = fd[4];
+        load_tile(p, r0, c, j, nxt);
+    }
     has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
     TileRef r2{};
     if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
@@ -631,10 +647,41 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
         max_partial = std::max(max_partial, n);
     }
 
+    // Each wave's first tile, resolved to frames here (the kernel's
+    // next_tile and resolve_tile for its first step).
+    const uint32_t tpb = batch->view.tokens_per_block;
+    uint32_t shift = 0;
+    while ((1u << shift) < tpb) ++shift;
+    std::vector<int32_t> first(static_cast<size_t>(W) * kWaves * kFirstWords, 0);
+    for (uint32_t w = 0; w < W; ++w) {
+        for (int wave = 0; wave < kWaves; ++wave) {
+            int32_t* f = first.data() + (static_cast<size_t>(w) * kWaves + wave) * kFirstWords;
+            const int32_t hl = wave % static_cast<int32_t>(hps);
+            const int32_t tlane = wave / static_cast<int32_t>(hps);
+            f[0] = -1;
+            f[5] = wg_begin[w];
+            f[6] = wg_begin[w + 1];
+            for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
+                const qvp_piece& pc = pieces[pi];
+                if (pc.t0 + tlane >= pc.t1) continue;
+                const int32_t t = pc.t0 + tlane;
+                const uint32_t* row = batch->host_ids.data() + batch->host_cu_blocks[pc.b];
+                const int32_t tok0 = t * kTileTokens;
+                f[0] = pi;
+                f[1] = t;
+                f[2] = pc.g * static_cast<int32_t>(hps) + hl;
+                f[3] = static_cast<int32_t>(row[std::min(tok0, pc.ctx - 1) >> shift]);
+                f[4] = static_cast<int32_t>(row[std::min(tok0 + 16, pc.ctx - 1) >> shift]);
+                break;
+            }
+        }
+    }
+
     s.off_wg_begin = 0;
     s.off_pieces = align_ints(W + 1);
     s.off_counters = s.off_pieces + align_ints(pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)));
-    s.total = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
+    s.off_first = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
+    s.total = s.off_first + align_ints(first.size());
 
     if (s.staging_done == nullptr) QVP_HIP(hipEventCreateWithFlags(&s.staging_done, hipEventDisableTiming));
     if (s.staging_pending) {
@@ -660,6 +707,7 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     std::copy(wg_begin.begin(), wg_begin.end(), h + s.off_wg_begin);
     const int32_t* praw = reinterpret_cast<const int32_t*>(pieces.data());
     std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
+    std::copy(first.begin(), first.end(), h + s.off_first);
     QVP_HIP(hipMemcpyAsync(s.device, h, s.total * sizeof(int32_t), hipMemcpyHostToDevice, stream));
     QVP_HIP(hipEventRecord(s.staging_done, stream));
     s.staging_pending = true;
@@ -688,6 +736,7 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     a.wg_begin = s.device + s.off_wg_begin;
     a.pieces = reinterpret_cast<const qvp_piece*>(s.device + s.off_pieces);
     a.counters = s.device + s.off_counters;
+    a.first = s.device + s.off_first;
     const uint64_t rows = static_cast<uint64_t>(s.num_slots) * s.hps * g.group;
     a.ws_ml = static_cast<float*>(workspace);
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + round_up(rows * 2 * sizeof(float), 256));
