@@ -70,24 +70,26 @@ def cpu_baseline(w: W.Workload, image: np.ndarray, query: np.ndarray, reps: int)
 
     tokens = w.num_seqs
     algo = w.algorithmic_bytes()
+    orc_dtype = O.ORC_F32 if w.kv_dtype == qvp.DTYPE_F32 else O.ORC_BF16
+    tname = "float" if w.kv_dtype == qvp.DTYPE_F32 else "bf16"
     if O.reference_available():
         sess = O.RefSession(image, w.block_stride, w.num_pool_blocks, w.tokens_per_block, w.num_layers,
                             w.num_kv_heads, w.head_dim, w.elem_bytes)
         times = []
         for _ in range(reps):
-            refused, _, secs = sess.decode(w.ids, w.cu_blocks, w.context_lens, O.ORC_BF16, query, w.layer,
+            refused, _, secs = sess.decode(w.ids, w.cu_blocks, w.context_lens, orc_dtype, query, w.layer,
                                            w.num_query_heads, w.head_dim, w.scale)
             assert refused == 0
             times.append(secs)
         sess.close()
         kind = "reference"
-        what = "compiled reference paged_attention_decode<bf16> (oracle/_ref, g++ -O2), one call per sequence"
+        what = f"compiled reference paged_attention_decode<{tname}> (oracle/_ref, g++ -O2), one call per sequence"
     else:
         times = []
         for _ in range(reps):
             t0 = time.perf_counter()
             refused, _, _ = O.decode_batch(image, w.block_stride, w.num_pool_blocks, w.ids, w.cu_blocks,
-                                           w.context_lens, O.ORC_BF16, query, w.layer, w.num_layers,
+                                           w.context_lens, orc_dtype, query, w.layer, w.num_layers,
                                            w.num_query_heads, w.num_kv_heads, w.head_dim, w.tokens_per_block,
                                            w.scale, 1)
             times.append(time.perf_counter() - t0)
@@ -100,7 +102,7 @@ def cpu_baseline(w: W.Workload, image: np.ndarray, query: np.ndarray, reps: int)
         "unit": "GB/s",
         "cores": 1,
         "kind": kind,
-        "sample": f"full config2 batch ({w.num_seqs} sequences, {int(w.context_lens.sum())} cached tokens), "
+        "sample": f"full {w.name} batch ({w.num_seqs} sequences, {int(w.context_lens.sum())} cached tokens), "
                   f"median of {reps} runs of {what} on {cpu_model()} "
                   f"({os.cpu_count()} logical CPUs visible, 1 used)",
         "seconds_per_step": t,
@@ -417,6 +419,54 @@ def swap_bench(steps: int, warmup: int) -> int:
     return 0
 
 
+def fp32_bench(steps: int, warmup: int, cpu_reps: int, with_cpu: bool) -> int:
+    """The config2 batch (same 64 context lengths, Hq28/Hkv4/D128, block 16)
+    with an fp32 cache -- the reference's paged_attention_decode<float> --
+    on the fp32 matrix-core kernel; one step = one decode call (kernel and
+    split merge)."""
+    c2 = W.config2()
+    w = W.custom(list(c2.context_lens), 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=2, spare=0.1)
+    w.name = "config2-shape fp32"
+    rng = np.random.default_rng(2)
+    chunk = rng.normal(0, 0.5, 16_777_259).astype(np.float32)
+    total = w.num_pool_blocks * w.block_stride // 4
+    image = np.tile(chunk, -(-total // chunk.size))[:total].view(np.uint8)
+    query = w.query()
+    pool = qvp.BlockPool(w.num_pool_blocks, w.block_bytes)
+    pool.upload_all(image)
+    q = qvp.DeviceBuffer.from_array(query)
+    out = qvp.DeviceBuffer(w.num_seqs * 28 * 128 * 4)
+    stream = qvp.Stream()
+    batch = qvp.Batch()
+    batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks, 512, stream)
+    ws = qvp.DeviceBuffer(batch.workspace_bytes(28, 128))
+    args = qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=pool.base, block_stride=pool.stride, batch=batch,
+                           kv_dtype=qvp.DTYPE_F32, out_dtype=qvp.DTYPE_F32, layer=0, num_layers=1,
+                           num_query_heads=28, num_kv_heads=4, head_dim=128, tokens_per_block=16, scale=w.scale,
+                           workspace=ws.ptr, workspace_bytes=ws.nbytes)
+    for _ in range(warmup):
+        qvp.paged_decode(args, stream)
+    stream.synchronize()
+    e0, e1 = qvp.Event(), qvp.Event()
+    e0.record(stream)
+    for _ in range(steps):
+        qvp.paged_decode(args, stream)
+    e1.record(stream)
+    stream.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    algo = w.algorithmic_bytes()
+    gbs = algo / (ms * 1e-3) / 1e9
+    line = {"mode": "fp32", "kernel": "decode_f32_grouped + merge_splits", "workload": w.name,
+            "data": "synthetic N(0,1) q, N(0,0.5) K/V, fp32", "steps": steps, "ms_per_step": round(ms, 5),
+            "algorithmic_bytes_per_step": algo, "decode_tokens_per_s": round(w.num_seqs / (ms * 1e-3), 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBPS, 4)}}
+    if with_cpu:
+        line["cpu_baseline"] = cpu_baseline(w, image, query, cpu_reps)
+    print(json.dumps(line))
+    return 0
+
+
 def append_bench(steps: int, warmup: int) -> int:
     w = W.config2()
     cases = [append_case("config2 step, one layer", w, 1, 0, 1, steps, warmup),
@@ -442,6 +492,7 @@ def main() -> int:
     ap.add_argument("--prefill", action="store_true", help="time the causal prefill of 4 x 2048-token prompts")
     ap.add_argument("--mrope", action="store_true", help="time M-RoPE position materialisation")
     ap.add_argument("--swap", action="store_true", help="time swap-out / swap-in of whole 7B frames")
+    ap.add_argument("--fp32", action="store_true", help="time the config2 batch with an fp32 cache")
     ap.add_argument("--torch-sdpa", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
@@ -457,6 +508,8 @@ def main() -> int:
         return mrope_bench(args.steps, args.warmup, not args.no_cpu)
     if args.swap:
         return swap_bench(args.steps, args.warmup)
+    if args.fp32:
+        return fp32_bench(args.steps, args.warmup, args.cpu_reps, not args.no_cpu)
     if args.torch_sdpa:
         print(json.dumps({"ms": torch_sdpa_ms(4, 2048, 28, 4, 128, args.steps, args.warmup)}))
         return 0

@@ -51,6 +51,18 @@ int launch_generic_decode(const DecodeGeometry& g, const qvp_packed_view& v, uin
                           uint32_t out_dtype, void* out, void* workspace, hipEvent_t split_event,
                           hipStream_t stream);
 uint64_t generic_workspace_bytes(const qvp_packed_view& v, uint32_t hq, uint32_t d);
+// Combines the per-split (m, l, O) of the generic workspace layout into the
+// output (one workgroup per (sequence, query head)).
+int launch_merge_splits(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t out_dtype, void* out,
+                        const float* ws_ml, const float* ws_acc, hipStream_t stream);
+
+// fp32 caches, head_dim 128, GQA group <= 16, power-of-two tpb >= 16, splits a
+// multiple of 16 tokens: the fp32 MFMA kernel, one workgroup per (split, kv
+// head), in the generic workspace layout. Returns a qvp_status.
+bool f32_grouped_supported(const DecodeGeometry& g, uint32_t kv_dtype, uint32_t split_tokens, uintptr_t query_addr,
+                           uintptr_t kv_base_addr);
+int launch_f32_grouped_decode(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t out_dtype, void* out,
+                              void* workspace, hipEvent_t split_event, hipStream_t stream);
 
 // MFMA path (bf16, head_dim 128, group <= 16, power-of-two tpb >= 16):
 // persistent workgroups over a balanced schedule built from the batch.

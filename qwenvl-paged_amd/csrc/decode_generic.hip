@@ -167,18 +167,23 @@ int launch_generic_decode(const DecodeGeometry& g, const qvp_packed_view& v, uin
     QVP_HIP(hipGetLastError());
     if (split_event != nullptr) QVP_HIP(hipEventRecord(split_event, stream));
 
+    return launch_merge_splits(g, v, out_dtype, out, sa.ws_ml, sa.ws_acc, stream);
+}
+
+int launch_merge_splits(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t out_dtype, void* out,
+                        const float* ws_ml, const float* ws_acc, hipStream_t stream) {
     const dim3 mgrid(v.num_seqs * g.num_q_heads);
     switch (out_dtype) {
         case QVP_DTYPE_F32:
-            hipLaunchKernelGGL(merge_splits<float>, mgrid, dim3(128), 0, stream, sa.ws_ml, sa.ws_acc, v.cu_splits,
+            hipLaunchKernelGGL(merge_splits<float>, mgrid, dim3(128), 0, stream, ws_ml, ws_acc, v.cu_splits,
                                static_cast<float*>(out), g.num_q_heads, g.head_dim);
             break;
         case QVP_DTYPE_BF16:
-            hipLaunchKernelGGL(merge_splits<uint16_t>, mgrid, dim3(128), 0, stream, sa.ws_ml, sa.ws_acc, v.cu_splits,
+            hipLaunchKernelGGL(merge_splits<uint16_t>, mgrid, dim3(128), 0, stream, ws_ml, ws_acc, v.cu_splits,
                                static_cast<uint16_t*>(out), g.num_q_heads, g.head_dim);
             break;
         default:
-            hipLaunchKernelGGL(merge_splits<_Float16>, mgrid, dim3(128), 0, stream, sa.ws_ml, sa.ws_acc, v.cu_splits,
+            hipLaunchKernelGGL(merge_splits<_Float16>, mgrid, dim3(128), 0, stream, ws_ml, ws_acc, v.cu_splits,
                                static_cast<_Float16*>(out), g.num_q_heads, g.head_dim);
             break;
     }

@@ -159,6 +159,10 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     }
     if (mfma) return qvp::launch_mfma_decode(g, batch, a->out_dtype, a->out, ws, ev, s);
+    if (qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens, reinterpret_cast<uintptr_t>(a->query),
+                                   reinterpret_cast<uintptr_t>(a->kv_base))) {
+        return qvp::launch_f32_grouped_decode(g, v, a->out_dtype, a->out, ws, ev, s);
+    }
     return qvp::launch_generic_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s);
 }
 

@@ -20,11 +20,15 @@ BF16_REL_FLOOR = 1e-3
 
 def tiled_pool_image(w: W.Workload, chunk_elems: int = 16_777_259) -> np.ndarray:
     """A pool image for large workloads, quick to make: one seeded chunk of
-    N(0, kv_sigma^2) bf16 elements repeated over the frames. The chunk length is
-    odd, so no two frames see the same bytes at the same offsets."""
-    assert w.kv_dtype == qvp.DTYPE_BF16 and w.block_stride == w.block_bytes
-    total = w.num_pool_blocks * w.block_bytes // 2
-    chunk = W.f32_to_bf16_bits(np.random.default_rng(w.seed).normal(0.0, w.kv_sigma, chunk_elems).astype(np.float32))
+    N(0, kv_sigma^2) elements of the cache type (bf16 or fp32) repeated over the
+    frames. The chunk length is odd, so no two frames see the same bytes at the
+    same offsets."""
+    assert w.kv_dtype in (qvp.DTYPE_BF16, qvp.DTYPE_F32) and w.block_stride == w.block_bytes
+    esz = qvp.DTYPE_BYTES[w.kv_dtype]
+    total = w.num_pool_blocks * w.block_bytes // esz
+    chunk = np.random.default_rng(w.seed).normal(0.0, w.kv_sigma, chunk_elems).astype(np.float32)
+    if w.kv_dtype == qvp.DTYPE_BF16:
+        chunk = W.f32_to_bf16_bits(chunk)
     reps = -(-total // chunk_elems)
     return np.tile(chunk, reps)[:total].view(np.uint8)
 
