@@ -368,8 +368,8 @@ typedef struct qvp_append_args {
  * KVCacheManager::ensure_token_writable returned the frame. frames / slots are
  * host arrays (slot = token position % tokens_per_block). Refused before
  * anything is enqueued: a frame >= num_blocks (QVP_ERR_UNMAPPED), a slot >=
- * tokens_per_block, a (frame, slot) pair given twice, layers outside
- * num_layers, strides under which two elements coincide or the layout
+ * tokens_per_block, a (frame, slot) pair given twice, more than 2^24 tokens,
+ * layers outside num_layers or more than 65535 of them, strides under which two elements coincide or the layout
  * exceeds block_stride (QVP_ERR_INVALID_ARGUMENT). */
 int qvp_append_kv(const qvp_append_args* args, const uint32_t* frames, const uint32_t* slots,
                   uint32_t count, void* stream);

@@ -10,14 +10,27 @@
 // arena and resume swaps them back, as batched gathers/scatters on the side
 // stream.
 //
+// With --engine 1 every step also does the rest of a serving step's GPU work:
+// admitted prompts get their K/V appended (KVAppendBatch), are attended by one
+// causal prefill (PagedAttentionBatch::prefill) and get M-RoPE positions
+// (MRopePositionBatch); decoding requests append their new token's K/V before
+// the decode and get their position. K/V and queries are synthetic device
+// buffers; each phase is timed with events on the engine stream. The stream
+// idles while the host prepares a phase (validation, the copy-on-write walk,
+// staging uploads), so a phase's event time includes that host work; a
+// kernel trace gives the kernels' own time.
+//
 // Checks at the end: every request finished, the pool and the swap arena are
 // empty again. Output: one JSON line with decode tokens/s over the trace (wall
 // clock, host scheduling and packing included), the decode kernels' own rate,
-// and the swap traffic's rate.
+// and the swap traffic's rate (plus, with --engine, prefill tokens and the
+// time of each phase).
 //
-// Usage: trace_bench [--requests N] [--seed S] [--pool-percent P] [--watermark B]
+// Usage: trace_bench [--requests N] [--seed S] [--pool-percent P] [--watermark B] [--engine 0|1]
 #include "qvp.h"
+#include "qwenvl_paged/KVAppend.h"
 #include "qwenvl_paged/KVCacheManager.h"
+#include "qwenvl_paged/MRope.h"
 #include "qwenvl_paged/MemoryAllocator.h"
 #include "qwenvl_paged/PagedAttention.h"
 #include "qwenvl_paged/Scheduler.h"
@@ -59,6 +72,7 @@ void check(bool ok, const std::string& what) {
 int main(int argc, char** argv) {
     std::uint32_t requests = 200, pool_percent = 60, watermark = 64;
     std::uint64_t seed = 5;
+    bool engine = false;
     for (int i = 1; i + 1 < argc; i += 2) {
         const std::string k = argv[i];
         const std::uint64_t v = std::strtoull(argv[i + 1], nullptr, 10);
@@ -66,6 +80,7 @@ int main(int argc, char** argv) {
         else if (k == "--seed") seed = v;
         else if (k == "--pool-percent") pool_percent = static_cast<std::uint32_t>(v);
         else if (k == "--watermark") watermark = static_cast<std::uint32_t>(v);
+        else if (k == "--engine") engine = v != 0;
     }
     constexpr std::uint32_t kTpb = 16, kHkv = 4, kHq = 28, kD = 128;
     const BlockShape shape{kTpb, 1, kHkv, kD, 2};
@@ -122,6 +137,36 @@ int main(int argc, char** argv) {
     PagedAttentionBatch attn;
     const float scale = 1.0f / std::sqrt(static_cast<float>(kD));
 
+    // Engine mode: synthetic K/V rows, prefill queries/outputs, positions.
+    PagedAttentionBatch prefill_attn;
+    KVAppendBatch append;
+    MRopePositionBatch positions;
+    const std::size_t max_rows = static_cast<std::size_t>(sc.max_batch_tokens) + sc.max_active_requests;
+    void *dk = nullptr, *dv = nullptr, *dpq = nullptr, *dpo = nullptr, *dpos = nullptr;
+    void *ea0 = nullptr, *ea1 = nullptr, *ep0 = nullptr, *ep1 = nullptr, *em0 = nullptr, *em1 = nullptr;
+    if (engine) {
+        const std::size_t row = static_cast<std::size_t>(kHkv) * kD * 2;
+        const std::size_t qrow = static_cast<std::size_t>(kHq) * kD * 2;
+        check(qvp_malloc(&dk, max_rows * row) == QVP_OK && qvp_malloc(&dv, max_rows * row) == QVP_OK &&
+                  qvp_malloc(&dpq, max_rows * qrow) == QVP_OK && qvp_malloc(&dpo, max_rows * qrow) == QVP_OK &&
+                  qvp_malloc(&dpos, max_rows * 3 * sizeof(std::int64_t)) == QVP_OK,
+              "engine buffers");
+        check(qvp_fill_bytes(dk, 0x3b, max_rows * row, stream) == QVP_OK &&
+                  qvp_fill_bytes(dv, 0x3c, max_rows * row, stream) == QVP_OK &&
+                  qvp_fill_bytes(dpq, 0x3c, max_rows * qrow, stream) == QVP_OK,
+              "engine fill");
+        check(qvp_event_create(&ea0) == QVP_OK && qvp_event_create(&ea1) == QVP_OK &&
+                  qvp_event_create(&ep0) == QVP_OK && qvp_event_create(&ep1) == QVP_OK &&
+                  qvp_event_create(&em0) == QVP_OK && qvp_event_create(&em1) == QVP_OK,
+              "engine events");
+    }
+    double append_gpu_ms = 0.0, prefill_gpu_ms = 0.0, mrope_gpu_ms = 0.0;
+    std::uint64_t prefill_tokens = 0;
+    std::vector<SequenceId> app_seq, pos_seq;
+    std::vector<TokenPosition> app_pos, pos_begin, pos_end;
+    std::vector<CacheView> pviews;
+    std::vector<std::uint32_t> plens, pfirst;
+
     for (std::uint32_t i = 0; i < requests; ++i) {
         Request r;
         r.request_id = i + 1;
@@ -167,8 +212,30 @@ int main(int argc, char** argv) {
                 swapped_out_blocks += sched.preemption_info(i + 1)->swapped_blocks;
             }
         }
+        app_seq.clear();
+        app_pos.clear();
+        pos_seq.clear();
+        pos_begin.clear();
+        pos_end.clear();
+        pviews.clear();
+        plens.clear();
+        pfirst.clear();
         for (std::uint64_t id : plan.prefill_requests) {
-            length[id] = plans[id - 1].prompt;
+            const std::uint32_t n = plans[id - 1].prompt;
+            length[id] = n;
+            if (engine) {
+                for (std::uint32_t t = 0; t < n; ++t) {
+                    app_seq.push_back(id);
+                    app_pos.push_back(t);
+                }
+                pviews.push_back(*cache.cache_view(id));
+                plens.push_back(n);
+                pfirst.push_back(0);
+                pos_seq.push_back(id);
+                pos_begin.push_back(0);
+                pos_end.push_back(n);
+                prefill_tokens += n;
+            }
             sched.complete_step(id, 1);
         }
         views.clear();
@@ -183,7 +250,15 @@ int main(int argc, char** argv) {
                 swapped_out_blocks += sched.preemption_info(id)->swapped_blocks;
                 continue;
             }
-            check(cache.ensure_token_writable(id, pos).has_value(), "append");
+            if (engine) {
+                app_seq.push_back(id);
+                app_pos.push_back(pos);
+                pos_seq.push_back(id);
+                pos_begin.push_back(pos);
+                pos_end.push_back(pos + 1);
+            } else {
+                check(cache.ensure_token_writable(id, pos).has_value(), "append");
+            }
             length[id] = pos + 1;
             views.push_back(*cache.cache_view(id));
             lens.push_back(pos + 1);
@@ -198,13 +273,47 @@ int main(int argc, char** argv) {
             check(alloc.flush(), "flush: " + alloc.last_error());
             check(qvp_event_record(es1, stream) == QVP_OK, "record");
         }
+        if (engine && !app_seq.empty()) {
+            // The step's K/V (prompt rows and decode tokens) through the
+            // copy-on-write point: the blocks it shares are copied first, then
+            // one store launch covers every row (offsets uploaded once when
+            // there are more than 128).
+            check(app_seq.size() <= max_rows, "append rows");
+            check(qvp_event_record(ea0, stream) == QVP_OK, "record");
+            check(append.append(cache, alloc, app_seq, app_pos, 0, 1, dk, dv), "append: " + append.last_error());
+            check(qvp_event_record(ea1, stream) == QVP_OK, "record");
+        }
+        if (engine && !pviews.empty()) {
+            check(qvp_event_record(ep0, stream) == QVP_OK, "record");
+            check(prefill_attn.prefill(pviews, plens, pfirst, 0, kHq, scale, dpq, dpo, ElementType::BF16),
+                  "prefill: " + prefill_attn.last_error());
+            check(qvp_event_record(ep1, stream) == QVP_OK, "record");
+        }
         if (!views.empty()) {
             check(qvp_event_record(ed0, stream) == QVP_OK, "record");
             check(attn.decode(views, lens, 0, kHq, scale, dq, dout, ElementType::BF16), attn.last_error());
             check(qvp_event_record(ed1, stream) == QVP_OK, "record");
         }
+        if (engine && !pos_seq.empty()) {
+            check(qvp_event_record(em0, stream) == QVP_OK, "record");
+            check(positions.materialise(cache, pos_seq, pos_begin, pos_end, static_cast<std::int64_t*>(dpos), stream),
+                  "positions: " + positions.last_error());
+            check(qvp_event_record(em1, stream) == QVP_OK, "record");
+        }
         check(qvp_stream_synchronize(stream) == QVP_OK, "sync");
         float ms = 0.f;
+        if (engine && !app_seq.empty()) {
+            check(qvp_event_elapsed_ms(&ms, ea0, ea1) == QVP_OK, "elapsed");
+            append_gpu_ms += ms;
+        }
+        if (engine && !pviews.empty()) {
+            check(qvp_event_elapsed_ms(&ms, ep0, ep1) == QVP_OK, "elapsed");
+            prefill_gpu_ms += ms;
+        }
+        if (engine && !pos_seq.empty()) {
+            check(qvp_event_elapsed_ms(&ms, em0, em1) == QVP_OK, "elapsed");
+            mrope_gpu_ms += ms;
+        }
         if (swaps) {
             check(qvp_event_elapsed_ms(&ms, es0, es1) == QVP_OK, "elapsed");
             swap_gpu_ms += ms;
@@ -235,7 +344,8 @@ int main(int argc, char** argv) {
         "\"decode_tokens_per_s\": %.1f, \"decode_kernel_ms_total\": %.3f, \"decode_tokens_per_s_kernel_only\": "
         "%.1f, \"preemptions\": %llu, \"resumes\": %llu, \"swapped_out_blocks\": %llu, \"swapped_in_blocks\": %llu, "
         "\"swap_bytes\": %.0f, \"swap_ms_total\": %.3f, \"swap_GBps\": %.2f, \"swap_launches\": %llu, "
-        "\"drained\": %s}\n",
+        "\"drained\": %s, \"engine\": %s, \"prefill_tokens\": %llu, \"prefill_kernel_ms_total\": %.3f, "
+        "\"prefill_tokens_per_s_kernel_only\": %.1f, \"append_ms_total\": %.3f, \"mrope_ms_total\": %.3f}\n",
         requests, static_cast<unsigned long long>(finished), static_cast<unsigned long long>(steps), pool,
         static_cast<unsigned long long>(demand_blocks), static_cast<unsigned long long>(decode_tokens),
         static_cast<unsigned long long>(total_output), wall, decode_tokens / wall, decode_gpu_ms,
@@ -243,8 +353,12 @@ int main(int argc, char** argv) {
         static_cast<unsigned long long>(resumes), static_cast<unsigned long long>(swapped_out_blocks),
         static_cast<unsigned long long>(swapped_in_blocks), swap_bytes, swap_gpu_ms,
         swap_gpu_ms > 0 ? swap_bytes / (swap_gpu_ms * 1e-3) / 1e9 : 0.0,
-        static_cast<unsigned long long>(alloc.swap_launches() - swap_launch_before), drained ? "true" : "false");
+        static_cast<unsigned long long>(alloc.swap_launches() - swap_launch_before), drained ? "true" : "false",
+        engine ? "true" : "false", static_cast<unsigned long long>(prefill_tokens), prefill_gpu_ms,
+        prefill_gpu_ms > 0 ? prefill_tokens / (prefill_gpu_ms * 1e-3) : 0.0, append_gpu_ms, mrope_gpu_ms);
     (void)qvp_free(dq);
     (void)qvp_free(dout);
+    for (void* ptr : {dk, dv, dpq, dpo, dpos}) (void)qvp_free(ptr);
+    for (void* ev : {ea0, ea1, ep0, ep1, em0, em1}) (void)qvp_event_destroy(ev);
     return (finished == requests && drained) ? 0 : 2;
 }

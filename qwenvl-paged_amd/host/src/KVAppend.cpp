@@ -40,10 +40,15 @@ bool KVAppendBatch::append(KVCacheManager& cache, MemoryAllocator& allocator, co
 
     // Everything that can be checked without side effects is checked before
     // the first copy-on-write decision.
+    // A prompt's rows come as runs of one sequence: its view is looked up once
+    // per run.
     std::vector<std::pair<SequenceId, TokenPosition>> keys(sequences.size());
+    std::optional<CacheView> view;
     for (std::size_t i = 0; i < sequences.size(); ++i) {
-        const std::optional<CacheView> view = cache.cache_view(sequences[i]);
-        if (!view || !view->valid()) return fail("unknown sequence " + std::to_string(sequences[i]));
+        if (i == 0 || sequences[i] != sequences[i - 1]) {
+            view = cache.cache_view(sequences[i]);
+            if (!view || !view->valid()) return fail("unknown sequence " + std::to_string(sequences[i]));
+        }
         const LogicalBlockIndex index = positions[i] / shape.tokens_per_block;
         if (!view->block_table->lookup(index)) {
             return fail("position " + std::to_string(positions[i]) + " of sequence " + std::to_string(sequences[i]) +
@@ -54,15 +59,24 @@ bool KVAppendBatch::append(KVCacheManager& cache, MemoryAllocator& allocator, co
     std::sort(keys.begin(), keys.end());
     if (std::adjacent_find(keys.begin(), keys.end()) != keys.end()) return fail("a token is given twice");
 
+    // After ensure_token_writable returned a frame for a token, the block is
+    // the sequence's own (KVCacheManager.cpp:104-151 copies a shared block
+    // and remaps it), so the next token of the same (sequence, block) gets the
+    // same frame without a second call.
     frames_.resize(sequences.size());
     slots_.resize(sequences.size());
     for (std::size_t i = 0; i < sequences.size(); ++i) {
-        const std::optional<PhysicalBlockId> frame = cache.ensure_token_writable(sequences[i], positions[i]);
-        if (!frame) {
-            return fail("no writable frame for position " + std::to_string(positions[i]) + " of sequence " +
-                        std::to_string(sequences[i]));
+        const LogicalBlockIndex index = positions[i] / shape.tokens_per_block;
+        if (i > 0 && sequences[i] == sequences[i - 1] && index == positions[i - 1] / shape.tokens_per_block) {
+            frames_[i] = frames_[i - 1];
+        } else {
+            const std::optional<PhysicalBlockId> frame = cache.ensure_token_writable(sequences[i], positions[i]);
+            if (!frame) {
+                return fail("no writable frame for position " + std::to_string(positions[i]) + " of sequence " +
+                            std::to_string(sequences[i]));
+            }
+            frames_[i] = *frame;
         }
-        frames_[i] = *frame;
         slots_[i] = positions[i] % shape.tokens_per_block;
     }
 

@@ -56,8 +56,13 @@ CASES = [
     (16, 1, 8, 128, qvp.DTYPE_BF16, 0, 1, 32, 100),      # config3 shape
     (16, 28, 4, 128, qvp.DTYPE_BF16, 0, 28, 16, 24),     # all 28 layers of a Qwen2-VL-7B frame
     (16, 28, 4, 128, qvp.DTYPE_BF16, 5, 3, 16, 24),      # a layer range
-    (16, 1, 4, 128, qvp.DTYPE_F16, 0, 1, 300, 40),       # several launches of 128 tokens
+    (16, 1, 4, 128, qvp.DTYPE_BF16, 0, 1, 128, 20),      # offsets in the kernel arguments, at the limit
+    (16, 1, 4, 128, qvp.DTYPE_BF16, 0, 1, 129, 20),      # one past: offsets uploaded to the device
+    (16, 1, 4, 128, qvp.DTYPE_F16, 0, 1, 300, 40),       # uploaded offsets
+    (16, 1, 4, 128, qvp.DTYPE_BF16, 0, 1, 6000, 400),    # a prompt's rows in one launch
+    (16, 28, 4, 128, qvp.DTYPE_BF16, 0, 28, 700, 50),    # a prompt's rows, all 28 layers
     (8, 2, 3, 4, qvp.DTYPE_F16, 1, 1, 9, 5),             # 8-byte rows: the byte-copy path
+    (8, 2, 3, 4, qvp.DTYPE_F16, 0, 2, 200, 40),          # byte-copy path with uploaded offsets
     (4, 3, 1, 5, qvp.DTYPE_F32, 0, 3, 7, 3),             # odd head_dim
 ]
 
@@ -75,6 +80,43 @@ def test_append_with_padded_frame_stride():
     print("case: append padded stride", flush=True)
     got, exp, _ = _run(16, 1, 4, 128, qvp.DTYPE_BF16, 0, 1, 20, 30, seed=3, stride_pad=256 + 32)
     assert np.array_equal(got, exp)
+
+
+def test_back_to_back_uploaded_appends_keep_their_offsets():
+    # Calls of the uploaded-offset path enqueued without waiting in between
+    # (growing staging, reusing both staging slots, the kernel-argument path
+    # between them) each write their own rows.
+    print("case: append back to back", flush=True)
+    tpb, layers, hkv, d = 16, 1, 4, 128
+    nframes = 600
+    rng = np.random.default_rng(11)
+    pool = qvp.BlockPool(nframes, tpb * layers * hkv * d * 2 * 2)
+    image = rng.integers(0, 256, nframes * pool.stride, dtype=np.uint8)
+    pool.upload_all(image)
+    stream = qvp.Stream()
+    exp = image.copy()
+    pairs = rng.permutation(nframes * tpb)
+    used = 0
+    keep = []
+    for count in (200, 5000, 40, 300, 9000, 129):
+        sel = pairs[used:used + count]
+        used += count
+        frames, slots = (sel // tpb).astype(np.uint32), (sel % tpb).astype(np.uint32)
+        k = rng.integers(0, 256, count * hkv * d * 2, dtype=np.uint8)
+        v = rng.integers(0, 256, count * hkv * d * 2, dtype=np.uint8)
+        dk, dv = qvp.DeviceBuffer.from_array(k), qvp.DeviceBuffer.from_array(v)
+        keep.append((dk, dv))
+        args = qvp.append_args(kv_base=pool.base, block_stride=pool.stride, num_blocks=nframes,
+                               kv_dtype=qvp.DTYPE_BF16, num_layers=layers, first_layer=0, layer_count=layers,
+                               num_kv_heads=hkv, head_dim=d, tokens_per_block=tpb, k=dk.ptr, v=dv.ptr)
+        qvp.append_kv(args, frames, slots, stream)
+        # The host arrays may be reused at once: the call staged the offsets.
+        frames[:] = 0
+        slots[:] = 0
+        assert O.append_kv(exp, pool.stride, nframes, 2, tpb, layers, hkv, d, 0, layers,
+                           (sel // tpb).astype(np.uint32), (sel % tpb).astype(np.uint32), k, v) == 0
+    stream.synchronize()
+    assert np.array_equal(pool.download_all(), exp)
 
 
 def test_refused_appends_write_nothing():
