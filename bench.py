@@ -14,7 +14,10 @@ algorithmic HBM bytes per step / step time. The pack-inclusive rate (host pack
 + pinned H2D + decode) is reported beside it as `step_with_pack_*`.
 
 `roofline` uses the decode kernel's own average duration, measured with HIP
-events recorded on the decode stream around it. `cpu_baseline` times the
+events recorded on the decode stream around it. `read_ceiling` is a plain
+streaming read of the same byte count (no gather, no math) on this device:
+the rate any kernel reading those bytes once reaches, launch ramp and drain
+included, and the decode kernel's rate as a fraction of it. `cpu_baseline` times the
 compiled reference paged_attention_decode<T> (oracle/_ref) on this host over
 the same batch, single-threaded like the reference engine loop.
 
@@ -485,6 +488,7 @@ def main() -> int:
     ap.add_argument("--pools", type=int, default=3, help="independent pool copies rotated between steps")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-probe", action="store_true", help="skip the HBM read-ceiling probe")
     ap.add_argument("--workload", choices=["config2", "config3"], default="config2")
     ap.add_argument("--cow", action="store_true", help="run the copy-on-write configuration driver")
     ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
@@ -646,10 +650,56 @@ def main() -> int:
         },
         "setup_s": round(setup_s, 2),
     }
+    if not args.no_probe:
+        probe = read_probe(kernel_bytes)
+        probe["kernel_frac_of_probe"] = round(achieved / probe["read_GBps"], 4)
+        line["read_ceiling"] = probe
     if not args.no_cpu and args.workload == "config2":
         line["cpu_baseline"] = cpu_baseline(w, image, query, args.cpu_reps)
     print(json.dumps(line))
     return 0
+
+
+def read_probe(nbytes: int, reps: int = 20, buffers: int = 3) -> dict:
+    """Practical HBM read ceiling for a kernel that reads `nbytes` once: a plain
+    streaming read (csrc/hbm_probe.hip, libqvp_probe.so) over `buffers`
+    rotating buffers of that size, several launch shapes, HIP events on the
+    probe's stream; the fastest shape's median duration counts."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(ROOT / "qwenvl-paged_amd" / "libqvp_probe.so"))
+    lib.qvp_probe_read.restype = ctypes.c_int
+    lib.qvp_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                                   ctypes.c_void_p, ctypes.c_void_p]
+    nbytes = nbytes // 16 * 16
+    bufs = [qvp.DeviceBuffer(nbytes) for _ in range(buffers)]
+    stream = qvp.Stream()
+    for b in bufs:
+        b.fill(0x5A, stream)
+    shapes = [(wgs, u) for wgs in (256, 512, 1024, 2048, 4096) for u in (1, 2, 4, 8, 16)]
+    sink = qvp.DeviceBuffer(max(w for w, _ in shapes) * 256 * 4)
+    best = None
+    for wgs, unroll in shapes:
+        times = []
+        for i in range(reps + 3):
+            e0, e1 = qvp.Event(), qvp.Event()
+            e0.record(stream)
+            if lib.qvp_probe_read(bufs[i % buffers].ptr, nbytes, wgs, unroll, sink.ptr, stream.handle) != 0:
+                raise RuntimeError("probe launch refused")
+            e1.record(stream)
+            stream.synchronize()
+            if i >= 3:
+                times.append(e0.elapsed_ms(e1))
+        med = statistics.median(times)
+        if os.environ.get("QVP_PROBE_VERBOSE"):
+            print(json.dumps({"probe_wgs": wgs, "unroll": unroll, "ms": round(med, 5),
+                              "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}), file=sys.stderr)
+        if best is None or med < best[0]:
+            best = (med, wgs, unroll)
+    ms, wgs, unroll = best
+    return {"read_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes, "ms": round(ms, 5),
+            "shape": f"{wgs} workgroups x 256 threads, {unroll} 16-byte loads in flight per thread",
+            "frac_of_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}
 
 
 if __name__ == "__main__":

@@ -75,6 +75,17 @@ def build_hip_library() -> Path:
     return LIB
 
 
+PROBE_LIB = PKG / "libqvp_probe.so"
+
+
+def build_probe_library() -> Path:
+    """The benchmark's HBM read-rate probe (csrc/hbm_probe.hip), a library of its own."""
+    tmp = PROBE_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", str(tmp), str(PKG / "csrc" / "hbm_probe.hip")])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def build_oracle() -> None:
     make = shutil.which("make") or "make"
     _run([make, "-s", "-C", str(ROOT / "oracle")])
@@ -82,6 +93,7 @@ def build_oracle() -> None:
 
 def build_all() -> None:
     build_hip_library()
+    build_probe_library()
     build_oracle()
     host = PKG / "host" / "build_host.py"
     if host.exists():

@@ -79,8 +79,9 @@ def test_grouped_query_head_shapes(hq, hkv):
         [32768],                               # one long segment cut across every workgroup
         list(range(1, 301)),                   # many tiny segments: several pieces per workgroup
         [4096] * 3 + [1] * 50 + [777] * 7,     # mixed
+        [1 + (i * 37) % 64 for i in range(4000)],  # dozens of pieces per range: LDS state sets reused
     ],
-    ids=["single-token", "one-long", "many-tiny", "mixed"],
+    ids=["single-token", "one-long", "many-tiny", "mixed", "many-short"],
 )
 def test_balanced_schedule_shapes(lens):
     print(f"case: schedule shape with {len(lens)} sequences", flush=True)
