@@ -20,7 +20,7 @@ struct qvp_piece {
 //   wg_begin[num_wgs + 1]  CSR over pieces per workgroup
 //   pieces[num_pieces]     qvp_piece
 //   counters[num_slots]    completion counters (zero between launches)
-//   first[num_wgs][4][8]   per wave: its first tile (piece, tile, kv head, the
+//   first[num_wgs][8][8]   per wave: its first tile (piece, tile, kv head, the
 //                          two block ids; piece -1 when it has none) and the
 //                          workgroup's piece range (begin, end)
 struct qvp_schedule {

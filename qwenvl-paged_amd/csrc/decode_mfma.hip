@@ -6,11 +6,12 @@
 // Work decomposition. Every (sequence b, kv head g) pair is a segment of
 // ceil(len_b / 32) tiles of 32 tokens. The host lays the sequences' tiles end
 // to end and cuts them into equal-sized contiguous ranges, one per workgroup
-// and kv head (two resident workgroups per CU, launched once: no tail of
-// half-empty rounds, no per-item start-up cost); the workgroups of one range
+// and kv head (one resident workgroup of eight waves per CU, launched once:
+// no tail of half-empty rounds, no per-item start-up cost, and no CU-mate
+// workgroup whose loads queue behind another's); the workgroups of one range
 // have consecutive ids, so a frame's kv heads are read side by side. A range
-// covers one or more pieces (its intersection with segments). Inside a piece the four waves of the
-// workgroup take tiles round-robin, keep an online-softmax state (running max
+// covers one or more pieces (its intersection with segments). Inside a piece
+// the waves of the workgroup take tiles round-robin, keep an online-softmax state (running max
 // m, running sum l, unnormalised accumulator O) and merge it through LDS when
 // the piece ends. A piece that is a whole segment writes the final output; the
 // other pieces write (m, l, O) to a workspace slot with agent-scope stores,
@@ -55,16 +56,18 @@
 namespace qvp {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kD = 128;
 constexpr int kRowPad = kD + 4;
-constexpr int kWgsPerCu = 2;
+// One workgroup of eight waves per CU. Two four-wave workgroups per CU (the
+// same waves) were measured 5% slower on the 72B shape: the dispatcher starts
+// a CU's second workgroup after every CU has its first, and its waves then
+// lose issue arbitration to the older ones.
+constexpr int kWgsPerCu = 1;
 // Tiles per wave (whole batch over the resident waves) from which kv heads are
 // decoded four side by side.
 constexpr uint64_t kMinTilesPerWaveForHeadGroups = 32;
-// Share of a first-round workgroup's tiles given to a second-round one.
-constexpr double kSecondRoundShare = 0.72;
 // A workgroup's range is contiguous, so only its first and last pieces can be
 // partial segments.
 constexpr int kMaxPartialPerWg = 2;
@@ -283,37 +286,8 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         have_partial = have_partial || slot >= 0;
         OutT* out = static_cast<OutT*>(a.out);
         const uint64_t out_row0 = (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * hpsG) * kD;
-        if (tl == 1) {
-            // The wave holds the whole piece for its head: it writes its rows
-            // itself, with no workgroup barrier (its own LDS writes are visible
-            // to its own later reads).
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            for (int e = lane; e < G * kD; e += 64) {
-                const int hc = e >> 7;
-                const int dd = e & (kD - 1);
-                const float acc = sm_o[wave][hc][dd];
-                if (slot < 0) {
-                    out[out_row0 + static_cast<uint64_t>(hl * G + hc) * kD + dd] = from_float<OutT>(acc / sm_l[wave][hc]);
-                } else {
-                    // Agent-scope stores are written through to the point of
-                    // coherence shared by all XCDs; the wait before the count-in
-                    // makes sure they have arrived.
-                    const uint64_t row = static_cast<uint64_t>(slot) * hpsG + hl * G + hc;
-                    __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (dd == 0) {
-                        __hip_atomic_store(&a.ws_ml[row * 2 + 0], sm_m[wave][hc], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                        __hip_atomic_store(&a.ws_ml[row * 2 + 1], sm_l[wave][hc], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
-            }
-            // Later writes of this wave's LDS rows come after these reads.
-            __builtin_amdgcn_wave_barrier();
-        } else if (hps == 1) {
-            // The four waves are tile lanes of one head: merge them through LDS.
+        if (hps == 1) {
+            // The eight waves are tile lanes of one head: merge them through LDS.
             lds_barrier();
             for (int e = threadIdx.x; e < G * kD; e += kThreads) {
                 const int hc = e >> 7;
@@ -342,7 +316,10 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
             }
             lds_barrier();
         } else {
-            // Two heads of two tile lanes each: merge the lanes through LDS.
+            // hps heads of kWaves / hps tile lanes each: merge each head's lanes
+            // through LDS. Slot stores are agent-scope: written through to the
+            // point of coherence shared by all XCDs (the wait before the
+            // count-in makes sure they have arrived).
             lds_barrier();
             for (int e = threadIdx.x; e < hpsG * kD; e += kThreads) {
                 const int ri = e >> 7;  // row within the segment: head ri / G, query column ri % G
@@ -380,7 +357,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     // for outstanding stores, so each wave first waits for all of its memory
     // operations (the slot stores are agent-scope stores: they are complete
     // once written through to the point of coherence), and the barrier then
-    // orders all four waves' stores before any counter moves. The asm's
+    // orders all the waves' stores before any counter moves. The asm's
     // memory clobber keeps the compiler from moving memory accesses across
     // the wait.
     // Only the first and the last piece of a contiguous range can be partial
@@ -492,7 +469,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     }
 }
 
-// Resident workgroups per device (two per CU), cached per device ordinal.
+// Resident workgroups per device (one per CU), cached per device ordinal.
 std::mutex g_dev_mutex;
 std::vector<uint32_t> g_dev_wgs;
 
@@ -513,9 +490,9 @@ int device_max_wgs(uint32_t* wgs) {
 size_t align_ints(size_t n) { return (n + 63) / 64 * 64; }
 
 // kv heads decoded side by side by one workgroup. Four (when they divide the
-// kv head count) lets each wave own one head of the same tiles: no per-piece
-// merge of the waves' states and whole token rows read together. But a
-// segment then spans four heads, so the batch is cut into 4x fewer, longer
+// kv head count) gives each head two tile lanes of the same tiles: whole
+// token rows are read together and each piece end merges only two lanes. But
+// a segment then spans four heads, so the batch is cut into 4x fewer, longer
 // segments and each split segment gathers more, larger slots in its final
 // merge; that pays only when every wave streams many tiles (long contexts).
 uint32_t head_group_size(uint32_t num_kv_heads, uint64_t tiles_per_head, uint32_t max_wgs) {
@@ -554,8 +531,8 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     s.valid = false;
 
     // Segments (b, q): sequence b's kv heads q * hps .. q * hps + hps - 1. With
-    // hps kv heads per segment the four waves of a workgroup split as hps
-    // heads x (4 / hps) tile lanes. Every segment of sequence b has the same
+    // hps kv heads per segment the eight waves of a workgroup split as hps
+    // heads x (8 / hps) tile lanes. Every segment of sequence b has the same
     // tiles, so the tile positions of all sequences laid end to end (T per
     // head group) are cut into R ranges, and workgroup r * nq + q takes range
     // r of head group q: the nq workgroups that read a token's kv heads run
@@ -576,20 +553,10 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
         std::min<uint64_t>(std::max<uint32_t>(1, max_wgs / nq), std::max<uint64_t>(1, (T + tl - 1) / tl)));
     const uint32_t W = R * nq;
 
-    // The dispatcher places workgroups 0 .. CUs - 1 first, one per CU, and the
-    // second workgroup of a CU issues its loads behind the first one's (older
-    // waves win the CU's issue arbitration): measured on config2, its first
-    // tile arrives ~6 us later and it streams ~20% slower while its CU-mate
-    // runs. Giving it kSecondRoundShare of a first-round range makes the two
-    // finish closer together (~4% shorter kernel).
-    const uint32_t first_round = std::min(R, std::max<uint32_t>(1, max_wgs / kWgsPerCu / nq));
-    const double units = first_round + (R - first_round) * kSecondRoundShare;
+    // Every workgroup is resident from the start (one per CU), so the ranges
+    // are equal.
     std::vector<uint64_t> bound(R + 1, 0);
-    for (uint32_t r = 1; r < R; ++r) {
-        const double before =
-            std::min<double>(r, first_round) + (r > first_round ? (r - first_round) * kSecondRoundShare : 0.0);
-        bound[r] = std::min<uint64_t>(T, static_cast<uint64_t>(T * before / units + 0.5));
-    }
+    for (uint32_t r = 1; r < R; ++r) bound[r] = T * r / R;
     bound[R] = T;
     std::vector<int32_t> wg_begin(W + 1);
     std::vector<qvp_piece> pieces;
