@@ -68,7 +68,7 @@ int launch_f32_grouped_decode(const DecodeGeometry& g, const qvp_packed_view& v,
 // persistent workgroups over a balanced schedule built from the batch.
 bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr,
                     uintptr_t kv_base_addr);
-int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t stream);
+int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream);
 uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim);
 int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t out_dtype, void* out,
                        void* workspace, hipEvent_t split_event, hipStream_t stream);

@@ -501,6 +501,40 @@ uint32_t head_group_size(uint32_t num_kv_heads, uint64_t tiles_per_head, uint32_
     return num_kv_heads % 4 == 0 ? 4u : (num_kv_heads % 2 == 0 ? 2u : 1u);
 }
 
+// Relative streaming cost of kv head group q (hps heads from q * hps). On
+// MI355X the bytes at offsets 256 .. 511 of every 1 KiB of device address
+// space stream slower than the rest when the 256-byte slices of a 1 KiB row
+// are read by different workgroups (Qwen2-VL-7B layout, one kv head per
+// workgroup: the head-1 workgroups ran 15-18% longer than the others in
+// per-workgroup timestamps, on every box measured; with the frame stride
+// padded by 256 bytes the slowness moved with the address, not with the
+// head). A head's weight is 1 + kSlowSliceCost x the fraction of its bytes in
+// that slice, over the four token rows that repeat the pattern; the
+// classes are fixed only when the pool base, the frame stride and the K/V
+// offsets are multiples of 1 KiB and the token and head strides multiples
+// of 256 bytes, otherwise every group weighs the same. Groups that cover
+// whole kilobytes (four heads of 256 bytes) weigh the same as each other.
+constexpr double kSlowSliceCost = 0.25;
+std::vector<double> head_group_weights(const DecodeGeometry& g, uint32_t hps, uint32_t nq) {
+    std::vector<double> w(nq, 1.0);
+    const uint64_t base = reinterpret_cast<uintptr_t>(g.kv_base);
+    if (base % 1024 != 0 || g.block_stride % 1024 != 0 || g.k_off % 1024 != 0 || g.v_off % 1024 != 0 ||
+        g.token_stride % 256 != 0 || g.head_stride % 256 != 0 || g.head_stride * hps >= 1024) {
+        return w;
+    }
+    for (uint32_t q = 0; q < nq; ++q) {
+        double slow = 0.0;
+        for (uint32_t h = q * hps; h < (q + 1) * hps; ++h) {
+            for (uint64_t t = 0; t < 4; ++t) {
+                const uint64_t off = (h * g.head_stride + t * g.token_stride) % 1024;
+                if (off >= 256 && off < 512) slow += 1.0;
+            }
+        }
+        w[q] = 1.0 + kSlowSliceCost * slow / (4.0 * hps);
+    }
+    return w;
+}
+
 }  // namespace
 
 void destroy_schedule(qvp_schedule& s) {
@@ -520,25 +554,11 @@ bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_
            aligned;
 }
 
-int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t stream) {
+int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream) {
+    const uint32_t num_kv_heads = g.num_kv_heads;
     qvp_schedule& s = batch->sched;
     uint32_t max_wgs = 0;
     QVP_TRY(device_max_wgs(&max_wgs));
-    if (s.valid && s.pack_generation == batch->generation && s.num_kv_heads == num_kv_heads &&
-        s.max_wgs == max_wgs) {
-        return QVP_OK;
-    }
-    s.valid = false;
-
-    // Segments (b, q): sequence b's kv heads q * hps .. q * hps + hps - 1. With
-    // hps kv heads per segment the eight waves of a workgroup split as hps
-    // heads x (8 / hps) tile lanes. Every segment of sequence b has the same
-    // tiles, so the tile positions of all sequences laid end to end (T per
-    // head group) are cut into R ranges, and workgroup r * nq + q takes range
-    // r of head group q: the nq workgroups that read a token's kv heads run
-    // side by side (consecutive ids start together), so the rows of a frame
-    // are read close together in time instead of once per head at unrelated
-    // times (measured on config2: -1.3 us).
     const std::vector<int32_t>& lens = batch->host_seq_lens;
     std::vector<uint64_t> pos_cum(lens.size() + 1, 0);
     for (size_t b = 0; b < lens.size(); ++b) {
@@ -547,43 +567,82 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     const uint64_t T = pos_cum[lens.size()];
     const uint32_t hps = head_group_size(num_kv_heads, T, max_wgs);
     const uint32_t nq = num_kv_heads / hps;
+    const std::vector<double> weights = head_group_weights(g, hps, nq);
+    if (s.valid && s.pack_generation == batch->generation && s.num_kv_heads == num_kv_heads &&
+        s.max_wgs == max_wgs && s.weights == weights) {
+        return QVP_OK;
+    }
+    s.valid = false;
+
+    // Segments (b, q): sequence b's kv heads q * hps .. q * hps + hps - 1. With
+    // hps kv heads per segment the eight waves of a workgroup split as hps
+    // heads x (8 / hps) tile lanes. Every segment of sequence b has the same
+    // tiles, so the tile positions of all sequences laid end to end (T per
+    // head group) are cut into R_q equal ranges per head group q, R_q in
+    // proportion to the group's streaming weight (all equal unless some kv
+    // heads sit in the slower address slice). Every workgroup is resident
+    // from the start (one per CU). Workgroup ids follow the ranges' start
+    // positions, head group breaking ties, so consecutive ids -- which the
+    // dispatcher places on consecutive XCDs -- read the kv heads of
+    // neighbouring tokens (measured on config2: 1.3 us faster than one XCD
+    // per token's heads).
     const uint64_t tl = kWaves / hps;
     // At least one tile per tile lane, at least one range.
     const uint32_t R = static_cast<uint32_t>(
         std::min<uint64_t>(std::max<uint32_t>(1, max_wgs / nq), std::max<uint64_t>(1, (T + tl - 1) / tl)));
     const uint32_t W = R * nq;
-
-    // Every workgroup is resident from the start (one per CU), so the ranges
-    // are equal.
-    std::vector<uint64_t> bound(R + 1, 0);
-    for (uint32_t r = 1; r < R; ++r) bound[r] = T * r / R;
-    bound[R] = T;
-    std::vector<int32_t> wg_begin(W + 1);
-    std::vector<qvp_piece> pieces;
-    pieces.reserve(static_cast<size_t>(W) + lens.size() * nq);
-    for (uint32_t r = 0; r < R; ++r) {
+    std::vector<uint32_t> Rq(nq, R);
+    if (R >= 2) {
+        double wsum = 0.0;
+        for (double x : weights) wsum += x;
+        uint32_t given = 0;
         for (uint32_t q = 0; q < nq; ++q) {
-            wg_begin[r * nq + q] = static_cast<int32_t>(pieces.size());
-            uint64_t pos = bound[r];
-            size_t b = static_cast<size_t>(std::upper_bound(pos_cum.begin(), pos_cum.end(), pos) - pos_cum.begin()) - 1;
-            while (pos < bound[r + 1]) {
-                while (pos_cum[b + 1] <= pos) ++b;
-                const uint64_t end = std::min(bound[r + 1], pos_cum[b + 1]);
-                qvp_piece pc{};
-                pc.b = static_cast<int32_t>(b);
-                pc.g = static_cast<int32_t>(q);
-                pc.t0 = static_cast<int32_t>(pos - pos_cum[b]);
-                pc.t1 = static_cast<int32_t>(end - pos_cum[b]);
-                pc.ctx = lens[b];
-                pc.slot = -1;
-                pc.seg_slot0 = -1;
-                pc.seg_nslots = 0;
-                pieces.push_back(pc);
-                pos = end;
-            }
+            Rq[q] = std::max<uint32_t>(1, static_cast<uint32_t>(W * weights[q] / wsum + 0.5));
+            given += Rq[q];
+        }
+        // Rounding leftovers go to (or come from) the heaviest group.
+        const uint32_t heavy = static_cast<uint32_t>(std::max_element(weights.begin(), weights.end()) - weights.begin());
+        Rq[heavy] = static_cast<uint32_t>(std::max<int64_t>(1, static_cast<int64_t>(Rq[heavy]) + W - given));
+        for (uint32_t q = 0; q < nq; ++q) Rq[q] = static_cast<uint32_t>(std::min<uint64_t>(Rq[q], std::max<uint64_t>(1, (T + tl - 1) / tl)));
+    }
+
+    struct RangeRef {
+        uint64_t begin, end;
+        uint32_t q;
+    };
+    std::vector<RangeRef> ranges;
+    for (uint32_t q = 0; q < nq; ++q) {
+        for (uint32_t r = 0; r < Rq[q]; ++r) ranges.push_back({T * r / Rq[q], T * (r + 1) / Rq[q], q});
+    }
+    std::stable_sort(ranges.begin(), ranges.end(), [](const RangeRef& x, const RangeRef& y) {
+        return x.begin != y.begin ? x.begin < y.begin : x.q < y.q;
+    });
+    const uint32_t Wn = static_cast<uint32_t>(ranges.size());
+    std::vector<int32_t> wg_begin(Wn + 1);
+    std::vector<qvp_piece> pieces;
+    pieces.reserve(static_cast<size_t>(Wn) + lens.size() * nq);
+    for (uint32_t w = 0; w < Wn; ++w) {
+        const RangeRef& rr = ranges[w];
+        wg_begin[w] = static_cast<int32_t>(pieces.size());
+        uint64_t pos = rr.begin;
+        size_t b = static_cast<size_t>(std::upper_bound(pos_cum.begin(), pos_cum.end(), pos) - pos_cum.begin()) - 1;
+        while (pos < rr.end) {
+            while (pos_cum[b + 1] <= pos) ++b;
+            const uint64_t end = std::min(rr.end, pos_cum[b + 1]);
+            qvp_piece pc{};
+            pc.b = static_cast<int32_t>(b);
+            pc.g = static_cast<int32_t>(rr.q);
+            pc.t0 = static_cast<int32_t>(pos - pos_cum[b]);
+            pc.t1 = static_cast<int32_t>(end - pos_cum[b]);
+            pc.ctx = lens[b];
+            pc.slot = -1;
+            pc.seg_slot0 = -1;
+            pc.seg_nslots = 0;
+            pieces.push_back(pc);
+            pos = end;
         }
     }
-    wg_begin[W] = static_cast<int32_t>(pieces.size());
+    wg_begin[Wn] = static_cast<int32_t>(pieces.size());
 
     // The pieces of a segment (b, q) lie in workgroups r * nq + q for
     // consecutive r; whole-segment pieces need no slot. A split segment's
@@ -617,7 +676,7 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     }
     // The kernel counts in only the first and the last piece of a range.
     uint32_t max_partial = 0;
-    for (uint32_t w = 0; w < W; ++w) {
+    for (uint32_t w = 0; w < Wn; ++w) {
         uint32_t n = 0;
         for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
             if (pieces[pi].slot < 0) continue;
@@ -634,8 +693,8 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     const uint32_t tpb = batch->view.tokens_per_block;
     uint32_t shift = 0;
     while ((1u << shift) < tpb) ++shift;
-    std::vector<int32_t> first(static_cast<size_t>(W) * kWaves * kFirstWords, 0);
-    for (uint32_t w = 0; w < W; ++w) {
+    std::vector<int32_t> first(static_cast<size_t>(Wn) * kWaves * kFirstWords, 0);
+    for (uint32_t w = 0; w < Wn; ++w) {
         for (int wave = 0; wave < kWaves; ++wave) {
             int32_t* f = first.data() + (static_cast<size_t>(w) * kWaves + wave) * kFirstWords;
             const int32_t hl = wave % static_cast<int32_t>(hps);
@@ -660,7 +719,7 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     }
 
     s.off_wg_begin = 0;
-    s.off_pieces = align_ints(W + 1);
+    s.off_pieces = align_ints(Wn + 1);
     s.off_counters = s.off_pieces + align_ints(pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)));
     s.off_first = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
     s.total = s.off_first + align_ints(first.size());
@@ -697,7 +756,8 @@ int mfma_prepare_schedule(qvp_batch* batch, uint32_t num_kv_heads, hipStream_t s
     s.pack_generation = batch->generation;
     s.num_kv_heads = num_kv_heads;
     s.max_wgs = max_wgs;
-    s.num_wgs = W;
+    s.weights = weights;
+    s.num_wgs = Wn;
     s.num_pieces = static_cast<uint32_t>(pieces.size());
     s.num_slots = static_cast<uint32_t>(next_slot);
     s.hps = hps;

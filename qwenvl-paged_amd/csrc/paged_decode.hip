@@ -144,7 +144,7 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
                                           reinterpret_cast<uintptr_t>(a->kv_base));
     uint64_t need = 0;
     if (mfma) {
-        QVP_TRY(qvp::mfma_prepare_schedule(batch, a->num_kv_heads, s));
+        QVP_TRY(qvp::mfma_prepare_schedule(batch, g, s));
         need = qvp::mfma_workspace_bytes(batch, g.group, g.head_dim);
     } else {
         need = qvp::generic_workspace_bytes(v, a->num_query_heads, a->head_dim);
