@@ -34,6 +34,8 @@ struct qvp_schedule {
     uint32_t max_partial_pieces_per_wg{0};
     uint32_t hps{1};  // kv heads per segment
     std::vector<double> weights;  // streaming weight per kv-head group the ranges were cut for
+    bool defer{false};            // piece results held in LDS until a range is done
+    uint32_t lds_bytes{0};        // dynamic LDS per workgroup for them
     size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, off_first{0}, total{0};  // int32 units
     int32_t* staging{nullptr};
     size_t staging_cap{0};

@@ -83,6 +83,12 @@ constexpr int kMergeBatch = 4;
 // shortened that kernel by ~2 us (0.3 to 0.6 measured, smooth).
 constexpr double kPieceBoundaryTiles = 0.5;
 
+// LDS of one workgroup: the CU's 160 KiB (one workgroup per CU), of which the
+// kernel's static arrays take kStaticLdsBytes; the rest can hold deferred
+// piece results.
+constexpr uint32_t kMaxLdsBytes = 160u * 1024u;
+constexpr uint32_t kStaticLdsBytes = (2 * kWaves * 16 + kWaves * 16 * kRowPad) * 4 + 64;
+
 // Words per wave of the schedule's first-tile table.
 constexpr int kFirstWords = 8;
 
@@ -95,6 +101,7 @@ struct MfmaArgs {
     float* ws_acc;  // [slot][hps][group][128]
     void* out;      // [num_seqs][Hq][128]
     int hps;        // kv heads per segment (4, 2 or 1)
+    int defer;      // hold piece results in LDS and write them after the range
 };
 
 
@@ -198,6 +205,9 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     __shared__ float sm_l[kWaves][16];
     __shared__ float sm_o[kWaves][16][kRowPad];
     __shared__ int sm_merge[kMaxPartialPerWg];
+    // Piece results held until the range is done (a.defer): [piece][hps *
+    // G][kD] accumulators, then [piece][hps * G][2] (m, l).
+    extern __shared__ float sm_def[];
 
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -218,6 +228,42 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     const auto* fd = as_const(a.first) + (static_cast<int>(blockIdx.x) * kWaves + wave) * kFirstWords;
     const int pb = fd[5];
     const int pe = fd[6];
+    float* def_acc = sm_def;
+    float* def_ml = sm_def + (pe - pb) * hpsG * kD;
+    OutT* out = static_cast<OutT*>(a.out);
+
+    // Writes element (ri, dd) of a piece's merged state: the output row when
+    // the piece is a whole segment, else its workspace slot, with agent-scope
+    // stores (written through to the point of coherence shared by all XCDs;
+    // the wait before the count-in makes sure they have arrived).
+    auto store_result = [&](const qvp_piece& d, int ri, int dd, float acc, float mmax, float lsum) {
+        if (d.slot < 0) {
+            out[(static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * hpsG + ri) * kD + dd] = from_float<OutT>(acc / lsum);
+        } else {
+            const uint64_t row = static_cast<uint64_t>(d.slot) * hpsG + ri;
+            __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (dd == 0) {
+                __hip_atomic_store(&a.ws_ml[row * 2 + 0], mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.ws_ml[row * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    };
+    // A piece's merged element goes to LDS when results are deferred: a
+    // global store here would sit in the wave's memory counter ahead of the
+    // next tile's loads, and the next tile's wait would then wait for the
+    // store's write-through as well.
+    auto emit = [&](int pi, const qvp_piece& d, int ri, int dd, float acc, float mmax, float lsum) {
+        if (a.defer) {
+            const int row = (pi - pb) * hpsG + ri;
+            def_acc[row * kD + dd] = acc;
+            if (dd == 0) {
+                def_ml[2 * row] = mmax;
+                def_ml[2 * row + 1] = lsum;
+            }
+        } else {
+            store_result(d, ri, dd, acc, mmax, lsum);
+        }
+    };
 
     // Software pipeline per wave: while the current tile is computed, the next
     // tile's loads are in flight (nxt) and the block ids of the tile after that
@@ -289,10 +335,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
 #pragma unroll
             for (int n = 0; n < 8; ++n) sm_o[wave][c][32 * j + 8 * r + n] = o[n][r];
 
-        const int slot = d.slot;
-        have_partial = have_partial || slot >= 0;
-        OutT* out = static_cast<OutT*>(a.out);
-        const uint64_t out_row0 = (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * hpsG) * kD;
+        have_partial = have_partial || d.slot >= 0;
         if (hps == 1) {
             // The eight waves are tile lanes of one head: merge them through LDS.
             lds_barrier();
@@ -310,23 +353,12 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
                     acc += sm_o[w][hc][dd] * f;
                     lsum += sm_l[w][hc] * f;
                 }
-                if (slot < 0) {
-                    out[out_row0 + e] = from_float<OutT>(acc / lsum);
-                } else {
-                    const uint64_t row = static_cast<uint64_t>(slot) * G + hc;
-                    __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (dd == 0) {
-                        __hip_atomic_store(&a.ws_ml[row * 2 + 0], mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        __hip_atomic_store(&a.ws_ml[row * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
+                emit(pi, d, hc, dd, acc, mmax, lsum);
             }
             lds_barrier();
         } else {
             // hps heads of kWaves / hps tile lanes each: merge each head's lanes
-            // through LDS. Slot stores are agent-scope: written through to the
-            // point of coherence shared by all XCDs (the wait before the
-            // count-in makes sure they have arrived).
+            // through LDS.
             lds_barrier();
             for (int e = threadIdx.x; e < hpsG * kD; e += kThreads) {
                 const int ri = e >> 7;  // row within the segment: head ri / G, query column ri % G
@@ -342,18 +374,23 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
                     acc += sm_o[w][hc][dd] * f;
                     lsum += sm_l[w][hc] * f;
                 }
-                if (slot < 0) {
-                    out[out_row0 + e] = from_float<OutT>(acc / lsum);
-                } else {
-                    const uint64_t row = static_cast<uint64_t>(slot) * hpsG + ri;
-                    __hip_atomic_store(&a.ws_acc[row * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (dd == 0) {
-                        __hip_atomic_store(&a.ws_ml[row * 2 + 0], mmax, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        __hip_atomic_store(&a.ws_ml[row * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
+                emit(pi, d, ri, dd, acc, mmax, lsum);
             }
             lds_barrier();
+        }
+    }
+
+    // Deferred results: every piece's rows, now that the range's loads are
+    // done (the last piece's merge ended with a barrier, so all rows are in
+    // LDS).
+    if (a.defer) {
+        for (int k = 0; k < pe - pb; ++k) {
+            const qvp_piece d = piece_at(a.pieces, pb + k);
+            for (int e = threadIdx.x; e < hpsG * kD; e += kThreads) {
+                const int row = k * hpsG + (e >> 7);
+                store_result(d, e >> 7, e & (kD - 1), def_acc[row * kD + (e & (kD - 1))], def_ml[2 * row],
+                             def_ml[2 * row + 1]);
+            }
         }
     }
 
@@ -407,7 +444,6 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     const int max_ns = max(m0.seg_nslots, m1.seg_nslots);
     const uint64_t orow0 = (static_cast<uint64_t>(m0.b) * p.num_q_heads + m0.g * hpsG) * kD;
     const uint64_t orow1 = (static_cast<uint64_t>(m1.b) * p.num_q_heads + m1.g * hpsG) * kD;
-    OutT* out = static_cast<OutT*>(a.out);
     const int per_seg = hpsG * kD;
     const int total = nm * per_seg;
     for (int f0 = threadIdx.x; f0 < total; f0 += kThreads * kMergeBatch) {
@@ -486,6 +522,16 @@ int device_max_wgs(uint32_t* wgs) {
     std::lock_guard<std::mutex> lock(g_dev_mutex);
     if (g_dev_wgs.size() <= static_cast<size_t>(dev)) g_dev_wgs.resize(dev + 1, 0);
     if (g_dev_wgs[dev] == 0) {
+        // The kernels may take all of the CU's LDS (deferred piece results
+        // beside the static arrays); allowed once per device, before any
+        // launch (and so before any graph capture).
+        const int dyn = static_cast<int>(kMaxLdsBytes - kStaticLdsBytes);
+        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_persistent<float>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_persistent<uint16_t>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_persistent<_Float16>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
         int cus = 0;
         QVP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         g_dev_wgs[dev] = static_cast<uint32_t>(std::max(1, cus) * kWgsPerCu);
@@ -743,6 +789,16 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
         max_partial = std::max(max_partial, n);
     }
 
+    // Piece results are held in LDS until a range is done when the largest
+    // range's pieces fit beside the kernel's static arrays.
+    uint32_t np_max = 0;
+    for (uint32_t w = 0; w < Wn; ++w) {
+        np_max = std::max<uint32_t>(np_max, static_cast<uint32_t>(wg_begin[w + 1] - wg_begin[w]));
+    }
+    const uint64_t def_bytes = static_cast<uint64_t>(np_max) * hps * g.group * (kD + 2) * sizeof(float);
+    s.defer = def_bytes + kStaticLdsBytes <= kMaxLdsBytes;
+    s.lds_bytes = s.defer ? static_cast<uint32_t>(def_bytes) : 0u;
+
     // Each wave's first tile, resolved to frames here (the kernel's
     // next_tile and resolve_tile for its first step).
     const uint32_t tpb = batch->view.tokens_per_block;
@@ -839,16 +895,18 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + round_up(rows * 2 * sizeof(float), 256));
     a.out = out;
     a.hps = static_cast<int>(s.hps);
+    a.defer = s.defer ? 1 : 0;
     const dim3 grid(s.num_wgs);
+    const size_t lds = s.lds_bytes;
     switch (out_dtype) {
         case QVP_DTYPE_F32:
-            hipLaunchKernelGGL(decode_mfma_persistent<float>, grid, dim3(kThreads), 0, stream, g, a);
+            hipLaunchKernelGGL(decode_mfma_persistent<float>, grid, dim3(kThreads), lds, stream, g, a);
             break;
         case QVP_DTYPE_BF16:
-            hipLaunchKernelGGL(decode_mfma_persistent<uint16_t>, grid, dim3(kThreads), 0, stream, g, a);
+            hipLaunchKernelGGL(decode_mfma_persistent<uint16_t>, grid, dim3(kThreads), lds, stream, g, a);
             break;
         default:
-            hipLaunchKernelGGL(decode_mfma_persistent<_Float16>, grid, dim3(kThreads), 0, stream, g, a);
+            hipLaunchKernelGGL(decode_mfma_persistent<_Float16>, grid, dim3(kThreads), lds, stream, g, a);
             break;
     }
     QVP_HIP(hipGetLastError());
