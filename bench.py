@@ -13,8 +13,11 @@ Infinity Cache cannot serve a step from the previous step's reads. `value` is
 algorithmic HBM bytes per step / step time. The pack-inclusive rate (host pack
 + pinned H2D + decode) is reported beside it as `step_with_pack_*`.
 
-`roofline` uses the decode kernel's own average duration, measured with HIP
-events recorded on the decode stream around it. `read_ceiling` is a plain
+`roofline` uses the decode kernel's own average launch duration: two HIP
+events recorded on the decode stream around K back-to-back launches, their
+interval over K (the figure rocprofv3's kernel trace reports for the kernel;
+`kernel_isolated_avg_ms` brackets each launch with its own event pair, which
+adds the events' cost). `read_ceiling` is a plain
 streaming read of the same byte count (no gather, no math) on this device:
 the rate any kernel reading those bytes once reaches, launch ramp and drain
 included, and the decode kernel's rate as a fraction of it. `cpu_baseline` times the
@@ -570,8 +573,20 @@ def main() -> int:
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1e3 / args.steps
 
-    # Timed region 2: the same steps with HIP events on the launch stream
-    # around each decode (one kernel: the split merge is fused into it).
+    # Timed region 2: the same K back-to-back decodes (one kernel each: the
+    # split merge is fused into it) between two HIP events recorded on the
+    # launch stream; the kernel's average launch duration is their interval
+    # over K, the figure rocprofv3's kernel trace reports for it.
+    ev0, ev1 = qvp.Event(), qvp.Event()
+    qvp.synchronize()
+    ev0.record(stream)
+    for i in range(args.steps):
+        qvp.paged_decode(plain[i % len(pools)], stream)
+    ev1.record(stream)
+    stream.synchronize()
+    kernel_avg = ev0.elapsed_ms(ev1) / args.steps
+    # The same launches each bracketed by its own event pair (each pair adds
+    # the events' own cost to the interval), reported beside it.
     starts = [qvp.Event() for _ in range(args.steps)]
     ends = [qvp.Event() for _ in range(args.steps)]
     qvp.synchronize()
@@ -599,7 +614,6 @@ def main() -> int:
     algo = w.algorithmic_bytes()
     kernel_bytes = w.kv_bytes() + w.num_seqs * w.num_query_heads * w.head_dim * 2 + \
         int(((w.context_lens.astype(np.int64) + 15) // 16).sum()) * 4 + w.num_seqs * 4
-    kernel_avg = statistics.mean(kernel_ms)
     gbps = algo / (ms_per_step * 1e-3) / 1e9
     achieved = kernel_bytes / (kernel_avg * 1e-3) / 1e9
     traffic = load_traffic()
@@ -646,6 +660,7 @@ def main() -> int:
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
             "traffic": traffic.get("bytes_per_launch") if traffic and args.workload == "config2" else None,
             "kernel_avg_ms": round(kernel_avg, 5),
+            "kernel_isolated_avg_ms": round(statistics.mean(kernel_ms), 5),
             "kernel_bytes_per_launch": kernel_bytes,
         },
         "setup_s": round(setup_s, 2),
