@@ -71,10 +71,10 @@ constexpr uint64_t kMinTilesPerWaveForHeadGroups = 32;
 // A workgroup's range is contiguous, so only its first and last pieces can be
 // partial segments.
 constexpr int kMaxPartialPerWg = 2;
-// Slots combined per round of loads in the end-of-range merge, and elements
-// per thread per round.
+// Slots combined per round of loads in the end-of-range merge, and work items
+// (four dims of a row) per thread per round.
 constexpr int kMergeChunk = 8;
-constexpr int kMergeBatch = 4;
+constexpr int kMergeBatch = 2;
 
 // Cost of a piece boundary inside a range, in one wave's tile times: the
 // waves' LDS merge (a workgroup barrier) and the piece's stores, which the
@@ -444,42 +444,45 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     const int max_ns = max(m0.seg_nslots, m1.seg_nslots);
     const uint64_t orow0 = (static_cast<uint64_t>(m0.b) * p.num_q_heads + m0.g * hpsG) * kD;
     const uint64_t orow1 = (static_cast<uint64_t>(m1.b) * p.num_q_heads + m1.g * hpsG) * kD;
-    const int per_seg = hpsG * kD;
+    // Work items are four consecutive dims of one row: per slot one 8-byte
+    // agent-scope load of the row's (m, l) and two of its four accumulators.
+    const int per_seg = hpsG * (kD / 4);
     const int total = nm * per_seg;
     for (int f0 = threadIdx.x; f0 < total; f0 += kThreads * kMergeBatch) {
-        int hc[kMergeBatch], dd[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch];
+        int ri[kMergeBatch], dq[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch];
         uint64_t orow[kMergeBatch];
-        float mmax[kMergeBatch], acc[kMergeBatch], lsum[kMergeBatch];
+        float mmax[kMergeBatch], lsum[kMergeBatch], acc[kMergeBatch][4];
 #pragma unroll
         for (int i = 0; i < kMergeBatch; ++i) {
             const int f = f0 + i * kThreads;
             const bool second = f >= per_seg;
             const int e = f < total ? f - (second ? per_seg : 0) : 0;
-            hc[i] = e >> 7;
-            dd[i] = e & (kD - 1);
+            ri[i] = e >> 5;
+            dq[i] = e & 31;
             s0[i] = second ? m1.seg_slot0 : m0.seg_slot0;
             ns[i] = f < total ? (second ? m1.seg_nslots : m0.seg_nslots) : 0;
             orow[i] = second ? orow1 : orow0;
             mmax[i] = -INFINITY;
-            acc[i] = 0.f;
             lsum[i] = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[i][k] = 0.f;
         }
         for (int c0 = 0; c0 < max_ns; c0 += kMergeChunk) {
-            float m[kMergeBatch][kMergeChunk], l[kMergeBatch][kMergeChunk], o[kMergeBatch][kMergeChunk];
+            uint64_t ml[kMergeBatch][kMergeChunk], o01[kMergeBatch][kMergeChunk], o23[kMergeBatch][kMergeChunk];
 #pragma unroll
             for (int i = 0; i < kMergeBatch; ++i) {
 #pragma unroll
                 for (int x = 0; x < kMergeChunk; ++x) {
-                    m[i][x] = -INFINITY;
-                    l[i][x] = 0.f;
-                    o[i][x] = 0.f;
+                    ml[i][x] = 0;
+                    o01[i][x] = 0;
+                    o23[i][x] = 0;
                     if (c0 + x < ns[i]) {
-                        const uint64_t row = static_cast<uint64_t>(s0[i] + c0 + x) * hpsG + hc[i];
-                        m[i][x] = __hip_atomic_load(&a.ws_ml[row * 2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        l[i][x] =
-                            __hip_atomic_load(&a.ws_ml[row * 2 + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        o[i][x] = __hip_atomic_load(&a.ws_acc[row * kD + dd[i]], __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
+                        const uint64_t row = static_cast<uint64_t>(s0[i] + c0 + x) * hpsG + ri[i];
+                        ml[i][x] = __hip_atomic_load(reinterpret_cast<const uint64_t*>(a.ws_ml + row * 2),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const uint64_t* op = reinterpret_cast<const uint64_t*>(a.ws_acc + row * kD + 4 * dq[i]);
+                        o01[i][x] = __hip_atomic_load(op, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        o23[i][x] = __hip_atomic_load(op + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
             }
@@ -487,23 +490,34 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
             for (int i = 0; i < kMergeBatch; ++i) {
                 float cm = mmax[i];
 #pragma unroll
-                for (int x = 0; x < kMergeChunk; ++x) cm = fmaxf(cm, m[i][x]);
-                // Elements past the end have no slot: keep them finite.
+                for (int x = 0; x < kMergeChunk; ++x) {
+                    if (c0 + x < ns[i]) cm = fmaxf(cm, __uint_as_float(static_cast<uint32_t>(ml[i][x])));
+                }
+                // Items past the end have no slot: keep them finite.
                 const float rescale = cm == -INFINITY ? 0.f : fast_exp2(mmax[i] - cm);
-                acc[i] *= rescale;
                 lsum[i] *= rescale;
 #pragma unroll
+                for (int k = 0; k < 4; ++k) acc[i][k] *= rescale;
+#pragma unroll
                 for (int x = 0; x < kMergeChunk; ++x) {
-                    const float f = c0 + x < ns[i] ? fast_exp2(m[i][x] - cm) : 0.f;
-                    acc[i] += o[i][x] * f;
-                    lsum[i] += l[i][x] * f;
+                    const float m = __uint_as_float(static_cast<uint32_t>(ml[i][x]));
+                    const float f = c0 + x < ns[i] ? fast_exp2(m - cm) : 0.f;
+                    lsum[i] += __uint_as_float(static_cast<uint32_t>(ml[i][x] >> 32)) * f;
+                    acc[i][0] += __uint_as_float(static_cast<uint32_t>(o01[i][x])) * f;
+                    acc[i][1] += __uint_as_float(static_cast<uint32_t>(o01[i][x] >> 32)) * f;
+                    acc[i][2] += __uint_as_float(static_cast<uint32_t>(o23[i][x])) * f;
+                    acc[i][3] += __uint_as_float(static_cast<uint32_t>(o23[i][x] >> 32)) * f;
                 }
                 mmax[i] = cm;
             }
         }
 #pragma unroll
         for (int i = 0; i < kMergeBatch; ++i) {
-            if (f0 + i * kThreads < total) out[orow[i] + hc[i] * kD + dd[i]] = from_float<OutT>(acc[i] / lsum[i]);
+            if (f0 + i * kThreads < total) {
+                OutT* dst = out + orow[i] + ri[i] * kD + 4 * dq[i];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) dst[k] = from_float<OutT>(acc[i][k] / lsum[i]);
+            }
         }
     }
     if (threadIdx.x < static_cast<unsigned>(nm)) {
