@@ -37,10 +37,15 @@ struct qvp_schedule {
     bool defer{false};            // piece results held in LDS until a range is done
     uint32_t lds_bytes{0};        // dynamic LDS per workgroup for them
     size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, off_first{0}, total{0};  // int32 units
-    int32_t* staging{nullptr};
-    size_t staging_cap{0};
-    hipEvent_t staging_done{nullptr};
-    bool staging_pending{false};
+    // Two pinned staging buffers, used in turn: rebuilding the schedule for
+    // step n + 1 waits only for the upload of the rebuild before last, which
+    // the stream reaches once step n - 1's decode is done, so the host can
+    // prepare the next step while the current one runs.
+    int32_t* staging[2]{nullptr, nullptr};
+    size_t staging_cap[2]{0, 0};
+    hipEvent_t staging_done[2]{nullptr, nullptr};
+    bool staging_pending[2]{false, false};
+    int staging_slot{0};
     int32_t* device{nullptr};
     size_t device_cap{0};
 };

@@ -647,9 +647,11 @@ std::vector<uint64_t> cut_ranges(const std::vector<uint64_t>& pos_cum, uint32_t 
 }  // namespace
 
 void destroy_schedule(qvp_schedule& s) {
-    if (s.staging_pending) (void)hipEventSynchronize(s.staging_done);
-    if (s.staging != nullptr) (void)hipHostFree(s.staging);
-    if (s.staging_done != nullptr) (void)hipEventDestroy(s.staging_done);
+    for (int i = 0; i < 2; ++i) {
+        if (s.staging_pending[i]) (void)hipEventSynchronize(s.staging_done[i]);
+        if (s.staging[i] != nullptr) (void)hipHostFree(s.staging[i]);
+        if (s.staging_done[i] != nullptr) (void)hipEventDestroy(s.staging_done[i]);
+    }
     if (s.device != nullptr) (void)hipFree(s.device);
     s = qvp_schedule{};
 }
@@ -849,17 +851,24 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     s.off_first = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
     s.total = s.off_first + align_ints(first.size());
 
-    if (s.staging_done == nullptr) QVP_HIP(hipEventCreateWithFlags(&s.staging_done, hipEventDisableTiming));
-    if (s.staging_pending) {
-        QVP_HIP(hipEventSynchronize(s.staging_done));
-        s.staging_pending = false;
+    const int slot = s.staging_slot;
+    s.staging_slot ^= 1;
+    if (s.staging_done[slot] == nullptr) {
+        QVP_HIP(hipEventCreateWithFlags(&s.staging_done[slot], hipEventDisableTiming));
     }
-    if (s.staging_cap < s.total) {
-        if (s.staging != nullptr) QVP_HIP(hipHostFree(s.staging));
-        s.staging = nullptr;
-        s.staging_cap = 0;
-        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&s.staging), s.total * sizeof(int32_t), hipHostMallocDefault));
-        s.staging_cap = s.total;
+    // The staging buffer about to be refilled may still be read by the
+    // upload of the rebuild before last.
+    if (s.staging_pending[slot]) {
+        QVP_HIP(hipEventSynchronize(s.staging_done[slot]));
+        s.staging_pending[slot] = false;
+    }
+    if (s.staging_cap[slot] < s.total) {
+        if (s.staging[slot] != nullptr) QVP_HIP(hipHostFree(s.staging[slot]));
+        s.staging[slot] = nullptr;
+        s.staging_cap[slot] = 0;
+        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&s.staging[slot]), s.total * sizeof(int32_t),
+                              hipHostMallocDefault));
+        s.staging_cap[slot] = s.total;
     }
     if (s.device_cap < s.total) {
         if (s.device != nullptr) QVP_HIP(hipFree(s.device));
@@ -868,15 +877,15 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
         QVP_HIP(hipMalloc(reinterpret_cast<void**>(&s.device), s.total * sizeof(int32_t)));
         s.device_cap = s.total;
     }
-    int32_t* h = s.staging;
+    int32_t* h = s.staging[slot];
     std::fill(h, h + s.total, 0);  // counters start at zero
     std::copy(wg_begin.begin(), wg_begin.end(), h + s.off_wg_begin);
     const int32_t* praw = reinterpret_cast<const int32_t*>(pieces.data());
     std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
     std::copy(first.begin(), first.end(), h + s.off_first);
     QVP_HIP(hipMemcpyAsync(s.device, h, s.total * sizeof(int32_t), hipMemcpyHostToDevice, stream));
-    QVP_HIP(hipEventRecord(s.staging_done, stream));
-    s.staging_pending = true;
+    QVP_HIP(hipEventRecord(s.staging_done[slot], stream));
+    s.staging_pending[slot] = true;
 
     s.pack_generation = batch->generation;
     s.num_kv_heads = num_kv_heads;
