@@ -761,35 +761,27 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     }
     wg_begin[Wn] = static_cast<int32_t>(pieces.size());
 
-    // The pieces of a segment (b, q) lie in workgroups r * nq + q for
-    // consecutive r; whole-segment pieces need no slot. A split segment's
-    // pieces get consecutive slots in tile order.
-    std::vector<uint32_t> order(pieces.size());
-    for (uint32_t i = 0; i < order.size(); ++i) order[i] = i;
-    std::sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
-        const qvp_piece& a = pieces[x];
-        const qvp_piece& c = pieces[y];
-        if (a.b != c.b) return a.b < c.b;
-        if (a.g != c.g) return a.g < c.g;
-        return a.t0 < c.t0;
-    });
+    // Whole-segment pieces need no slot; a split segment's pieces get
+    // consecutive slots in tile order, segments numbered in (sequence, head
+    // group) order. A head group's ranges were laid out in position order,
+    // so a segment's pieces already appear in tile order: one counting pass
+    // numbers them (no sort).
+    const size_t nseg = lens.size() * nq;
+    std::vector<int32_t> seg_count(nseg, 0), seg_base(nseg, -1), seg_next(nseg, 0);
+    for (const qvp_piece& pc : pieces) ++seg_count[static_cast<size_t>(pc.b) * nq + pc.g];
     int32_t next_slot = 0;
-    for (size_t i = 0; i < order.size();) {
-        size_t k = i + 1;
-        while (k < order.size() && pieces[order[k]].b == pieces[order[i]].b &&
-               pieces[order[k]].g == pieces[order[i]].g) {
-            ++k;
+    for (size_t k = 0; k < nseg; ++k) {
+        if (seg_count[k] > 1) {
+            seg_base[k] = next_slot;
+            next_slot += seg_count[k];
         }
-        if (k - i > 1) {
-            const int32_t first = next_slot;
-            for (size_t x = i; x < k; ++x) {
-                qvp_piece& pc = pieces[order[x]];
-                pc.slot = next_slot++;
-                pc.seg_slot0 = first;
-                pc.seg_nslots = static_cast<int32_t>(k - i);
-            }
-        }
-        i = k;
+    }
+    for (qvp_piece& pc : pieces) {
+        const size_t k = static_cast<size_t>(pc.b) * nq + pc.g;
+        if (seg_base[k] < 0) continue;
+        pc.slot = seg_base[k] + seg_next[k]++;
+        pc.seg_slot0 = seg_base[k];
+        pc.seg_nslots = seg_count[k];
     }
     // The kernel counts in only the first and the last piece of a range.
     uint32_t max_partial = 0;
@@ -815,41 +807,12 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     s.defer = def_bytes + kStaticLdsBytes <= kMaxLdsBytes;
     s.lds_bytes = s.defer ? static_cast<uint32_t>(def_bytes) : 0u;
 
-    // Each wave's first tile, resolved to frames here (the kernel's
-    // next_tile and resolve_tile for its first step).
-    const uint32_t tpb = batch->view.tokens_per_block;
-    uint32_t shift = 0;
-    while ((1u << shift) < tpb) ++shift;
-    std::vector<int32_t> first(static_cast<size_t>(Wn) * kWaves * kFirstWords, 0);
-    for (uint32_t w = 0; w < Wn; ++w) {
-        for (int wave = 0; wave < kWaves; ++wave) {
-            int32_t* f = first.data() + (static_cast<size_t>(w) * kWaves + wave) * kFirstWords;
-            const int32_t hl = wave % static_cast<int32_t>(hps);
-            const int32_t tlane = wave / static_cast<int32_t>(hps);
-            f[0] = -1;
-            f[5] = wg_begin[w];
-            f[6] = wg_begin[w + 1];
-            for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
-                const qvp_piece& pc = pieces[pi];
-                if (pc.t0 + tlane >= pc.t1) continue;
-                const int32_t t = pc.t0 + tlane;
-                const uint32_t* row = batch->host_ids.data() + batch->host_cu_blocks[pc.b];
-                const int32_t tok0 = t * kTileTokens;
-                f[0] = pi;
-                f[1] = t;
-                f[2] = pc.g * static_cast<int32_t>(hps) + hl;
-                f[3] = static_cast<int32_t>(row[std::min(tok0, pc.ctx - 1) >> shift]);
-                f[4] = static_cast<int32_t>(row[std::min(tok0 + 16, pc.ctx - 1) >> shift]);
-                break;
-            }
-        }
-    }
-
     s.off_wg_begin = 0;
     s.off_pieces = align_ints(Wn + 1);
     s.off_counters = s.off_pieces + align_ints(pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)));
     s.off_first = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
-    s.total = s.off_first + align_ints(first.size());
+    const size_t first_words = static_cast<size_t>(Wn) * kWaves * kFirstWords;
+    s.total = s.off_first + align_ints(first_words);
 
     const int slot = s.staging_slot;
     s.staging_slot ^= 1;
@@ -882,7 +845,36 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     std::copy(wg_begin.begin(), wg_begin.end(), h + s.off_wg_begin);
     const int32_t* praw = reinterpret_cast<const int32_t*>(pieces.data());
     std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
-    std::copy(first.begin(), first.end(), h + s.off_first);
+    // Each wave's first tile, resolved to frames here (the kernel's
+    // next_tile and resolve_tile for its first step), written straight into
+    // the staging buffer (its other words stay zero).
+    const uint32_t tpb = batch->view.tokens_per_block;
+    uint32_t shift = 0;
+    while ((1u << shift) < tpb) ++shift;
+    for (uint32_t w = 0; w < Wn; ++w) {
+        for (int wave = 0; wave < kWaves; ++wave) {
+            int32_t* f = h + s.off_first + (static_cast<size_t>(w) * kWaves + wave) * kFirstWords;
+            const int32_t hl = wave % static_cast<int32_t>(hps);
+            const int32_t tlane = wave / static_cast<int32_t>(hps);
+            f[0] = -1;
+            f[5] = wg_begin[w];
+            f[6] = wg_begin[w + 1];
+            for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
+                const qvp_piece& pc = pieces[pi];
+                if (pc.t0 + tlane >= pc.t1) continue;
+                const int32_t t = pc.t0 + tlane;
+                const uint32_t* row = batch->host_ids.data() + batch->host_cu_blocks[pc.b];
+                const int32_t tok0 = t * kTileTokens;
+                f[0] = pi;
+                f[1] = t;
+                f[2] = pc.g * static_cast<int32_t>(hps) + hl;
+                f[3] = static_cast<int32_t>(row[std::min(tok0, pc.ctx - 1) >> shift]);
+                f[4] = static_cast<int32_t>(row[std::min(tok0 + 16, pc.ctx - 1) >> shift]);
+                break;
+            }
+        }
+    }
+
     QVP_HIP(hipMemcpyAsync(s.device, h, s.total * sizeof(int32_t), hipMemcpyHostToDevice, stream));
     QVP_HIP(hipEventRecord(s.staging_done[slot], stream));
     s.staging_pending[slot] = true;
