@@ -89,6 +89,35 @@ def test_balanced_schedule_shapes(lens):
     _parity(w, out_dtypes=(qvp.DTYPE_F32, qvp.DTYPE_BF16))
 
 
+def test_pool_base_off_the_kib_grid_takes_equal_head_weights():
+    """The schedule gives kv heads whose bytes sit at offsets 256..511 of each
+    KiB more workgroups only when the pool base keeps those offsets fixed; a
+    base 256 bytes off a KiB boundary takes the equal-weight path. Both
+    schedules must decode to the oracle's result."""
+    print("case: pool base off the KiB grid", flush=True)
+    w = W.custom([700, 2000, 3100, 513, 1500, 2600], 28, 4, 128, seed=91)
+    run = GpuRun(w)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    assert_close_bf16(run.decode(out_dtype=qvp.DTYPE_F32), ref32, "KiB-aligned pool base")
+
+    buf = qvp.DeviceBuffer(run.image.nbytes + 2048)
+    off = (256 - buf.ptr % 1024) % 1024
+    assert (buf.ptr + off) % 1024 == 256
+    buf.upload(run.image, offset=off)
+    batch = qvp.Batch()
+    batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, w.split_tokens)
+    out = qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4)
+    out.fill(0xFF)
+    args = qvp.decode_args(query=run.q.ptr, out=out.ptr, kv_base=buf.ptr + off, block_stride=w.block_stride,
+                           batch=batch, kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_F32, layer=w.layer,
+                           num_layers=w.num_layers, num_query_heads=w.num_query_heads,
+                           num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+                           tokens_per_block=w.tokens_per_block, scale=w.scale, strides=w.strides)
+    qvp.paged_decode(args)
+    got = out.download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim))
+    assert_close_bf16(got, ref32, "pool base 256 bytes off the KiB grid")
+
+
 def test_config3_subset_72b_shape():
     print("case: config3 shape, 2 sequences", flush=True)
     _parity(W.config3(num_seqs=2), out_dtypes=(qvp.DTYPE_F32,))
