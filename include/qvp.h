@@ -262,6 +262,32 @@ int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads,
  * uses a per-device workspace it grows on demand. */
 int qvp_paged_decode(const qvp_decode_args* args, void* stream);
 
+/* The work decomposition of the last qvp_paged_decode enqueued on a batch.
+ * No reference counterpart (the reference decodes one sequence at a time,
+ * PagedAttention.h:53-127): it tells benchmarks and tests which kernel ran
+ * and how the batch was divided. */
+typedef enum qvp_decode_kernel {
+    QVP_DECODE_NONE = 0,        /* nothing decoded since the last qvp_pack */
+    QVP_DECODE_MFMA = 1,        /* persistent bf16 MFMA kernel, cost-balanced tile ranges */
+    QVP_DECODE_F32_GROUPED = 2, /* fp32 MFMA kernel over split_tokens partitions + merge */
+    QVP_DECODE_GENERIC = 3      /* VALU kernel over split_tokens partitions + merge */
+} qvp_decode_kernel;
+
+typedef struct qvp_decode_plan {
+    uint32_t kernel;            /* qvp_decode_kernel */
+    uint32_t workgroups;        /* workgroups of the decode kernel */
+    uint32_t pieces;            /* MFMA: (sequence, kv-head group, tile range) pieces;
+                                   split kernels: token partitions */
+    uint32_t slots;             /* partial results merged through the workspace */
+    uint32_t kv_heads_per_segment; /* MFMA: kv heads one workgroup decodes side by side */
+    uint32_t split_tokens;      /* split kernels: tokens per partition; MFMA: 0 (its
+                                   ranges are cut by cost, not by a partition size) */
+    uint32_t deferred_results;  /* MFMA: 1 when piece results wait in LDS until a range ends */
+    uint32_t query_group;       /* query heads per kv head of that decode */
+} qvp_decode_plan;
+
+int qvp_decode_plan_info(const qvp_batch* batch, qvp_decode_plan* plan);
+
 /* ------------------------------------------------------------------------ */
 /* Causal paged prefill (PagedAttention.h:43-44: paged_attention_decode<T>  */
 /* applied per prompt position p with context_len = p + 1)                  */

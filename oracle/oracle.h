@@ -8,8 +8,10 @@
  *
  * Every function cites the reference source it restates (paths relative to the
  * QwenVL-Paged tree). Pinning (see tests/test_oracle.py): the decode matches
- * the compiled reference bit for bit (oracle/_ref) and the committed fixtures
- * under tests/golden/, and the closed-form cases of
+ * the compiled reference bit for bit for float, bf16 and fp16 elements
+ * (oracle/_ref) and the committed fixtures under tests/golden/; the fp16 and
+ * bf16 conversions match numpy's float16 / round-to-nearest-even on every
+ * half bit pattern and on edge and random floats; and the closed-form cases of
  * tests/PagedAttention.test.cpp (uniform keys, one-hot selection, GQA, CoW
  * branches); the layout functions match CacheView.test.cpp's invariants; pack
  * and copy are checked against BlockTable entries and memcpy identity; the

@@ -96,6 +96,10 @@ def reference() -> ctypes.CDLL:
         lib.ref_block_byte_size.argtypes = [c_uint32] * 5
         lib.ref_block_size_bytes.restype = c_uint64
         lib.ref_block_size_bytes.argtypes = [c_uint32] * 5 + [c_uint64]
+        lib.ref_half_from_float.restype = ctypes.c_uint16
+        lib.ref_half_from_float.argtypes = [c_float]
+        lib.ref_float_from_half.restype = c_float
+        lib.ref_float_from_half.argtypes = [ctypes.c_uint16]
         lib.ref_element_offset.restype = c_int64
         lib.ref_element_offset.argtypes = [c_uint32] * 8
         _ref = lib

@@ -19,6 +19,8 @@
 #include "qwenvl_paged/SwapBackend.h"
 #include "trace_driver.h"
 
+#include <immintrin.h>
+
 #include <chrono>
 #include <cstring>
 #include <memory>
@@ -52,6 +54,23 @@ struct Bf16 {
     }
 };
 static_assert(sizeof(Bf16) == 2, "bf16 must be two bytes");
+
+// IEEE binary16 element type for fp16 caches. The conversions are the x86
+// F16C instructions (vcvtps2ph with round-to-nearest-even, vcvtph2ps): a
+// hardware implementation independent of oracle.c's bit manipulation, so
+// the decode check below pins the oracle's fp16 arithmetic and conversions.
+__attribute__((target("f16c"))) std::uint16_t half_from_float(float f) {
+    return static_cast<std::uint16_t>(_cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT));
+}
+__attribute__((target("f16c"))) float float_from_half(std::uint16_t h) { return _cvtsh_ss(h); }
+
+struct Half {
+    std::uint16_t bits;
+    Half() = default;
+    explicit Half(float f) : bits(half_from_float(f)) {}
+    explicit operator float() const { return float_from_half(bits); }
+};
+static_assert(sizeof(Half) == 2, "half must be two bytes");
 
 struct Session {
     BlockShape shape{};
@@ -129,8 +148,9 @@ void* ref_session_create(const std::uint8_t* pool, std::uint64_t stride, std::ui
 
 void ref_session_destroy(void* session) { delete static_cast<Session*>(session); }
 
-// Runs paged_attention_decode<T> for every sequence; dtype 0 = float, 1 = bf16.
-// Returns the number of refused sequences, or -1 for an unsupported dtype.
+// Runs paged_attention_decode<T> for every sequence; dtype 0 = float, 1 =
+// bf16, 2 = fp16. Returns the number of refused sequences, or -1 for an
+// unsupported dtype.
 int ref_session_decode(void* session, std::uint32_t num_seqs, const std::uint32_t* ids,
                        const std::uint32_t* cu_blocks, const std::uint32_t* ctx_lens, int dtype,
                        const void* query, std::uint32_t layer, std::uint32_t hq, float scale, void* out,
@@ -138,8 +158,13 @@ int ref_session_decode(void* session, std::uint32_t num_seqs, const std::uint32_
     Session& s = *static_cast<Session*>(session);
     if (dtype == 0) return decode_all<float>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds);
     if (dtype == 1) return decode_all<Bf16>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds);
+    if (dtype == 2) return decode_all<Half>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds);
     return -1;
 }
+
+// The shim's fp16 conversions, for the tests that check them against numpy.
+std::uint16_t ref_half_from_float(float f) { return half_from_float(f); }
+float ref_float_from_half(std::uint16_t h) { return float_from_half(h); }
 
 std::uint64_t ref_block_byte_size(std::uint32_t tpb, std::uint32_t layers, std::uint32_t heads,
                                   std::uint32_t dim, std::uint32_t bpe) {

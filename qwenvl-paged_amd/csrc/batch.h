@@ -27,6 +27,7 @@ struct qvp_schedule {
     bool valid{false};
     uint64_t pack_generation{0};
     uint32_t num_kv_heads{0};
+    uint32_t group{0};  // query heads per kv head (sizes the deferred LDS and the slots)
     uint32_t max_wgs{0};
     uint32_t num_wgs{0};
     uint32_t num_pieces{0};
@@ -77,6 +78,7 @@ struct qvp_batch {
     std::vector<uint32_t> host_ids;      // host copy of the needed block ids, CSR over host_cu_blocks
     std::vector<uint32_t> host_cu_blocks;
     qvp_packed_view view{};
+    qvp_decode_plan last_plan{};       // what the last decode on this pack ran (reset by qvp_pack)
     qvp_schedule sched{};
     qvp_prefill_plan prefill{};
 };

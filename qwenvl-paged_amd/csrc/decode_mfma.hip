@@ -680,7 +680,7 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     const uint32_t nq = num_kv_heads / hps;
     const std::vector<double> weights = head_group_weights(g, hps, nq);
     if (s.valid && s.pack_generation == batch->generation && s.num_kv_heads == num_kv_heads &&
-        s.max_wgs == max_wgs && s.weights == weights) {
+        s.group == g.group && s.max_wgs == max_wgs && s.weights == weights) {
         return QVP_OK;
     }
     s.valid = false;
@@ -881,6 +881,7 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
 
     s.pack_generation = batch->generation;
     s.num_kv_heads = num_kv_heads;
+    s.group = g.group;
     s.max_wgs = max_wgs;
     s.weights = weights;
     s.num_wgs = Wn;

@@ -253,6 +253,7 @@ int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
         batch->host_cu_blocks.push_back(static_cast<uint32_t>(batch->host_ids.size()));
     }
     batch->generation += 1;
+    batch->last_plan = qvp_decode_plan{};
     batch->valid = true;
     return QVP_OK;
 }

@@ -158,12 +158,39 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
     } else if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     }
-    if (mfma) return qvp::launch_mfma_decode(g, batch, a->out_dtype, a->out, ws, ev, s);
-    if (qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens, reinterpret_cast<uintptr_t>(a->query),
-                                   reinterpret_cast<uintptr_t>(a->kv_base))) {
-        return qvp::launch_f32_grouped_decode(g, v, a->out_dtype, a->out, ws, ev, s);
+    qvp_decode_plan plan{};
+    plan.query_group = g.group;
+    int status = QVP_OK;
+    if (mfma) {
+        status = qvp::launch_mfma_decode(g, batch, a->out_dtype, a->out, ws, ev, s);
+        const qvp_schedule& sc = batch->sched;
+        plan.kernel = QVP_DECODE_MFMA;
+        plan.workgroups = sc.num_wgs;
+        plan.pieces = sc.num_pieces;
+        plan.slots = sc.num_slots;
+        plan.kv_heads_per_segment = sc.hps;
+        plan.deferred_results = sc.defer ? 1u : 0u;
+    } else {
+        const bool f32 = qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens,
+                                                    reinterpret_cast<uintptr_t>(a->query),
+                                                    reinterpret_cast<uintptr_t>(a->kv_base));
+        status = f32 ? qvp::launch_f32_grouped_decode(g, v, a->out_dtype, a->out, ws, ev, s)
+                     : qvp::launch_generic_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s);
+        plan.kernel = f32 ? QVP_DECODE_F32_GROUPED : QVP_DECODE_GENERIC;
+        plan.workgroups = v.num_splits * (f32 ? a->num_kv_heads : a->num_query_heads);
+        plan.pieces = v.num_splits;
+        plan.slots = v.num_splits;
+        plan.kv_heads_per_segment = 1;
+        plan.split_tokens = v.split_tokens;
     }
-    return qvp::launch_generic_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s);
+    if (status == QVP_OK) batch->last_plan = plan;
+    return status;
+}
+
+int qvp_decode_plan_info(const qvp_batch* batch, qvp_decode_plan* plan) {
+    if (batch == nullptr || plan == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "NULL argument");
+    *plan = batch->last_plan;
+    return QVP_OK;
 }
 
 }  // extern "C"

@@ -127,6 +127,21 @@ class AppendArgs(ctypes.Structure):
     ]
 
 
+class DecodePlan(ctypes.Structure):
+    _fields_ = [
+        ("kernel", c_uint32),
+        ("workgroups", c_uint32),
+        ("pieces", c_uint32),
+        ("slots", c_uint32),
+        ("kv_heads_per_segment", c_uint32),
+        ("split_tokens", c_uint32),
+        ("deferred_results", c_uint32),
+        ("query_group", c_uint32),
+    ]
+
+
+DECODE_KERNELS = {0: "none", 1: "mfma", 2: "f32_grouped", 3: "generic"}
+
 _u32p = POINTER(c_uint32)
 _u64p = POINTER(c_uint64)
 
@@ -171,6 +186,7 @@ SIGNATURES = {
     "qvp_batch_view": (c_int, [c_void_p, POINTER(PackedView)]),
     "qvp_decode_workspace_bytes": (c_int, [c_void_p, c_uint32, c_uint32, _u64p]),
     "qvp_paged_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "qvp_decode_plan_info": (c_int, [c_void_p, POINTER(DecodePlan)]),
     "qvp_copy_blocks": (c_int, [c_void_p, c_uint64, c_uint32, _u32p, _u32p, c_uint32, c_uint64, c_void_p]),
     "qvp_swap_gather": (
         c_int,
@@ -483,6 +499,14 @@ class Batch:
         synchronize()
         out["block_tables"] = out["block_tables"].reshape(B, nb)
         return out
+
+    def decode_plan(self) -> dict:
+        """The work decomposition of the last decode on this pack."""
+        p = DecodePlan()
+        check(load().qvp_decode_plan_info(self.handle, byref(p)))
+        d = {name: int(getattr(p, name)) for name, _ in DecodePlan._fields_}
+        d["kernel"] = DECODE_KERNELS.get(d["kernel"], str(d["kernel"]))
+        return d
 
     def workspace_bytes(self, num_query_heads: int, head_dim: int) -> int:
         n = c_uint64(0)

@@ -20,7 +20,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-from qvp import DTYPE_BF16, DTYPE_F32, layout_strides
+from qvp import DTYPE_BF16, DTYPE_F16, DTYPE_F32, layout_strides
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -86,6 +86,16 @@ def bf16_bits_to_f32(h: np.ndarray) -> np.ndarray:
     return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
 
 
+def to_elements(x: np.ndarray, kv_dtype: int) -> np.ndarray:
+    """float32 draws in the cache element type: fp32 as is, bf16 and fp16 as
+    round-to-nearest-even bit patterns (fp16 through numpy's float16)."""
+    if kv_dtype == DTYPE_F32:
+        return np.asarray(x, np.float32)
+    if kv_dtype == DTYPE_BF16:
+        return f32_to_bf16_bits(x)
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
 def shuffled_allocation_order(num_blocks: int, seed: int) -> np.ndarray:
     """Frame ids in the order allocate() returns them after allocate-all and a
     release in seeded permutation order."""
@@ -140,15 +150,15 @@ class Workload:
         return self.num_query_heads // self.num_kv_heads
 
     def query(self) -> np.ndarray:
-        """Query [B][Hq][D] in the cache element type (fp32 or bf16 bits)."""
+        """Query [B][Hq][D] in the cache element type (fp32, or bf16 / fp16 bits)."""
         n = self.num_seqs * self.num_query_heads * self.head_dim
         q = normal(self.seed ^ 0x5151, n, self.q_sigma).reshape(self.num_seqs, self.num_query_heads, self.head_dim)
-        return q if self.kv_dtype == DTYPE_F32 else f32_to_bf16_bits(q)
+        return to_elements(q, self.kv_dtype)
 
     def pool_image(self, chunk_elems: int = 1 << 24) -> np.ndarray:
         """Host image of the whole pool (num_pool_blocks * block_stride bytes):
         every element of every frame drawn N(0, kv_sigma^2) (fp32, or rounded
-        to bf16), padding bytes zero."""
+        to bf16 / fp16), padding bytes zero."""
         per_frame = self.block_bytes // self.elem_bytes
         total = per_frame * self.num_pool_blocks
         np_dtype = np.float32 if self.kv_dtype == DTYPE_F32 else np.uint16
@@ -156,7 +166,7 @@ class Workload:
         for off in range(0, total, chunk_elems):
             n = min(chunk_elems, total - off)
             v = normal(self.seed ^ 0xCAC4E, n, self.kv_sigma, offset=off // 2)
-            elems[off:off + n] = v if self.kv_dtype == DTYPE_F32 else f32_to_bf16_bits(v)
+            elems[off:off + n] = to_elements(v, self.kv_dtype)
         frames = elems.view(np.uint8).reshape(self.num_pool_blocks, self.block_bytes)
         if self.block_stride == self.block_bytes:
             return frames.reshape(-1)

@@ -6,7 +6,9 @@ sources where that tree is present). Run from the repository root:
 
 Fixtures (data only: inputs are regenerated from seeds, outputs stored):
   decode_goldens.npz       paged_attention_decode<T> of the reference on
-                           config1 (fp32) and two bf16 workloads, with a SHA-256
+                           config1 (fp32), two bf16 workloads and an fp16
+                           workload (T = an IEEE half whose conversions are the
+                           x86 F16C instructions), with a SHA-256
                            of each workload's pool image and query so that a
                            drift of the input generators is caught
   scheduler_trace_w4.txt   event log of the continuous-batching trace of
@@ -43,6 +45,7 @@ def golden_workloads() -> dict[str, W.Workload]:
         "bf16_gqa7": W.custom([1, 17, 300, 64], 28, 4, 128, W.DTYPE_BF16, seed=21),
         "bf16_tpb32": W.custom([33, 95, 700], 16, 2, 128, W.DTYPE_BF16, tokens_per_block=32, seed=22,
                                num_layers=2, layer=1),
+        "f16_gqa4": W.custom([1, 17, 300, 64, 513], 16, 4, 128, W.DTYPE_F16, seed=23, kv_sigma=1.0),
     }
 
 
@@ -54,7 +57,7 @@ def input_digest(w: W.Workload) -> str:
 
 
 def reference_decode(w: W.Workload) -> np.ndarray:
-    dtype = O.ORC_F32 if w.kv_dtype == W.DTYPE_F32 else O.ORC_BF16
+    dtype = {W.DTYPE_F32: O.ORC_F32, W.DTYPE_BF16: O.ORC_BF16, W.DTYPE_F16: O.ORC_F16}[w.kv_dtype]
     sess = O.RefSession(w.pool_image(), w.block_stride, w.num_pool_blocks, w.tokens_per_block, w.num_layers,
                         w.num_kv_heads, w.head_dim, w.elem_bytes)
     refused, out, _ = sess.decode(w.ids, w.cu_blocks, w.context_lens, dtype, w.query(), w.layer,

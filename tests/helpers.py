@@ -23,12 +23,11 @@ def tiled_pool_image(w: W.Workload, chunk_elems: int = 16_777_259) -> np.ndarray
     N(0, kv_sigma^2) elements of the cache type (bf16 or fp32) repeated over the
     frames. The chunk length is odd, so no two frames see the same bytes at the
     same offsets."""
-    assert w.kv_dtype in (qvp.DTYPE_BF16, qvp.DTYPE_F32) and w.block_stride == w.block_bytes
+    assert w.block_stride == w.block_bytes
     esz = qvp.DTYPE_BYTES[w.kv_dtype]
     total = w.num_pool_blocks * w.block_bytes // esz
     chunk = np.random.default_rng(w.seed).normal(0.0, w.kv_sigma, chunk_elems).astype(np.float32)
-    if w.kv_dtype == qvp.DTYPE_BF16:
-        chunk = W.f32_to_bf16_bits(chunk)
+    chunk = W.to_elements(chunk, w.kv_dtype)
     reps = -(-total // chunk_elems)
     return np.tile(chunk, reps)[:total].view(np.uint8)
 

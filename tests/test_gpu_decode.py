@@ -50,9 +50,52 @@ def test_config2_bf16_matches_oracle_fp32_and_bf16_outputs():
 
 
 @pytest.mark.parametrize("split", [128, 256, 512, 1024, 4096])
-def test_split_size_does_not_change_the_result(split):
-    print(f"case: config2 B=8 split={split}", flush=True)
-    _parity(W.config2(seed=11, num_seqs=8), out_dtypes=(qvp.DTYPE_F32,), split_tokens=split)
+@pytest.mark.parametrize("kv_dtype", [qvp.DTYPE_F32, qvp.DTYPE_F16], ids=["f32-grouped", "generic-f16"])
+def test_split_kernels_follow_the_split_size(kv_dtype, split):
+    """The fp32 and generic kernels partition each sequence into split_tokens
+    pieces and merge them; every partition size gives the oracle's result."""
+    print(f"case: split kernels dtype={kv_dtype} split={split}", flush=True)
+    lens = [37, 600, 1500, 4096, 129, 2049]
+    if kv_dtype == qvp.DTYPE_F32:
+        w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=11, kv_sigma=1.0)
+        run = GpuRun(w)
+    else:
+        w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F16, seed=11)
+        w32 = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=11, kv_sigma=0.5)
+        image = w32.pool_image().view(np.float32).astype(np.float16).view(np.uint8)
+        run = GpuRun(w, image=image, query=w32.query().astype(np.float16).view(np.uint16))
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32, split_tokens=split)
+    plan = run.batch.decode_plan()
+    assert plan["kernel"] == ("f32_grouped" if kv_dtype == qvp.DTYPE_F32 else "generic"), plan
+    assert plan["split_tokens"] == split, plan
+    expect_splits = int(sum(-(-int(n) // split) for n in lens))
+    assert plan["pieces"] == expect_splits, plan
+    if kv_dtype == qvp.DTYPE_F32:
+        err = float(np.abs(got - ref32).max())
+        assert err <= F32_ABS_TOL, f"fp32 max abs {err:.3e}"
+    else:
+        assert_close_bf16(got, ref32, f"fp16 split={split}")
+
+
+def test_mfma_path_ignores_the_split_size():
+    """The bf16 MFMA kernel cuts the batch into cost-balanced tile ranges
+    instead of split_tokens partitions: every split size packs to the same
+    schedule and the same bits."""
+    w = W.config2(seed=11, num_seqs=8)
+    run = GpuRun(w)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    first = None
+    for split in (128, 512, 4096):
+        print(f"case: mfma path split={split}", flush=True)
+        got = run.decode(out_dtype=qvp.DTYPE_F32, split_tokens=split)
+        plan = run.batch.decode_plan()
+        assert plan["kernel"] == "mfma" and plan["split_tokens"] == 0, plan
+        if first is None:
+            first = got
+            assert_close_bf16(got, ref32, "mfma path")
+        else:
+            assert np.array_equal(first.view(np.uint32), got.view(np.uint32)), f"split {split} changed the bits"
 
 
 EDGE_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 511, 512, 513, 1000]
@@ -121,6 +164,85 @@ def test_pool_base_off_the_kib_grid_takes_equal_head_weights():
 def test_config3_subset_72b_shape():
     print("case: config3 shape, 2 sequences", flush=True)
     _parity(W.config3(num_seqs=2), out_dtypes=(qvp.DTYPE_F32,))
+
+
+def test_config3_full_batch_matches_oracle():
+    """The whole 72B batch (B=32, ctx U[8192, 32768], Hq 64 / Hkv 8): with
+    this many tiles per resident wave the schedule decodes four kv heads side
+    by side with GQA group 8 (32 rows per segment in the LDS merge, the
+    deferred piece results and the final slot merge), the path its benchmark
+    figure runs. Compared with the oracle on every output element, fp32 and
+    bf16 outputs (tests/PagedAttention.test.cpp:460-495 at batch scale)."""
+    w = W.config3()
+    print(f"case: config3 full batch B={w.num_seqs} total tokens {int(w.context_lens.sum())}", flush=True)
+    run = GpuRun(w, image=tiled_pool_image(w))
+    ref_out, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    plan = run.batch.decode_plan()
+    print(f"plan: {plan}", flush=True)
+    assert plan["kernel"] == "mfma" and plan["kv_heads_per_segment"] == 4 and plan["query_group"] == 8, plan
+    assert plan["slots"] > 0, plan
+    assert_close_bf16(got, ref32, "config3 fp32 out")
+    got16 = run.decode(out_dtype=qvp.DTYPE_BF16)
+    assert_close_16bit(got16, ref32, qvp.DTYPE_BF16, "config3 bf16 out")
+    assert_close_16bit(got16, to_f32(ref_out, qvp.DTYPE_BF16), qvp.DTYPE_BF16, "config3 vs oracle T out")
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,total_tokens",
+    [
+        (64, 8, 300_000),    # four kv heads per segment, GQA group 8
+        (28, 4, 560_000),    # four kv heads per segment, GQA group 7 (the 7B shape, long contexts)
+        (42, 6, 380_000),    # two kv heads per segment, GQA group 7
+        (16, 2, 1_080_000),  # two kv heads per segment, GQA group 8
+    ],
+    ids=["hps4-g8", "hps4-g7", "hps2-g7", "hps2-g8"],
+)
+def test_kv_head_groups_with_gqa_groups(hq, hkv, total_tokens):
+    """kv heads side by side (>= 32 tiles per resident wave) with a GQA group
+    above one: each segment carries hps x G query rows through the per-piece
+    LDS merge, the deferred results and the split merge."""
+    rng = np.random.default_rng(hq * 1000 + hkv)
+    cuts = np.sort(rng.choice(np.arange(1, total_tokens), size=9, replace=False))
+    lens = [int(x) for x in np.diff(np.concatenate([[0], cuts, [total_tokens]]))]
+    lens.insert(4, 37)  # a short sequence among long ones stays one whole segment
+    print(f"case: kv head groups hq={hq} hkv={hkv} lens={lens}", flush=True)
+    w = W.custom(lens, hq, hkv, 128, seed=hq + hkv, spare=0.02)
+    run = GpuRun(w, image=tiled_pool_image(w))
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    plan = run.batch.decode_plan()
+    print(f"plan: {plan}", flush=True)
+    assert plan["kernel"] == "mfma" and plan["query_group"] == hq // hkv, plan
+    assert plan["kv_heads_per_segment"] == (4 if hkv % 4 == 0 else 2), plan
+    assert_close_bf16(got, ref32, f"kv head groups hq={hq} hkv={hkv}")
+
+
+def test_one_packed_batch_decoded_with_two_query_group_sizes():
+    """One pack, decoded first with 4 query heads on 4 kv heads and then with
+    32 on the same 4 kv heads, without repacking: the cached work schedule
+    sizes its per-piece LDS and slots by the GQA group, so the second decode
+    must not reuse the first one's."""
+    lens = [100, 2000, 513, 3000, 64, 1500, 2600, 700]
+    results = {}
+    w_small = W.custom(lens, 4, 4, 128, seed=77)
+    w_big = W.custom(lens, 32, 4, 128, seed=77)
+    assert np.array_equal(w_small.ids, w_big.ids)
+    run = GpuRun(w_small)
+    run.batch.pack(w_small.ids, w_small.cu_blocks, w_small.context_lens, 16, w_small.num_pool_blocks)
+    for w in (w_small, w_big, w_small):
+        print(f"case: same pack, hq={w.num_query_heads} hkv={w.num_kv_heads}", flush=True)
+        q = qvp.DeviceBuffer.from_array(w.query())
+        out = qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4)
+        out.fill(0xFF)
+        args = qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=run.pool.base, block_stride=run.pool.stride,
+                               batch=run.batch, kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_F32, layer=0,
+                               num_layers=1, num_query_heads=w.num_query_heads, num_kv_heads=w.num_kv_heads,
+                               head_dim=128, tokens_per_block=16, scale=w.scale, strides=w.strides)
+        qvp.paged_decode(args)
+        got = out.download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim))
+        _, ref32 = oracle_decode(w, run.image, w.query())
+        results[w.num_query_heads] = assert_close_bf16(got, ref32, f"same pack hq={w.num_query_heads}")
 
 
 @pytest.mark.parametrize("hkv", [16, 6])

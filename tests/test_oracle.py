@@ -3,8 +3,9 @@ the GPU path. No GPU needed.
 
 What pins each oracle function:
   decode    bitwise equality with the reference's own paged_attention_decode<T>
-            (committed fixture tests/golden/decode_goldens.npz, and the live
-            compiled reference oracle/_ref where it was built); the closed-form
+            for T = float, bf16 and fp16 (committed fixture
+            tests/golden/decode_goldens.npz, and the live compiled reference
+            oracle/_ref where it was built); the closed-form
             cases of the reference suite (tests/PagedAttention.test.cpp:380-566:
             equal keys -> mean of values, one-hot keys -> exact selection, GQA
             head mapping, layer isolation, copy-on-write branches); float64
@@ -14,6 +15,9 @@ What pins each oracle function:
   pack      block tables equal the CSR ids (BlockTable::entries() order),
             lengths and prefix sums by construction, split bookkeeping
   copy      memcpy identity, other frames untouched
+  fp16/bf16 conversions: numpy's float16 on every half bit pattern and on
+            edge and random floats (ties, overflow, subnormals); bf16 on ties,
+            infinities, NaN and random floats
 A planted mistake (in a Python restatement, on the CPU) shows the closed-form
 checks reject plausible errors: swapped K/V, a dropped scale, a wrong GQA map.
 """
@@ -79,8 +83,11 @@ def textbook(q, K, V, scale, group):
 # Decode against the reference itself
 # ---------------------------------------------------------------------------
 
+ORC_DTYPE = {W.DTYPE_F32: O.ORC_F32, W.DTYPE_BF16: O.ORC_BF16, W.DTYPE_F16: O.ORC_F16}
+
+
 def _oracle_out(w: W.Workload):
-    dtype = O.ORC_F32 if w.kv_dtype == W.DTYPE_F32 else O.ORC_BF16
+    dtype = ORC_DTYPE[w.kv_dtype]
     refused, out, _ = O.decode_batch(w.pool_image(), w.block_stride, w.num_pool_blocks, w.ids, w.cu_blocks,
                                      w.context_lens, dtype, w.query(), w.layer, w.num_layers, w.num_query_heads,
                                      w.num_kv_heads, w.head_dim, w.tokens_per_block, w.scale, 4)
@@ -95,7 +102,7 @@ def _golden_workloads():
     return make_golden.golden_workloads(), make_golden.input_digest
 
 
-@pytest.mark.parametrize("name", ["config1", "bf16_gqa7", "bf16_tpb32"])
+@pytest.mark.parametrize("name", ["config1", "bf16_gqa7", "bf16_tpb32", "f16_gqa4"])
 def test_oracle_matches_reference_goldens_bitwise(name):
     workloads, digest = _golden_workloads()
     w = workloads[name]
@@ -114,11 +121,13 @@ def test_oracle_matches_reference_goldens_bitwise(name):
     dict(ctx=[5, 129, 1000], hq=28, hkv=4, d=128, dtype=W.DTYPE_BF16),
     dict(ctx=[7, 64, 257], hq=16, hkv=1, d=96, dtype=W.DTYPE_BF16, tpb=8),
     dict(ctx=[100, 3], hq=12, hkv=3, d=40, dtype=W.DTYPE_F32, tpb=5, layers=3, layer=2),
+    dict(ctx=[1, 33, 500, 129], hq=28, hkv=4, d=128, dtype=W.DTYPE_F16),
+    dict(ctx=[9, 70], hq=6, hkv=2, d=40, dtype=W.DTYPE_F16, tpb=8, layers=2, layer=1),
 ])
 def test_oracle_matches_live_reference_bitwise(case):
     w = W.custom(case["ctx"], case["hq"], case["hkv"], case["d"], case["dtype"], tokens_per_block=case.get("tpb", 16),
                  num_layers=case.get("layers", 1), layer=case.get("layer", 0), seed=31)
-    dtype = O.ORC_F32 if w.kv_dtype == W.DTYPE_F32 else O.ORC_BF16
+    dtype = ORC_DTYPE[w.kv_dtype]
     sess = O.RefSession(w.pool_image(), w.block_stride, w.num_pool_blocks, w.tokens_per_block, w.num_layers,
                         w.num_kv_heads, w.head_dim, w.elem_bytes)
     refused, ref, _ = sess.decode(w.ids, w.cu_blocks, w.context_lens, dtype, w.query(), w.layer, w.num_query_heads,
@@ -476,6 +485,79 @@ def test_bf16_conversion_rounds_to_nearest_even():
     x = np.random.default_rng(0).normal(size=4096).astype(np.float32)
     bits = W.f32_to_bf16_bits(x)
     assert np.array_equal(bits, np.array([lib.orc_bf16_from_f32(float(v)) for v in x], np.uint16))
+
+
+def _f16_edge_and_random_f32(n_random: int = 1_000_000) -> np.ndarray:
+    """float32 values that exercise every branch of a float -> half rounding:
+    ties to even in the normal range, the overflow threshold, subnormal ties,
+    the smallest normal, signed zeros and infinities, plus random bit patterns
+    over the whole exponent range and random normals."""
+    ulp = lambda e: 2.0 ** (e - 10)  # noqa: E731 - half spacing at exponent e
+    edges = [0.0, -0.0, 1.0, -1.0, 1 + ulp(0) / 2, 1 + 3 * ulp(0) / 2, 1 + ulp(0) / 2 + 2 ** -20,
+             2.0 - ulp(0) / 4, 65504.0, 65504.0 + 8.0, 65519.99, 65520.0, 65536.0, 1e9, -65520.0,
+             2.0 ** -14, 2.0 ** -14 - 2.0 ** -25, 2.0 ** -14 - 2.0 ** -26, 2.0 ** -24, 2.0 ** -25,
+             3 * 2.0 ** -25, 5 * 2.0 ** -25, 2.0 ** -25 + 2.0 ** -40, 2.0 ** -26, 1e-30, -2.0 ** -25,
+             float("inf"), float("-inf"), 3.14159, -2.71828, 1000.5, 1001.5, 2048.0 + 1.0, 2048.0 + 3.0]
+    rng = np.random.default_rng(16)
+    bits = rng.integers(0, 2 ** 32, n_random // 2, dtype=np.uint64).astype(np.uint32)
+    rand_bits = bits.view(np.float32)
+    rand_bits = rand_bits[~np.isnan(rand_bits)]
+    normals = (rng.normal(size=n_random // 2) * rng.choice([1e-6, 1e-3, 1.0, 1e3, 3e4], n_random // 2)).astype(
+        np.float32)
+    return np.concatenate([np.array(edges, np.float32), rand_bits, normals])
+
+
+def test_f16_to_f32_matches_numpy_on_every_bit_pattern():
+    """orc_f32_from_f16 (oracle.c) against numpy's float16 -> float32 for all
+    65,536 half bit patterns: bitwise, except NaNs, which must stay NaNs of the
+    same sign (a float crossing ctypes may be quieted)."""
+    lib = O.oracle()
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    expect = h.view(np.float16).astype(np.float32)
+    got = np.array([lib.orc_f32_from_f16(int(x)) for x in h], np.float32)
+    nan = np.isnan(expect)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), expect[~nan].view(np.uint32))
+    assert np.array_equal(np.signbit(got[nan]), np.signbit(expect[nan]))
+
+
+def test_f32_to_f16_matches_numpy_rounding():
+    """orc_f16_from_f32 / orc_round_to_f16 (oracle.c) against numpy's
+    float32 -> float16 (round to nearest, ties to even; overflow to infinity;
+    gradual underflow) on edge values and ~10^6 random floats, bitwise; a NaN
+    stays a NaN of the same sign."""
+    lib = O.oracle()
+    x = _f16_edge_and_random_f32()
+    with np.errstate(over="ignore"):
+        expect = x.astype(np.float16).view(np.uint16)
+    got = np.zeros(x.size, np.uint16)
+    lib.orc_round_to_f16(x.ctypes.data, got.ctypes.data, x.size)
+    assert np.array_equal(got, expect), np.flatnonzero(got != expect)[:10]
+    # The scalar entry point agrees with the array one.
+    for v, e in zip(x[:64], expect[:64]):
+        assert lib.orc_f16_from_f32(float(v)) == e
+    for nan in (float("nan"), -float("nan")):
+        h = lib.orc_f16_from_f32(nan)
+        assert (h & 0x7C00) == 0x7C00 and (h & 0x3FF) != 0 and (h >> 15) == int(np.signbit(nan))
+
+
+@pytest.mark.skipif(not O.reference_available(), reason="oracle/_ref not built (reference tree absent)")
+def test_reference_half_type_converts_like_numpy():
+    """The reference decode's fp16 element type (oracle/ref_shim.cpp, x86 F16C
+    conversions) rounds like numpy, so its decode is an independent check of
+    the oracle's fp16 path."""
+    ref = O.reference()
+    x = _f16_edge_and_random_f32(20_000)
+    with np.errstate(over="ignore"):
+        expect = x.astype(np.float16).view(np.uint16)
+    got = np.array([ref.ref_half_from_float(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, expect)
+    h = np.arange(0, 65536, 7, dtype=np.uint32).astype(np.uint16)
+    e32 = h.view(np.float16).astype(np.float32)
+    g32 = np.array([ref.ref_float_from_half(int(v)) for v in h], np.float32)
+    ok = ~np.isnan(e32)
+    assert np.array_equal(g32[ok].view(np.uint32), e32[ok].view(np.uint32))
+    assert np.array_equal(np.isnan(g32), ~ok)
 
 
 def test_workload_generators_are_deterministic():
