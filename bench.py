@@ -116,13 +116,76 @@ def cpu_baseline(w: W.Workload, image: np.ndarray, query: np.ndarray, reps: int)
     }
 
 
+# The decode kernel's sources: a traffic profile holds for the build of these.
+KERNEL_SOURCES = ["decode_mfma.hip", "mfma_tile.h", "decode_common.h", "common.h", "batch.h"]
+
+
+def kernel_source_digest() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        h.update((ROOT / "qwenvl-paged_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def load_traffic() -> dict | None:
-    if TRAFFIC_FILE.exists():
-        try:
-            return json.loads(TRAFFIC_FILE.read_text())
-        except (OSError, ValueError):
-            return None
-    return None
+    """The committed HBM-traffic profile of the decode kernel, if it was
+    measured on the current kernel sources."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    try:
+        t = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel_source_sha256_16") != kernel_source_digest():
+        return None
+    t["source"] = f"{TRAFFIC_FILE.relative_to(ROOT)} (rocprofv3 FETCH_SIZE / WRITE_SIZE, kernel sources " \
+                  f"{t['kernel_source_sha256_16']})"
+    return t
+
+
+def write_traffic(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_write_csv: str,
+                  commands: list[str]) -> int:
+    """Writes the traffic profile from two rocprofv3 --pmc runs of the decode
+    (FETCH_SIZE, WRITE_SIZE, KiB per dispatch) and the same two counters over
+    the plain copy kernel of --copy-calibration (known bytes), stamped with
+    the kernel sources' digest."""
+    import csv as _csv
+
+    def per_dispatch(path: str, counter: str, name_part: str) -> float:
+        vals = [float(r["Counter_Value"]) for r in _csv.DictReader(open(path))
+                if r["Counter_Name"] == counter and name_part in r["Kernel_Name"]]
+        return statistics.median(vals)
+
+    w = W.config2()
+    kb = w.kv_bytes() + w.num_seqs * w.num_query_heads * w.head_dim * 2 + \
+        int(((w.context_lens.astype(np.int64) + 15) // 16).sum()) * 4 + w.num_seqs * 4
+    fetch = per_dispatch(fetch_csv, "FETCH_SIZE", "decode_mfma_persistent")
+    write = per_dispatch(write_csv, "WRITE_SIZE", "decode_mfma_persistent")
+    cf = per_dispatch(copy_fetch_csv, "FETCH_SIZE", "copy_segments")
+    cw = per_dispatch(copy_write_csv, "WRITE_SIZE", "copy_segments")
+    moved = 128 << 20
+    ff, wf = moved / 1024 / cf, moved / 1024 / cw
+    traffic = fetch * 1024 * ff + write * 1024 * wf
+    out = {
+        "kernel": "decode_mfma_persistent<bf16>",
+        "workload": "config2",
+        "kernel_source_sha256_16": kernel_source_digest(),
+        "algorithmic_bytes_per_launch": kb,
+        "fetch_size_kib_per_dispatch": round(fetch, 3),
+        "write_size_kib_per_dispatch": round(write, 3),
+        "fetch_factor": round(ff, 4),
+        "write_factor": round(wf, 4),
+        "bytes_per_launch": int(traffic),
+        "traffic_over_algorithmic": round(traffic / kb, 4),
+        "calibration": {"kernel": "copy_segments", "bytes_read": moved, "bytes_written": moved,
+                        "fetch_size_kib": round(cf, 3), "write_size_kib": round(cw, 3)},
+        "commands": commands,
+    }
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return 0
 
 
 def repeated_pool_image(w: W.Workload, chunk_bytes: int = 64 << 20) -> np.ndarray:
@@ -504,7 +567,13 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
                          "used to scale rocprof FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--traffic-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
+                    help="write profiles/decode_mfma_bf16_d128_config2_traffic.json from rocprofv3 --pmc counter "
+                         "CSVs of the decode (FETCH_SIZE, WRITE_SIZE) and of --copy-calibration (no GPU needed)")
+    ap.add_argument("--traffic-commands", nargs="*", default=[], help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.traffic_summary:
+        return write_traffic(*args.traffic_summary, args.traffic_commands)
     if args.copy_calibration:
         return copy_calibration(args.steps)
     if args.append:
@@ -546,7 +615,7 @@ def main() -> int:
     n_out = w.num_seqs * w.num_query_heads * w.head_dim
     out = qvp.DeviceBuffer(n_out * 2)
     batch = qvp.Batch()
-    view = batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, args.split, stream)
+    batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, args.split, stream)
     ws = qvp.DeviceBuffer(batch.workspace_bytes(w.num_query_heads, w.head_dim))
     setup_s = time.perf_counter() - t_setup
 
@@ -597,14 +666,36 @@ def main() -> int:
     stream.synchronize()
     kernel_ms = [starts[i].elapsed_ms(ends[i]) for i in range(args.steps)]
 
-    # Pack-inclusive step (host pack + pinned H2D of the tables + decode).
-    qvp.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, args.split, stream)
-        qvp.paged_decode(plain[i % len(pools)], stream)
-    stream.synchronize()
-    pack_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    plan = batch.decode_plan()
+
+    # Pack-inclusive steps: every step packs the batch (host pass over the
+    # block ids into pinned staging, the decode's work schedule planned with
+    # it, one upload kernel carrying both) and decodes it.
+    def packed_steps(pack_stream) -> float:
+        ev = qvp.Event()
+        qvp.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            a = plain[i % len(pools)]
+            batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, args.split,
+                       pack_stream, decode=a)
+            if pack_stream is not stream:
+                ev.record(pack_stream)
+                stream.wait(ev)
+            qvp.paged_decode(a, stream)
+        stream.synchronize()
+        qvp.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # (a) one stream: upload and decode of each step in sequence;
+    # (b) engine pipeline: the pack uploads on a second stream while the
+    #     previous step's decode runs (packs alternate between two device
+    #     buffers; the library makes a pack wait for the decode that read its
+    #     buffer two steps before), the decode waits for its pack's upload.
+    pack_stream = qvp.Stream()
+    packed_steps(stream)  # warm-up: staging and device buffers reach their size
+    pack_ms = packed_steps(stream)
+    pipelined_ms = packed_steps(pack_stream)
 
     # Parity spot check of the last output against the CPU reference path is
     # done by the test suite; here only make sure the output is finite.
@@ -640,16 +731,24 @@ def main() -> int:
                 f"Hq64/Hkv8/D128, block 16, bf16 KV, pool +10% spare, {len(pools)} pool copies"),
             "batch": w.num_seqs,
             "cached_tokens": int(w.context_lens.sum()),
-            "split_tokens": view.split_tokens,
-            "num_splits": view.num_splits,
+            # The schedule the decode kernel ran (qvp_decode_plan_info): the
+            # bf16 MFMA kernel cuts cost-balanced tile ranges, one per
+            # workgroup, and has no split-size parameter.
+            "decode_plan": plan,
             "parallelism": "single GPU",
         },
         "pct_of_peak_hbm": round(100.0 * gbps / PEAK_HBM_GBPS, 2),
-        "decode_tokens_per_s": round(w.num_seqs / (ms_per_step * 1e-3), 1),
+        # Tokens/s as B / (per-step wall time of pack + upload + decode), the
+        # engine pipeline of (b) below; kernel-only and one-stream figures beside it.
+        "decode_tokens_per_s": round(w.num_seqs / (pipelined_ms * 1e-3), 1),
+        "decode_tokens_per_s_kernel_only": round(w.num_seqs / (ms_per_step * 1e-3), 1),
         "decode_tokens_per_s_all_layers_attention_only": round(
-            w.num_seqs / ((28 if args.workload == "config2" else 80) * ms_per_step * 1e-3), 1),
+            w.num_seqs / ((28 if args.workload == "config2" else 80) * pipelined_ms * 1e-3), 1),
         "algorithmic_bytes_per_step": algo,
         "step_with_pack_ms": round(pack_ms, 5),
+        "step_with_pack_pipelined_ms": round(pipelined_ms, 5),
+        "step_with_pack_over_kernel": round(pack_ms / kernel_avg, 3),
+        "step_with_pack_pipelined_over_kernel": round(pipelined_ms / kernel_avg, 3),
         "step_with_pack_tokens_per_s": round(w.num_seqs / (pack_ms * 1e-3), 1),
         "roofline": {
             "kernel": "decode_mfma_bf16_d128",
@@ -658,7 +757,11 @@ def main() -> int:
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            # HBM bytes per launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+            # runs of profiles/, valid only for the kernel sources they were
+            # measured on (null when the sources changed since).
             "traffic": traffic.get("bytes_per_launch") if traffic and args.workload == "config2" else None,
+            "traffic_source": traffic.get("source") if traffic else "no traffic profile for these kernel sources",
             "kernel_avg_ms": round(kernel_avg, 5),
             "kernel_isolated_avg_ms": round(statistics.mean(kernel_ms), 5),
             "kernel_bytes_per_launch": kernel_bytes,

@@ -127,7 +127,8 @@ int qvp_event_elapsed_ms(float* ms, void* start, void* stop);
  * qvp_mrope_positions upload host-built lists on every call and are not
  * captured. The kernels reset their own merge counters, so a graph may be
  * replayed any number of times; it reads and writes the buffers it was
- * captured with. */
+ * captured with, so a captured decode stays valid until the second qvp_pack
+ * after the capture on its batch reuses the packed buffer it reads. */
 int qvp_graph_begin_capture(void* stream);
 int qvp_graph_end_capture(void* stream, void** graph_exec);
 int qvp_graph_launch(void* graph_exec, void* stream);
@@ -208,8 +209,14 @@ int qvp_batch_destroy(qvp_batch* batch);
  * mapped blocks, QVP_ERR_UNMAPPED for a missing frame) leaves the batch's
  * previous contents intact (PagedAttention.h:73-89).
  * split_tokens (0 selects 512) is rounded up to a multiple of 128.
- * The arrays are staged in pinned memory (double-buffered) and copied to the
- * device asynchronously on `stream`. */
+ * The arrays are staged in pinned memory and uploaded by one kernel on
+ * `stream`. Packs alternate between two device buffers: the arrays of pack n
+ * stay valid until pack n + 2, so pack n + 1 may be enqueued on another
+ * stream while pack n's decode still runs (the caller makes the decode's
+ * stream wait for the pack's). Decodes and prefills enqueued through this
+ * library are tracked: pack n + 2 waits on the device for them, whatever
+ * stream they ran on. Other readers of qvp_batch_view's pointers must be
+ * ordered before pack n + 2 by the caller. */
 int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
              const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
              uint32_t num_pool_blocks, uint32_t split_tokens, void* stream);
@@ -261,6 +268,23 @@ int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads,
  * and the split-merge kernel on `stream`. With workspace == NULL the library
  * uses a per-device workspace it grows on demand. */
 int qvp_paged_decode(const qvp_decode_args* args, void* stream);
+
+/* qvp_pack, plus the work schedule of the decode the pack is for, built now
+ * and uploaded with the packed arrays in the same single upload (a later
+ * qvp_paged_decode with the same query-head count, kv-head count and cache
+ * layout finds it ready and enqueues only its kernel; a decode with other
+ * arguments builds its own). `decode` describes that decode exactly as
+ * qvp_paged_decode will receive it; its `batch` field is ignored and it is
+ * validated by the same rules (a refusal packs nothing). NULL is qvp_pack.
+ * A decode the persistent MFMA kernel does not run needs no schedule: the
+ * pack then equals qvp_pack. No reference counterpart: the reference
+ * resolves blocks per token inside paged_attention_decode
+ * (PagedAttention.h:73-89); this moves a step's host work and its upload
+ * into the pack. */
+int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
+                        const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
+                        uint32_t num_pool_blocks, uint32_t split_tokens, const qvp_decode_args* decode,
+                        void* stream);
 
 /* The work decomposition of the last qvp_paged_decode enqueued on a batch.
  * No reference counterpart (the reference decodes one sequence at a time,

@@ -131,7 +131,7 @@ int launch_list(const AppendGeometry& g, const uint32_t* frames, const uint32_t*
         sg.device[k] = nullptr;
         sg.cap[k] = 0;
         const size_t cap = std::max<size_t>(count, 4096);
-        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&sg.host[k]), cap * sizeof(uint64_t), hipHostMallocDefault));
+        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&sg.host[k]), cap * sizeof(uint64_t), hipHostMallocCoherent));
         QVP_HIP(hipMalloc(reinterpret_cast<void**>(&sg.device[k]), cap * sizeof(uint64_t)));
         sg.cap[k] = cap;
     }
@@ -139,7 +139,7 @@ int launch_list(const AppendGeometry& g, const uint32_t* frames, const uint32_t*
         sg.host[k][i] = static_cast<uint64_t>(frames[i]) * block_stride + static_cast<uint64_t>(slots[i]) * token_stride;
     }
     if (sg.kernel_pending[k]) QVP_HIP(hipStreamWaitEvent(st, sg.consumed[k], 0));
-    QVP_HIP(hipMemcpyAsync(sg.device[k], sg.host[k], count * sizeof(uint64_t), hipMemcpyHostToDevice, st));
+    QVP_TRY(qvp::pull_from_pinned(sg.device[k], sg.host[k], count * sizeof(uint64_t), st));
     QVP_HIP(hipEventRecord(sg.copied[k], st));
     sg.copy_pending[k] = true;
     hipLaunchKernelGGL(append_rows_list, dim3(count, layer_count, 2), dim3(kAppendThreads), 0, st, g, sg.device[k]);

@@ -15,6 +15,18 @@ struct qvp_piece {
     int32_t b, g, t0, t1, ctx, slot, seg_slot0, seg_nslots;
 };
 
+// The last enqueued consumer of a device buffer: its stream, and an event
+// recorded right after the read when it ran beside the buffer's writer. A
+// writer on another stream waits for that event on the device (recording one
+// on the reader's stream first when none was needed then; that stream must
+// still exist).
+struct qvp_reader {
+    hipEvent_t event{nullptr};
+    hipStream_t stream{nullptr};
+    bool pending{false};
+    bool recorded{false};  // event already marks the read
+};
+
 // Balanced schedule of the persistent MFMA decode for one packed batch and one
 // kv-head count. Device layout (int32 units, each array 256-byte aligned):
 //   wg_begin[num_wgs + 1]  CSR over pieces per workgroup
@@ -25,6 +37,13 @@ struct qvp_piece {
 //                          workgroup's piece range (begin, end)
 struct qvp_schedule {
     bool valid{false};
+    // Device words of the schedule in use: either the batch's packed buffer
+    // (built with the pack) or this schedule's own buffer (built at decode).
+    int32_t* words{nullptr};
+    bool in_pack_buffer{false};
+    // Host plan between planning and writing: per-workgroup piece CSR and pieces.
+    std::vector<int32_t> plan_wg_begin;
+    std::vector<qvp_piece> plan_pieces;
     uint64_t pack_generation{0};
     uint32_t num_kv_heads{0};
     uint32_t group{0};  // query heads per kv head (sizes the deferred LDS and the slots)
@@ -49,6 +68,7 @@ struct qvp_schedule {
     int staging_slot{0};
     int32_t* device{nullptr};
     size_t device_cap{0};
+    qvp_reader reader;  // last decode that read `device`
 };
 
 // Work list of a causal prefill over one packed batch (rebuilt per call: the
@@ -64,19 +84,30 @@ struct qvp_prefill_plan {
     qvp_batch* virt{nullptr};
 };
 
+// A packed batch. Packs alternate between two slots, each a pinned staging
+// buffer and a device buffer (the packed arrays, then optionally the decode
+// schedule built with them): packing step n + 1 neither waits for step n's
+// upload on the host nor overwrites the arrays step n's decode reads.
 struct qvp_batch {
     int32_t* staging[2]{nullptr, nullptr};
     size_t staging_cap[2]{0, 0};  // in int32 elements
     hipEvent_t staging_done[2]{nullptr, nullptr};
     bool staging_pending[2]{false, false};
-    int parity{0};
-    int32_t* device{nullptr};
-    size_t device_cap{0};
+    int parity{0};                 // slot the next pack fills
+    int current{0};                // slot of the last successful pack
+    int32_t* device[2]{nullptr, nullptr};
+    size_t device_cap[2]{0, 0};    // in int32 elements
+    qvp_reader readers[2];         // last decode / prefill that read each slot
+    hipStream_t upload_stream[2]{nullptr, nullptr};  // stream of each slot's upload
     bool valid{false};
     uint64_t generation{0};            // bumped by every successful pack
     std::vector<int32_t> host_seq_lens;  // host copy of seq_lens for scheduling
     std::vector<uint32_t> host_ids;      // host copy of the needed block ids, CSR over host_cu_blocks
     std::vector<uint32_t> host_cu_blocks;
+    // Scratch of a pack that plans a schedule before the batch is replaced.
+    std::vector<int32_t> lens_scratch;
+    std::vector<uint32_t> ids_scratch;
+    std::vector<uint32_t> cu_scratch;
     qvp_packed_view view{};
     qvp_decode_plan last_plan{};       // what the last decode on this pack ran (reset by qvp_pack)
     qvp_schedule sched{};
@@ -84,6 +115,13 @@ struct qvp_batch {
 };
 
 namespace qvp {
+// Makes `stream` wait on the device for a buffer's last reader when that
+// reader was enqueued on another stream.
+int wait_for_reader(qvp_reader& r, hipStream_t stream);
+// Records `stream` as a buffer's last reader (call after its kernels);
+// `writer` is the stream that wrote the buffer.
+int note_reader(qvp_reader& r, hipStream_t stream, hipStream_t writer);
+void destroy_reader(qvp_reader& r);
 // Frees the schedule's buffers (called by qvp_batch_destroy).
 void destroy_schedule(qvp_schedule& s);
 // Frees the prefill plan's buffers and its private batch.

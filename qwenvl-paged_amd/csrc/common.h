@@ -38,6 +38,15 @@ int hip_fail(hipError_t err, const char* what);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Copies `bytes` (a multiple of 4; both pointers 16-byte aligned) from pinned
+// host memory allocated by hipHostMalloc with hipHostMallocCoherent (so the
+// GPU never holds a stale cached copy of a staging buffer the host refilled)
+// into device memory, with a kernel on `stream` that reads the host buffer
+// over the bus. A runtime host-to-device copy would go to the DMA engine and
+// pay two cross-engine handoffs between the surrounding kernels; the kernel
+// stays on the compute queue.
+int pull_from_pinned(void* dst, const void* pinned_host, size_t bytes, hipStream_t stream);
+
 inline size_t dtype_size(uint32_t dtype) {
     switch (dtype) {
         case QVP_DTYPE_F32: return 4;

@@ -64,10 +64,33 @@ bool f32_grouped_supported(const DecodeGeometry& g, uint32_t kv_dtype, uint32_t 
 int launch_f32_grouped_decode(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t out_dtype, void* out,
                               void* workspace, hipEvent_t split_event, hipStream_t stream);
 
+// Validates decode arguments against a packed view (every refusal of
+// qvp_paged_decode) and fills the kernels' geometry. *supported_mfma tells
+// whether the persistent MFMA kernel runs this decode.
+int decode_geometry(const qvp_decode_args* a, const qvp_packed_view& v, DecodeGeometry* g, bool* supported_mfma);
+
 // MFMA path (bf16, head_dim 128, group <= 16, power-of-two tpb >= 16):
 // persistent workgroups over a balanced schedule built from the batch.
 bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr,
                     uintptr_t kv_base_addr);
+
+// The host-side batch a schedule is planned from (context lengths and the
+// needed block ids in CSR form).
+struct ScheduleInput {
+    uint32_t num_seqs;
+    const int32_t* lens;
+    const uint32_t* ids;
+    const uint32_t* cu_blocks;
+    uint32_t tpb;
+    uint64_t generation;  // pack generation the schedule will belong to
+};
+// True when the batch's schedule was built for this pack and this geometry.
+bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g);
+// Plans the schedule (host): fills s's plan, sizes and key; s.total words.
+int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry& g);
+// Writes the planned schedule's s.total words to h (pinned staging).
+void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t* h);
+// Builds and uploads the schedule on `stream` unless it is current.
 int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream);
 uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim);
 int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t out_dtype, void* out,

@@ -653,6 +653,7 @@ void destroy_schedule(qvp_schedule& s) {
         if (s.staging_done[i] != nullptr) (void)hipEventDestroy(s.staging_done[i]);
     }
     if (s.device != nullptr) (void)hipFree(s.device);
+    destroy_reader(s.reader);
     s = qvp_schedule{};
 }
 
@@ -665,24 +666,31 @@ bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_
            aligned;
 }
 
-int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream) {
+bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g) {
+    const qvp_schedule& s = batch->sched;
+    if (!s.valid || s.pack_generation != batch->generation || s.num_kv_heads != g.num_kv_heads ||
+        s.group != g.group) {
+        return false;
+    }
+    uint32_t max_wgs = 0;
+    if (device_max_wgs(&max_wgs) != QVP_OK || s.max_wgs != max_wgs) return false;
+    const uint32_t nq = s.num_kv_heads / s.hps;
+    return s.weights == head_group_weights(g, s.hps, nq);
+}
+
+int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry& g) {
     const uint32_t num_kv_heads = g.num_kv_heads;
-    qvp_schedule& s = batch->sched;
     uint32_t max_wgs = 0;
     QVP_TRY(device_max_wgs(&max_wgs));
-    const std::vector<int32_t>& lens = batch->host_seq_lens;
-    std::vector<uint64_t> pos_cum(lens.size() + 1, 0);
-    for (size_t b = 0; b < lens.size(); ++b) {
-        pos_cum[b + 1] = pos_cum[b] + (static_cast<uint64_t>(lens[b]) + kTileTokens - 1) / kTileTokens;
+    const uint32_t nseq = in.num_seqs;
+    std::vector<uint64_t> pos_cum(nseq + 1, 0);
+    for (uint32_t b = 0; b < nseq; ++b) {
+        pos_cum[b + 1] = pos_cum[b] + (static_cast<uint64_t>(in.lens[b]) + kTileTokens - 1) / kTileTokens;
     }
-    const uint64_t T = pos_cum[lens.size()];
+    const uint64_t T = pos_cum[nseq];
     const uint32_t hps = head_group_size(num_kv_heads, T, max_wgs);
     const uint32_t nq = num_kv_heads / hps;
     const std::vector<double> weights = head_group_weights(g, hps, nq);
-    if (s.valid && s.pack_generation == batch->generation && s.num_kv_heads == num_kv_heads &&
-        s.group == g.group && s.max_wgs == max_wgs && s.weights == weights) {
-        return QVP_OK;
-    }
     s.valid = false;
 
     // Segments (b, q): sequence b's kv heads q * hps .. q * hps + hps - 1. With
@@ -735,9 +743,11 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
         return x.begin != y.begin ? x.begin < y.begin : x.q < y.q;
     });
     const uint32_t Wn = static_cast<uint32_t>(ranges.size());
-    std::vector<int32_t> wg_begin(Wn + 1);
-    std::vector<qvp_piece> pieces;
-    pieces.reserve(static_cast<size_t>(Wn) + lens.size() * nq);
+    std::vector<int32_t>& wg_begin = s.plan_wg_begin;
+    std::vector<qvp_piece>& pieces = s.plan_pieces;
+    wg_begin.assign(Wn + 1, 0);
+    pieces.clear();
+    pieces.reserve(static_cast<size_t>(Wn) + static_cast<size_t>(nseq) * nq);
     for (uint32_t w = 0; w < Wn; ++w) {
         const RangeRef& rr = ranges[w];
         wg_begin[w] = static_cast<int32_t>(pieces.size());
@@ -751,7 +761,7 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
             pc.g = static_cast<int32_t>(rr.q);
             pc.t0 = static_cast<int32_t>(pos - pos_cum[b]);
             pc.t1 = static_cast<int32_t>(end - pos_cum[b]);
-            pc.ctx = lens[b];
+            pc.ctx = static_cast<int32_t>(in.lens[b]);
             pc.slot = -1;
             pc.seg_slot0 = -1;
             pc.seg_nslots = 0;
@@ -766,7 +776,7 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     // group) order. A head group's ranges were laid out in position order,
     // so a segment's pieces already appear in tile order: one counting pass
     // numbers them (no sort).
-    const size_t nseg = lens.size() * nq;
+    const size_t nseg = static_cast<size_t>(nseq) * nq;
     std::vector<int32_t> seg_count(nseg, 0), seg_base(nseg, -1), seg_next(nseg, 0);
     for (const qvp_piece& pc : pieces) ++seg_count[static_cast<size_t>(pc.b) * nq + pc.g];
     int32_t next_slot = 0;
@@ -814,6 +824,70 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     const size_t first_words = static_cast<size_t>(Wn) * kWaves * kFirstWords;
     s.total = s.off_first + align_ints(first_words);
 
+    s.pack_generation = in.generation;
+    s.num_kv_heads = num_kv_heads;
+    s.group = g.group;
+    s.max_wgs = max_wgs;
+    s.weights = weights;
+    s.num_wgs = Wn;
+    s.num_pieces = static_cast<uint32_t>(pieces.size());
+    s.num_slots = static_cast<uint32_t>(next_slot);
+    s.hps = hps;
+    s.max_partial_pieces_per_wg = max_partial;
+    return QVP_OK;
+}
+
+void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t* h) {
+    const std::vector<int32_t>& wg_begin = s.plan_wg_begin;
+    const std::vector<qvp_piece>& pieces = s.plan_pieces;
+    const uint32_t Wn = s.num_wgs;
+    const int32_t hps = static_cast<int32_t>(s.hps);
+    std::fill(h, h + s.total, 0);  // counters start at zero
+    std::copy(wg_begin.begin(), wg_begin.end(), h + s.off_wg_begin);
+    const int32_t* praw = reinterpret_cast<const int32_t*>(pieces.data());
+    std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
+    // Each wave's first tile, resolved to frames here (the kernel's
+    // next_tile and resolve_tile for its first step), written straight into
+    // the staging buffer (its other words stay zero).
+    uint32_t shift = 0;
+    while ((1u << shift) < in.tpb) ++shift;
+    for (uint32_t w = 0; w < Wn; ++w) {
+        for (int wave = 0; wave < kWaves; ++wave) {
+            int32_t* f = h + s.off_first + (static_cast<size_t>(w) * kWaves + wave) * kFirstWords;
+            const int32_t hl = wave % hps;
+            const int32_t tlane = wave / hps;
+            f[0] = -1;
+            f[5] = wg_begin[w];
+            f[6] = wg_begin[w + 1];
+            for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
+                const qvp_piece& pc = pieces[pi];
+                if (pc.t0 + tlane >= pc.t1) continue;
+                const int32_t t = pc.t0 + tlane;
+                const uint32_t* row = in.ids + in.cu_blocks[pc.b];
+                const int32_t tok0 = t * kTileTokens;
+                f[0] = pi;
+                f[1] = t;
+                f[2] = pc.g * hps + hl;
+                f[3] = static_cast<int32_t>(row[std::min(tok0, pc.ctx - 1) >> shift]);
+                f[4] = static_cast<int32_t>(row[std::min(tok0 + 16, pc.ctx - 1) >> shift]);
+                break;
+            }
+        }
+    }
+}
+
+int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream) {
+    if (mfma_schedule_current(batch, g)) return QVP_OK;
+    qvp_schedule& s = batch->sched;
+    ScheduleInput in{};
+    in.num_seqs = static_cast<uint32_t>(batch->host_seq_lens.size());
+    in.lens = batch->host_seq_lens.data();
+    in.ids = batch->host_ids.data();
+    in.cu_blocks = batch->host_cu_blocks.data();
+    in.tpb = batch->view.tokens_per_block;
+    in.generation = batch->generation;
+    QVP_TRY(mfma_plan_schedule(s, in, g));
+
     const int slot = s.staging_slot;
     s.staging_slot ^= 1;
     if (s.staging_done[slot] == nullptr) {
@@ -830,65 +904,29 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
         s.staging[slot] = nullptr;
         s.staging_cap[slot] = 0;
         QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&s.staging[slot]), s.total * sizeof(int32_t),
-                              hipHostMallocDefault));
+                              hipHostMallocCoherent));
         s.staging_cap[slot] = s.total;
     }
     if (s.device_cap < s.total) {
-        if (s.device != nullptr) QVP_HIP(hipFree(s.device));
+        // The old buffer may still be read by an earlier decode.
+        if (s.device != nullptr) {
+            QVP_HIP(hipDeviceSynchronize());
+            QVP_HIP(hipFree(s.device));
+        }
         s.device = nullptr;
         s.device_cap = 0;
         QVP_HIP(hipMalloc(reinterpret_cast<void**>(&s.device), s.total * sizeof(int32_t)));
         s.device_cap = s.total;
     }
-    int32_t* h = s.staging[slot];
-    std::fill(h, h + s.total, 0);  // counters start at zero
-    std::copy(wg_begin.begin(), wg_begin.end(), h + s.off_wg_begin);
-    const int32_t* praw = reinterpret_cast<const int32_t*>(pieces.data());
-    std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
-    // Each wave's first tile, resolved to frames here (the kernel's
-    // next_tile and resolve_tile for its first step), written straight into
-    // the staging buffer (its other words stay zero).
-    const uint32_t tpb = batch->view.tokens_per_block;
-    uint32_t shift = 0;
-    while ((1u << shift) < tpb) ++shift;
-    for (uint32_t w = 0; w < Wn; ++w) {
-        for (int wave = 0; wave < kWaves; ++wave) {
-            int32_t* f = h + s.off_first + (static_cast<size_t>(w) * kWaves + wave) * kFirstWords;
-            const int32_t hl = wave % static_cast<int32_t>(hps);
-            const int32_t tlane = wave / static_cast<int32_t>(hps);
-            f[0] = -1;
-            f[5] = wg_begin[w];
-            f[6] = wg_begin[w + 1];
-            for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
-                const qvp_piece& pc = pieces[pi];
-                if (pc.t0 + tlane >= pc.t1) continue;
-                const int32_t t = pc.t0 + tlane;
-                const uint32_t* row = batch->host_ids.data() + batch->host_cu_blocks[pc.b];
-                const int32_t tok0 = t * kTileTokens;
-                f[0] = pi;
-                f[1] = t;
-                f[2] = pc.g * static_cast<int32_t>(hps) + hl;
-                f[3] = static_cast<int32_t>(row[std::min(tok0, pc.ctx - 1) >> shift]);
-                f[4] = static_cast<int32_t>(row[std::min(tok0 + 16, pc.ctx - 1) >> shift]);
-                break;
-            }
-        }
-    }
-
-    QVP_HIP(hipMemcpyAsync(s.device, h, s.total * sizeof(int32_t), hipMemcpyHostToDevice, stream));
+    mfma_write_schedule(s, in, s.staging[slot]);
+    // A decode enqueued on another stream may still read the previous
+    // schedule in this buffer.
+    QVP_TRY(wait_for_reader(s.reader, stream));
+    QVP_TRY(pull_from_pinned(s.device, s.staging[slot], s.total * sizeof(int32_t), stream));
     QVP_HIP(hipEventRecord(s.staging_done[slot], stream));
     s.staging_pending[slot] = true;
-
-    s.pack_generation = batch->generation;
-    s.num_kv_heads = num_kv_heads;
-    s.group = g.group;
-    s.max_wgs = max_wgs;
-    s.weights = weights;
-    s.num_wgs = Wn;
-    s.num_pieces = static_cast<uint32_t>(pieces.size());
-    s.num_slots = static_cast<uint32_t>(next_slot);
-    s.hps = hps;
-    s.max_partial_pieces_per_wg = max_partial;
+    s.words = s.device;
+    s.in_pack_buffer = false;
     s.valid = true;
     return QVP_OK;
 }
@@ -902,10 +940,10 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
                        void* workspace, hipEvent_t split_event, hipStream_t stream) {
     const qvp_schedule& s = batch->sched;
     MfmaArgs a{};
-    a.wg_begin = s.device + s.off_wg_begin;
-    a.pieces = reinterpret_cast<const qvp_piece*>(s.device + s.off_pieces);
-    a.counters = s.device + s.off_counters;
-    a.first = s.device + s.off_first;
+    a.wg_begin = s.words + s.off_wg_begin;
+    a.pieces = reinterpret_cast<const qvp_piece*>(s.words + s.off_pieces);
+    a.counters = s.words + s.off_counters;
+    a.first = s.words + s.off_first;
     const uint64_t rows = static_cast<uint64_t>(s.num_slots) * s.hps * g.group;
     a.ws_ml = static_cast<float*>(workspace);
     a.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + round_up(rows * 2 * sizeof(float), 256));

@@ -246,7 +246,7 @@ extern "C" int qvp_mrope_positions(qvp_mrope* m, const qvp_mrope_span* spans, co
         m->staging_cap[slot] = 0;
         const size_t cap = std::max<size_t>(words, 4096);
         QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&m->staging[slot]), cap * sizeof(int64_t),
-                              hipHostMallocDefault));
+                              hipHostMallocCoherent));
         m->staging_cap[slot] = cap;
     }
     if (m->device_cap < words) {
@@ -313,7 +313,7 @@ extern "C" int qvp_mrope_positions(qvp_mrope* m, const qvp_mrope_span* spans, co
         sent += wlast - wfirst;
     }
 
-    QVP_HIP(hipMemcpyAsync(m->device, m->staging[slot], words * sizeof(int64_t), hipMemcpyHostToDevice, s));
+    QVP_TRY(qvp::pull_from_pinned(m->device, m->staging[slot], words * sizeof(int64_t), s));
     QVP_HIP(hipEventRecord(m->staging_done[slot], s));
     m->staging_pending[slot] = true;
     m->parity ^= 1;

@@ -7,11 +7,15 @@
 // and :73-89 (resolve every needed block before writing any output).
 //
 // Host work is one pass over the CSR input into a pinned staging buffer; the
-// buffers alternate between two calls so the host can fill one while the DMA
-// engine still reads the other, and the device receives all arrays in a single
-// asynchronous copy.
+// device receives all arrays -- and, when the caller names the decode the
+// pack is for, that decode's work schedule -- in a single upload kernel on
+// the caller's stream. Packs alternate between two slots (staging and device
+// buffers), so the host fills one while the device still reads the other,
+// and a pack enqueued on a second stream can upload step n + 1 while step
+// n's decode runs.
 #include "batch.h"
 #include "common.h"
+#include "decode_common.h"
 
 #include <algorithm>
 #include <new>
@@ -74,15 +78,20 @@ int qvp_batch_create(qvp_batch** batch) {
 int qvp_batch_destroy(qvp_batch* batch) {
     if (batch == nullptr) return QVP_OK;
     int status = QVP_OK;
+    // Decodes may still read the buffers.
+    if (batch->readers[0].pending || batch->readers[1].pending || batch->sched.reader.pending) {
+        (void)hipDeviceSynchronize();
+    }
     for (int i = 0; i < 2; ++i) {
         if (batch->staging_pending[i]) (void)hipEventSynchronize(batch->staging_done[i]);
         if (batch->staging[i] != nullptr && hipHostFree(batch->staging[i]) != hipSuccess) {
             status = fail(QVP_ERR_DEVICE, "hipHostFree(staging)");
         }
         (void)hipEventDestroy(batch->staging_done[i]);
-    }
-    if (batch->device != nullptr && hipFree(batch->device) != hipSuccess) {
-        status = fail(QVP_ERR_DEVICE, "hipFree(batch)");
+        if (batch->device[i] != nullptr && hipFree(batch->device[i]) != hipSuccess) {
+            status = fail(QVP_ERR_DEVICE, "hipFree(batch)");
+        }
+        qvp::destroy_reader(batch->readers[i]);
     }
     qvp::destroy_schedule(batch->sched);
     qvp::destroy_prefill_plan(batch->prefill);
@@ -100,6 +109,14 @@ int qvp_batch_view(const qvp_batch* batch, qvp_packed_view* view) {
 int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
              const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
              uint32_t num_pool_blocks, uint32_t split_tokens, void* stream) {
+    return qvp_pack_for_decode(batch, num_seqs, block_ids, cu_blocks, context_lens, tokens_per_block,
+                               num_pool_blocks, split_tokens, nullptr, stream);
+}
+
+int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
+                        const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
+                        uint32_t num_pool_blocks, uint32_t split_tokens, const qvp_decode_args* decode,
+                        void* stream) {
     if (batch == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "batch is NULL");
     if (tokens_per_block == 0) return fail(QVP_ERR_INVALID_ARGUMENT, "tokens_per_block is 0");
     if (num_seqs > 0 && (cu_blocks == nullptr || context_lens == nullptr)) {
@@ -157,29 +174,66 @@ int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
     const Layout lay = make_layout(num_seqs, max_nb, static_cast<uint32_t>(num_splits));
     const int slot = batch->parity;
 
-    // The staging buffer about to be reused may still be read by the copy of
-    // the call before last.
+    // The decode this pack is for, when named and run by the MFMA kernel: its
+    // schedule is planned now and travels in the same upload, after the
+    // packed arrays. Its arguments are validated as qvp_paged_decode would.
+    const uint64_t generation = batch->generation + 1;
+    qvp::ScheduleInput sin{};
+    bool with_schedule = false;
+    if (decode != nullptr && num_seqs > 0) {
+        qvp_packed_view pv{};
+        pv.tokens_per_block = tokens_per_block;
+        pv.num_seqs = num_seqs;
+        pv.max_blocks_per_seq = max_nb;
+        qvp::DecodeGeometry g{};
+        QVP_TRY(qvp::decode_geometry(decode, pv, &g, &with_schedule));
+        if (with_schedule) {
+            batch->lens_scratch.assign(context_lens, context_lens + num_seqs);
+            batch->ids_scratch.clear();
+            batch->cu_scratch.assign(1, 0);
+            for (uint32_t b = 0; b < num_seqs; ++b) {
+                const uint32_t needed = (context_lens[b] + tokens_per_block - 1) / tokens_per_block;
+                batch->ids_scratch.insert(batch->ids_scratch.end(), block_ids + cu_blocks[b],
+                                          block_ids + cu_blocks[b] + needed);
+                batch->cu_scratch.push_back(static_cast<uint32_t>(batch->ids_scratch.size()));
+            }
+            sin.num_seqs = num_seqs;
+            sin.lens = batch->lens_scratch.data();
+            sin.ids = batch->ids_scratch.data();
+            sin.cu_blocks = batch->cu_scratch.data();
+            sin.tpb = tokens_per_block;
+            sin.generation = generation;
+            batch->sched.valid = false;
+            QVP_TRY(qvp::mfma_plan_schedule(batch->sched, sin, g));
+        }
+    }
+    const size_t total = lay.total + (with_schedule ? batch->sched.total : 0);
+
+    // The staging buffer about to be reused may still be read by the upload
+    // of the call before last.
     if (batch->staging_pending[slot]) {
         QVP_HIP(hipEventSynchronize(batch->staging_done[slot]));
         batch->staging_pending[slot] = false;
     }
-    if (batch->staging_cap[slot] < lay.total) {
+    if (batch->staging_cap[slot] < total) {
         if (batch->staging[slot] != nullptr) QVP_HIP(hipHostFree(batch->staging[slot]));
         batch->staging[slot] = nullptr;
         batch->staging_cap[slot] = 0;
-        const size_t cap = std::max<size_t>(lay.total, 4096);
+        const size_t cap = std::max<size_t>(total + total / 4, 4096);
         QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&batch->staging[slot]), cap * sizeof(int32_t),
-                              hipHostMallocDefault));
+                              hipHostMallocCoherent));
         batch->staging_cap[slot] = cap;
     }
-    if (batch->device_cap < lay.total) {
-        batch->valid = false;
-        if (batch->device != nullptr) QVP_HIP(hipFree(batch->device));
-        batch->device = nullptr;
-        batch->device_cap = 0;
-        const size_t cap = std::max<size_t>(lay.total, 4096);
-        QVP_HIP(hipMalloc(reinterpret_cast<void**>(&batch->device), cap * sizeof(int32_t)));
-        batch->device_cap = cap;
+    hipStream_t s = qvp::as_stream(stream);
+    if (batch->device_cap[slot] < total) {
+        // A decode may still read this slot's old buffer.
+        if (batch->readers[slot].pending) QVP_HIP(hipDeviceSynchronize());
+        if (batch->device[slot] != nullptr) QVP_HIP(hipFree(batch->device[slot]));
+        batch->device[slot] = nullptr;
+        batch->device_cap[slot] = 0;
+        const size_t cap = std::max<size_t>(total + total / 4, 4096);
+        QVP_HIP(hipMalloc(reinterpret_cast<void**>(&batch->device[slot]), cap * sizeof(int32_t)));
+        batch->device_cap[slot] = cap;
     }
 
     // Pass 2: fill the staging buffer.
@@ -212,23 +266,34 @@ int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
     }
     cu_seqlens[num_seqs] = token_acc;
     cu_splits[num_seqs] = split_acc;
+    if (with_schedule) qvp::mfma_write_schedule(batch->sched, sin, h + lay.total);
 
-    hipStream_t s = qvp::as_stream(stream);
-    hipError_t err = hipMemcpyAsync(batch->device, h, lay.total * sizeof(int32_t),
-                                    hipMemcpyHostToDevice, s);
-    if (err != hipSuccess) {
+    // The pack before last (same slot) may still be read by a decode on
+    // another stream; one upload then carries the arrays and the schedule.
+    int st = qvp::wait_for_reader(batch->readers[slot], s);
+    if (st == QVP_OK) st = qvp::pull_from_pinned(batch->device[slot], h, total * sizeof(int32_t), s);
+    if (st != QVP_OK) {
         batch->valid = false;
-        return qvp::hip_fail(err, "hipMemcpyAsync(pack)");
+        batch->sched.valid = false;
+        return st;
     }
-    err = hipEventRecord(batch->staging_done[slot], s);
+    hipError_t err = hipEventRecord(batch->staging_done[slot], s);
     if (err != hipSuccess) {
         batch->valid = false;
+        batch->sched.valid = false;
         return qvp::hip_fail(err, "hipEventRecord(pack)");
     }
     batch->staging_pending[slot] = true;
+    batch->upload_stream[slot] = s;
     batch->parity ^= 1;
+    batch->current = slot;
 
-    int32_t* d = batch->device;
+    int32_t* d = batch->device[slot];
+    if (with_schedule) {
+        batch->sched.words = d + lay.total;
+        batch->sched.in_pack_buffer = true;
+        batch->sched.valid = true;
+    }
     qvp_packed_view& v = batch->view;
     v.block_tables = d + lay.tables;
     v.seq_lens = d + lay.seq_lens;
@@ -244,18 +309,71 @@ int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
     v.num_pool_blocks = num_pool_blocks;
     v.max_seq_len = max_len;
     v.total_tokens = total_tokens;
-    batch->host_seq_lens.assign(seq_lens, seq_lens + num_seqs);
-    batch->host_ids.clear();
-    batch->host_cu_blocks.assign(1, 0);
-    for (uint32_t b = 0; b < num_seqs; ++b) {
-        const uint32_t needed = (context_lens[b] + tokens_per_block - 1) / tokens_per_block;
-        batch->host_ids.insert(batch->host_ids.end(), block_ids + cu_blocks[b], block_ids + cu_blocks[b] + needed);
-        batch->host_cu_blocks.push_back(static_cast<uint32_t>(batch->host_ids.size()));
+    if (with_schedule) {
+        std::swap(batch->host_seq_lens, batch->lens_scratch);
+        std::swap(batch->host_ids, batch->ids_scratch);
+        std::swap(batch->host_cu_blocks, batch->cu_scratch);
+    } else {
+        batch->host_seq_lens.assign(context_lens, context_lens + num_seqs);
+        batch->host_ids.clear();
+        batch->host_cu_blocks.assign(1, 0);
+        for (uint32_t b = 0; b < num_seqs; ++b) {
+            const uint32_t needed = (context_lens[b] + tokens_per_block - 1) / tokens_per_block;
+            batch->host_ids.insert(batch->host_ids.end(), block_ids + cu_blocks[b],
+                                   block_ids + cu_blocks[b] + needed);
+            batch->host_cu_blocks.push_back(static_cast<uint32_t>(batch->host_ids.size()));
+        }
     }
-    batch->generation += 1;
+    batch->generation = generation;
     batch->last_plan = qvp_decode_plan{};
     batch->valid = true;
     return QVP_OK;
 }
 
 }  // extern "C"
+
+namespace qvp {
+
+int wait_for_reader(qvp_reader& r, hipStream_t stream) {
+    if (!r.pending || r.stream == stream) return QVP_OK;
+    if (!r.recorded) {
+        // The reader's stream has the read enqueued; an event recorded on it
+        // now completes after that read (and whatever followed it there).
+        if (r.event == nullptr) QVP_HIP(hipEventCreateWithFlags(&r.event, hipEventDisableTiming));
+        QVP_HIP(hipEventRecord(r.event, r.stream));
+        r.recorded = true;
+    }
+    QVP_HIP(hipStreamWaitEvent(stream, r.event, 0));
+    return QVP_OK;
+}
+
+int note_reader(qvp_reader& r, hipStream_t stream, hipStream_t writer) {
+    // Work captured into a graph reads the buffers whenever the graph is
+    // replayed, which no event can stand for; graphs are valid until the
+    // pack after next (see qvp_graph_begin_capture).
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    QVP_HIP(hipStreamIsCapturing(stream, &capture));
+    if (capture != hipStreamCaptureStatusNone) return QVP_OK;
+    r.stream = stream;
+    r.pending = true;
+    r.recorded = false;
+    // Read on another stream than the buffer's writer (an upload pipelined
+    // beside the decodes): the event is recorded right after the read, so
+    // the next write waits for exactly this read, not for later work on the
+    // reader's stream. Reads on the writer's own stream (the one-stream
+    // engine loop) record nothing: an event between back-to-back kernels
+    // stalls the second one.
+    if (stream != writer) {
+        if (r.event == nullptr) QVP_HIP(hipEventCreateWithFlags(&r.event, hipEventDisableTiming));
+        QVP_HIP(hipEventRecord(r.event, stream));
+        r.recorded = true;
+    }
+    return QVP_OK;
+}
+
+void destroy_reader(qvp_reader& r) {
+    if (r.event != nullptr) (void)hipEventDestroy(r.event);
+    r = qvp_reader{};
+}
+
+}  // namespace qvp

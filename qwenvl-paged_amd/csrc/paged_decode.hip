@@ -70,26 +70,14 @@ uint64_t mfma_bound_bytes(const qvp_packed_view& v, uint32_t hq, uint32_t d) {
 
 }  // namespace
 
-extern "C" {
+namespace qvp {
 
-int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads, uint32_t head_dim, uint64_t* bytes) {
-    if (bytes == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "bytes is NULL");
-    qvp_packed_view v{};
-    QVP_TRY(qvp_batch_view(batch, &v));
-    *bytes = std::max(qvp::generic_workspace_bytes(v, num_query_heads, head_dim),
-                      mfma_bound_bytes(v, num_query_heads, head_dim));
-    return QVP_OK;
-}
-
-int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
-    if (a == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "args is NULL");
-    qvp_packed_view v{};
-    QVP_TRY(qvp_batch_view(a->batch, &v));
+int decode_geometry(const qvp_decode_args* a, const qvp_packed_view& v, DecodeGeometry* out, bool* supported_mfma) {
     if (a->query == nullptr || a->out == nullptr || a->kv_base == nullptr) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "query, out or kv_base is NULL");
     }
-    const size_t esz = qvp::dtype_size(a->kv_dtype);
-    const size_t osz = qvp::dtype_size(a->out_dtype);
+    const size_t esz = dtype_size(a->kv_dtype);
+    const size_t osz = dtype_size(a->out_dtype);
     if (esz == 0 || osz == 0) return fail(QVP_ERR_INVALID_ARGUMENT, "unknown dtype");
     if (a->num_query_heads == 0 || a->num_kv_heads == 0 || a->num_query_heads % a->num_kv_heads != 0) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "%u query heads do not group onto %u kv heads", a->num_query_heads,
@@ -116,9 +104,8 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
                     static_cast<unsigned long long>(last_elem * esz),
                     static_cast<unsigned long long>(a->block_stride));
     }
-    if (v.num_seqs == 0) return QVP_OK;
-
-    qvp::DecodeGeometry g{};
+    DecodeGeometry& g = *out;
+    g = DecodeGeometry{};
     g.kv_base = static_cast<const uint8_t*>(a->kv_base);
     g.block_stride = a->block_stride;
     g.k_off = static_cast<uint64_t>(a->layer) * a->layer_stride * esz;
@@ -135,13 +122,37 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
     g.num_kv_heads = a->num_kv_heads;
     g.group = a->num_query_heads / a->num_kv_heads;
     g.head_dim = a->head_dim;
-    g.scale_log2 = a->scale * qvp::kLog2e;
+    g.scale_log2 = a->scale * kLog2e;
+    *supported_mfma = mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
+                                     reinterpret_cast<uintptr_t>(a->kv_base));
+    return QVP_OK;
+}
+
+}  // namespace qvp
+
+extern "C" {
+
+int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads, uint32_t head_dim, uint64_t* bytes) {
+    if (bytes == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "bytes is NULL");
+    qvp_packed_view v{};
+    QVP_TRY(qvp_batch_view(batch, &v));
+    *bytes = std::max(qvp::generic_workspace_bytes(v, num_query_heads, head_dim),
+                      mfma_bound_bytes(v, num_query_heads, head_dim));
+    return QVP_OK;
+}
+
+int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
+    if (a == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "args is NULL");
+    qvp_packed_view v{};
+    QVP_TRY(qvp_batch_view(a->batch, &v));
+    qvp::DecodeGeometry g{};
+    bool mfma = false;
+    QVP_TRY(qvp::decode_geometry(a, v, &g, &mfma));
+    if (v.num_seqs == 0) return QVP_OK;
 
     hipStream_t s = qvp::as_stream(stream);
     hipEvent_t ev = reinterpret_cast<hipEvent_t>(a->split_event);
     qvp_batch* batch = const_cast<qvp_batch*>(a->batch);
-    const bool mfma = qvp::mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
-                                          reinterpret_cast<uintptr_t>(a->kv_base));
     uint64_t need = 0;
     if (mfma) {
         QVP_TRY(qvp::mfma_prepare_schedule(batch, g, s));
@@ -183,8 +194,12 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
         plan.kv_heads_per_segment = 1;
         plan.split_tokens = v.split_tokens;
     }
-    if (status == QVP_OK) batch->last_plan = plan;
-    return status;
+    if (status != QVP_OK) return status;
+    batch->last_plan = plan;
+    // Later packs and schedule rebuilds on other streams wait for this read.
+    QVP_TRY(qvp::note_reader(batch->readers[batch->current], s, batch->upload_stream[batch->current]));
+    if (mfma && !batch->sched.in_pack_buffer) QVP_TRY(qvp::note_reader(batch->sched.reader, s, s));
+    return QVP_OK;
 }
 
 int qvp_decode_plan_info(const qvp_batch* batch, qvp_decode_plan* plan) {

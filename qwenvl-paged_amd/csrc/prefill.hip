@@ -476,7 +476,7 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
         if (plan.staging != nullptr) QVP_HIP(hipHostFree(plan.staging));
         plan.staging = nullptr;
         plan.staging_cap = 0;
-        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&plan.staging), ints * sizeof(int32_t), hipHostMallocDefault));
+        QVP_HIP(hipHostMalloc(reinterpret_cast<void**>(&plan.staging), ints * sizeof(int32_t), hipHostMallocCoherent));
         plan.staging_cap = ints;
     }
     if (plan.device_cap < ints) {
@@ -491,7 +491,7 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
         plan.device_cap = ints;
     }
     std::memcpy(plan.staging, items.data(), ints * sizeof(int32_t));
-    QVP_HIP(hipMemcpyAsync(plan.device, plan.staging, ints * sizeof(int32_t), hipMemcpyHostToDevice, s));
+    QVP_TRY(qvp::pull_from_pinned(plan.device, plan.staging, ints * sizeof(int32_t), s));
     QVP_HIP(hipEventRecord(plan.staging_done, s));
     plan.staging_pending = true;
 
@@ -511,5 +511,7 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
             break;
     }
     QVP_HIP(hipGetLastError());
-    return QVP_OK;
+    // The kernel reads the packed block tables: a later pack into this slot
+    // from another stream waits for it.
+    return qvp::note_reader(batch->readers[batch->current], s, batch->upload_stream[batch->current]);
 }

@@ -232,7 +232,59 @@ __global__ void fill_bytes_kernel(uint8_t* __restrict__ dst, uint32_t pattern, s
     }
 }
 
+// Staged-upload kernel: every thread issues its (up to) four 16-byte host
+// reads before any store, so a small upload costs about one bus round trip.
+constexpr int kPullThreads = 256;
+constexpr int kPullUnroll = 4;
+
+__global__ __launch_bounds__(kPullThreads) void pull_pinned_kernel(const uint4* __restrict__ src,
+                                                                   uint4* __restrict__ dst, size_t n16,
+                                                                   const uint32_t* __restrict__ src_tail,
+                                                                   uint32_t* __restrict__ dst_tail, uint32_t tail) {
+    const size_t step = static_cast<size_t>(gridDim.x) * kPullThreads;
+    for (size_t base = static_cast<size_t>(blockIdx.x) * kPullThreads + threadIdx.x; base < n16;
+         base += step * kPullUnroll) {
+        uint4 r[kPullUnroll];
+#pragma unroll
+        for (int u = 0; u < kPullUnroll; ++u) {
+            const size_t i = base + u * step;
+            if (i < n16) r[u] = src[i];
+        }
+#pragma unroll
+        for (int u = 0; u < kPullUnroll; ++u) {
+            const size_t i = base + u * step;
+            if (i < n16) dst[i] = r[u];
+        }
+    }
+    if (blockIdx.x == 0 && threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
+}
+
 }  // namespace
+
+namespace qvp {
+
+int pull_from_pinned(void* dst, const void* pinned_host, size_t bytes, hipStream_t stream) {
+    if (bytes == 0) return QVP_OK;
+    if (bytes % 4 != 0 || (reinterpret_cast<uintptr_t>(dst) & 15u) != 0 ||
+        (reinterpret_cast<uintptr_t>(pinned_host) & 15u) != 0) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "staged upload of %zu bytes is not word-sized or 16-byte aligned",
+                    bytes);
+    }
+    void* src = nullptr;
+    QVP_HIP(hipHostGetDevicePointer(&src, const_cast<void*>(pinned_host), 0));
+    const size_t n16 = bytes / 16;
+    const uint32_t tail = static_cast<uint32_t>((bytes % 16) / 4);
+    size_t blocks = (n16 + kPullThreads * kPullUnroll - 1) / (kPullThreads * kPullUnroll);
+    blocks = blocks == 0 ? 1 : (blocks > 256 ? 256 : blocks);
+    hipLaunchKernelGGL(pull_pinned_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kPullThreads), 0, stream,
+                       static_cast<const uint4*>(src), static_cast<uint4*>(dst), n16,
+                       reinterpret_cast<const uint32_t*>(static_cast<const uint8_t*>(src) + n16 * 16),
+                       reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(dst) + n16 * 16), tail);
+    QVP_HIP(hipGetLastError());
+    return QVP_OK;
+}
+
+}  // namespace qvp
 
 extern "C" int qvp_fill_bytes(void* dst, uint8_t value, size_t bytes, void* stream) {
     if (bytes == 0) return QVP_OK;

@@ -20,6 +20,7 @@
 #include <vector>
 
 struct qvp_batch;
+struct qvp_decode_args;
 
 namespace qwenvl_paged {
 
@@ -90,13 +91,19 @@ public:
 
 private:
     bool fail(std::string msg);
-    // Checks shared by decode and prefill, then packs the batch on the
-    // allocator's stream; fills the pool geometry of the launch.
+    // Checks shared by decode and prefill and the batch's block ids in CSR
+    // form (flushing queued copies first); fills the launch's element type
+    // and the allocator's stream.
     bool pack(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
               std::uint32_t layer, std::uint32_t num_query_heads, const void* device_query, void* device_out,
               int& cache_type, void*& stream);
+    // Packs the collected batch on `stream`, with the schedule of `decode`
+    // when given (qvp_pack_for_decode).
+    bool upload(const std::vector<std::uint32_t>& context_lens, std::uint32_t tokens_per_block,
+                const qvp_decode_args* decode, void* stream);
 
     qvp_batch* batch_{nullptr};
+    std::uint32_t num_pool_blocks_{0};
     std::vector<std::uint32_t> ids_;
     std::vector<std::uint32_t> cu_;
     std::string last_error_;

@@ -184,8 +184,17 @@ bool PagedAttentionBatch::pack(const std::vector<CacheView>& views, const std::v
     const PhysicalBlock* frame0 = allocator->block(0);
     const std::uint32_t num_blocks = static_cast<std::uint32_t>(allocator->stats().total_blocks);
     if (frame0 == nullptr) return fail("empty pool");
-    if (qvp_pack(batch_, static_cast<std::uint32_t>(views.size()), ids_.empty() ? nullptr : ids_.data(), cu_.data(),
-                 context_lens.data(), shape.tokens_per_block, num_blocks, split_tokens_, stream) != QVP_OK) {
+    num_pool_blocks_ = num_blocks;
+    return true;
+}
+
+bool PagedAttentionBatch::upload(const std::vector<std::uint32_t>& context_lens, std::uint32_t tokens_per_block,
+                                 const qvp_decode_args* decode, void* stream) {
+    // One upload per step: with the decode's arguments the pack also carries
+    // that decode's work schedule.
+    if (qvp_pack_for_decode(batch_, static_cast<std::uint32_t>(context_lens.size()),
+                            ids_.empty() ? nullptr : ids_.data(), cu_.data(), context_lens.data(), tokens_per_block,
+                            num_pool_blocks_, split_tokens_, decode, stream) != QVP_OK) {
         return fail(std::string("pack: ") + qvp_last_error());
     }
     return true;
@@ -219,6 +228,7 @@ bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std:
     args.stream_stride = layout.stream_stride();
     args.layer_stride = layout.layer_stride();
     args.scale = scale;
+    if (!upload(context_lens, shape.tokens_per_block, &args, stream)) return false;
     if (qvp_paged_decode(&args, stream) != QVP_OK) return fail(std::string("decode: ") + qvp_last_error());
     return true;
 }
@@ -257,6 +267,7 @@ bool PagedAttentionBatch::prefill(const std::vector<CacheView>& views, const std
     args.stream_stride = layout.stream_stride();
     args.layer_stride = layout.layer_stride();
     args.scale = scale;
+    if (!upload(context_lens, shape.tokens_per_block, nullptr, stream)) return false;
     if (qvp_paged_prefill(&args, stream) != QVP_OK) return fail(std::string("prefill: ") + qvp_last_error());
     return true;
 }

@@ -187,6 +187,8 @@ SIGNATURES = {
     "qvp_decode_workspace_bytes": (c_int, [c_void_p, c_uint32, c_uint32, _u64p]),
     "qvp_paged_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "qvp_decode_plan_info": (c_int, [c_void_p, POINTER(DecodePlan)]),
+    "qvp_pack_for_decode": (c_int, [c_void_p, c_uint32, _u32p, _u32p, _u32p, c_uint32, c_uint32, c_uint32,
+                                    c_void_p, c_void_p]),
     "qvp_copy_blocks": (c_int, [c_void_p, c_uint64, c_uint32, _u32p, _u32p, c_uint32, c_uint64, c_void_p]),
     "qvp_swap_gather": (
         c_int,
@@ -469,13 +471,18 @@ class Batch:
         self.handle = p.value
 
     def pack(self, ids, cu_blocks, context_lens, tokens_per_block: int, num_pool_blocks: int,
-             split_tokens: int = 0, stream=None) -> PackedView:
+             split_tokens: int = 0, stream=None, decode: "DecodeArgs | None" = None) -> PackedView:
+        """qvp_pack, or qvp_pack_for_decode when the decode the pack is for is given."""
         ids_a, ids_p = _u32(ids if len(ids) else np.zeros(1, np.uint32))
         cu_a, cu_p = _u32(cu_blocks)
         ctx_a, ctx_p = _u32(context_lens)
         num_seqs = len(ctx_a)
-        check(load().qvp_pack(self.handle, num_seqs, ids_p, cu_p, ctx_p, tokens_per_block, num_pool_blocks,
-                              split_tokens, _sp(stream)))
+        if decode is None:
+            check(load().qvp_pack(self.handle, num_seqs, ids_p, cu_p, ctx_p, tokens_per_block, num_pool_blocks,
+                                  split_tokens, _sp(stream)))
+        else:
+            check(load().qvp_pack_for_decode(self.handle, num_seqs, ids_p, cu_p, ctx_p, tokens_per_block,
+                                             num_pool_blocks, split_tokens, byref(decode), _sp(stream)))
         # The library copies from pinned staging, so the numpy inputs may go now.
         return self.view()
 
