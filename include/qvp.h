@@ -286,6 +286,24 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
                         uint32_t num_pool_blocks, uint32_t split_tokens, const qvp_decode_args* decode,
                         void* stream);
 
+/* qvp_paged_decode for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). No
+ * counterpart in the reference. It calls no hipMalloc, hipHostMalloc,
+ * hipFree or other allocating routine: the workspace is a fixed device array
+ * of 16 MiB that the library reserves in every device's memory when it loads
+ * (held until the process ends), so args->workspace must be NULL, and a
+ * decode needing more workspace (e.g. a bf16 config2 batch needs 1.7 MB) is
+ * refused with QVP_ERR_CAPACITY. When the bf16 MFMA kernel runs the decode,
+ * the batch must already hold its work schedule (packed with
+ * qvp_pack_for_decode for this decode, or decoded once by qvp_paged_decode
+ * since its last pack), or buffers large enough to rebuild it; otherwise the
+ * call is refused with QVP_ERR_CAPACITY before anything is enqueued. Every
+ * call on a device shares that device's array: calls that overlap on one
+ * device (e.g. on two streams) race and must be ordered by the caller. The
+ * array needs no initial contents (every word the kernels read was written
+ * earlier in the same launch). */
+int qvp_paged_decode_noalloc(const qvp_decode_args* args, void* stream);
+
 /* The work decomposition of the last qvp_paged_decode enqueued on a batch.
  * No reference counterpart (the reference decodes one sequence at a time,
  * PagedAttention.h:53-127): it tells benchmarks and tests which kernel ran

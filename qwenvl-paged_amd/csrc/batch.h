@@ -119,8 +119,9 @@ namespace qvp {
 // reader was enqueued on another stream.
 int wait_for_reader(qvp_reader& r, hipStream_t stream);
 // Records `stream` as a buffer's last reader (call after its kernels);
-// `writer` is the stream that wrote the buffer.
-int note_reader(qvp_reader& r, hipStream_t stream, hipStream_t writer);
+// `writer` is the stream that wrote the buffer. Without may_allocate no event
+// object is created.
+int note_reader(qvp_reader& r, hipStream_t stream, hipStream_t writer, bool may_allocate = true);
 void destroy_reader(qvp_reader& r);
 // Frees the schedule's buffers (called by qvp_batch_destroy).
 void destroy_schedule(qvp_schedule& s);

@@ -90,8 +90,10 @@ bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g);
 int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry& g);
 // Writes the planned schedule's s.total words to h (pinned staging).
 void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t* h);
-// Builds and uploads the schedule on `stream` unless it is current.
-int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream);
+// Builds and uploads the schedule on `stream` unless it is current. Without
+// may_allocate a rebuild that needs new staging or device buffers (or event
+// objects) is refused with QVP_ERR_CAPACITY before anything changes.
+int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream, bool may_allocate = true);
 uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim);
 int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t out_dtype, void* out,
                        void* workspace, hipEvent_t split_event, hipStream_t stream);

@@ -876,7 +876,7 @@ void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t
     }
 }
 
-int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream) {
+int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream, bool may_allocate) {
     if (mfma_schedule_current(batch, g)) return QVP_OK;
     qvp_schedule& s = batch->sched;
     ScheduleInput in{};
@@ -886,6 +886,18 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     in.cu_blocks = batch->host_cu_blocks.data();
     in.tpb = batch->view.tokens_per_block;
     in.generation = batch->generation;
+    if (!may_allocate) {
+        // Plan into a copy, so that a refusal leaves the schedule as it was.
+        qvp_schedule probe{};
+        QVP_TRY(mfma_plan_schedule(probe, in, g));
+        const int next = s.staging_slot;
+        if (s.staging_done[next] == nullptr || s.staging_cap[next] < probe.total || s.device_cap < probe.total) {
+            return fail(QVP_ERR_CAPACITY,
+                        "the decode's work schedule needs %zu words of buffers this batch does not have yet: pack it "
+                        "with qvp_pack_for_decode for this decode, or decode it once with qvp_paged_decode",
+                        probe.total);
+        }
+    }
     QVP_TRY(mfma_plan_schedule(s, in, g));
 
     const int slot = s.staging_slot;

@@ -347,7 +347,7 @@ int wait_for_reader(qvp_reader& r, hipStream_t stream) {
     return QVP_OK;
 }
 
-int note_reader(qvp_reader& r, hipStream_t stream, hipStream_t writer) {
+int note_reader(qvp_reader& r, hipStream_t stream, hipStream_t writer, bool may_allocate) {
     // Work captured into a graph reads the buffers whenever the graph is
     // replayed, which no event can stand for; graphs are valid until the
     // pack after next (see qvp_graph_begin_capture).
@@ -363,7 +363,9 @@ int note_reader(qvp_reader& r, hipStream_t stream, hipStream_t writer) {
     // reader's stream. Reads on the writer's own stream (the one-stream
     // engine loop) record nothing: an event between back-to-back kernels
     // stalls the second one.
-    if (stream != writer) {
+    // (Without an event object and leave to create one, the writer records
+    // one on this stream when it comes.)
+    if (stream != writer && (r.event != nullptr || may_allocate)) {
         if (r.event == nullptr) QVP_HIP(hipEventCreateWithFlags(&r.event, hipEventDisableTiming));
         QVP_HIP(hipEventRecord(r.event, stream));
         r.recorded = true;

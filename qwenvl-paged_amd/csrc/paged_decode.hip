@@ -50,6 +50,36 @@ int library_workspace(uint64_t need, void** out) {
     return QVP_OK;
 }
 
+// Workspace of qvp_paged_decode_noalloc: a fixed array in each device's
+// memory, reserved when the code object loads and held until the process
+// ends, so the call itself allocates nothing. In host code `scratch` names a
+// host-side stand-in; its device address comes from hipGetSymbolAddress,
+// taken once per device (with that device current) and kept below.
+constexpr uint64_t kScratchBytes = 16ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int scratch_address(void** out) {
+    int dev = 0;
+    QVP_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxScratchDevices) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "device %d beyond the %d devices the scratch table covers", dev,
+                    kMaxScratchDevices);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        QVP_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (ptr == nullptr) return fail(QVP_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return QVP_OK;
+}
+
 uint32_t log2_u32(uint32_t x) {
     uint32_t r = 0;
     while ((1u << r) < x) ++r;
@@ -141,7 +171,15 @@ int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads,
     return QVP_OK;
 }
 
-int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Shared body of qvp_paged_decode and qvp_paged_decode_noalloc. With
+// no_alloc, the device scratch array is the workspace and nothing is
+// allocated: a schedule that would need new buffers, or a workspace beyond
+// the scratch array, is refused with QVP_ERR_CAPACITY.
+int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
     if (a == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "args is NULL");
     qvp_packed_view v{};
     QVP_TRY(qvp_batch_view(a->batch, &v));
@@ -154,14 +192,25 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
     hipEvent_t ev = reinterpret_cast<hipEvent_t>(a->split_event);
     qvp_batch* batch = const_cast<qvp_batch*>(a->batch);
     uint64_t need = 0;
+    void* ws = a->workspace;
+    if (no_alloc) {
+        if (ws != nullptr) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "the allocation-free decode uses its own scratch; workspace must be NULL");
+        }
+        QVP_TRY(scratch_address(&ws));
+    }
     if (mfma) {
-        QVP_TRY(qvp::mfma_prepare_schedule(batch, g, s));
+        QVP_TRY(qvp::mfma_prepare_schedule(batch, g, s, !no_alloc));
         need = qvp::mfma_workspace_bytes(batch, g.group, g.head_dim);
     } else {
         need = qvp::generic_workspace_bytes(v, a->num_query_heads, a->head_dim);
     }
-    void* ws = a->workspace;
-    if (ws == nullptr) {
+    if (no_alloc) {
+        if (need > kScratchBytes) {
+            return fail(QVP_ERR_CAPACITY, "decode needs %llu bytes of workspace, the scratch array holds %llu",
+                        static_cast<unsigned long long>(need), static_cast<unsigned long long>(kScratchBytes));
+        }
+    } else if (ws == nullptr) {
         QVP_TRY(library_workspace(need, &ws));
     } else if (a->workspace_bytes < need) {
         return fail(QVP_ERR_CAPACITY, "workspace of %llu bytes, need %llu",
@@ -197,10 +246,18 @@ int qvp_paged_decode(const qvp_decode_args* a, void* stream) {
     if (status != QVP_OK) return status;
     batch->last_plan = plan;
     // Later packs and schedule rebuilds on other streams wait for this read.
-    QVP_TRY(qvp::note_reader(batch->readers[batch->current], s, batch->upload_stream[batch->current]));
-    if (mfma && !batch->sched.in_pack_buffer) QVP_TRY(qvp::note_reader(batch->sched.reader, s, s));
+    QVP_TRY(qvp::note_reader(batch->readers[batch->current], s, batch->upload_stream[batch->current], !no_alloc));
+    if (mfma && !batch->sched.in_pack_buffer) QVP_TRY(qvp::note_reader(batch->sched.reader, s, s, !no_alloc));
     return QVP_OK;
 }
+
+}  // namespace
+
+extern "C" {
+
+int qvp_paged_decode(const qvp_decode_args* a, void* stream) { return decode_impl(a, stream, false); }
+
+int qvp_paged_decode_noalloc(const qvp_decode_args* a, void* stream) { return decode_impl(a, stream, true); }
 
 int qvp_decode_plan_info(const qvp_batch* batch, qvp_decode_plan* plan) {
     if (batch == nullptr || plan == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "NULL argument");

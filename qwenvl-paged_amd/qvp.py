@@ -187,6 +187,7 @@ SIGNATURES = {
     "qvp_decode_workspace_bytes": (c_int, [c_void_p, c_uint32, c_uint32, _u64p]),
     "qvp_paged_decode": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "qvp_decode_plan_info": (c_int, [c_void_p, POINTER(DecodePlan)]),
+    "qvp_paged_decode_noalloc": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "qvp_pack_for_decode": (c_int, [c_void_p, c_uint32, _u32p, _u32p, _u32p, c_uint32, c_uint32, c_uint32,
                                     c_void_p, c_void_p]),
     "qvp_copy_blocks": (c_int, [c_void_p, c_uint64, c_uint32, _u32p, _u32p, c_uint32, c_uint64, c_void_p]),
@@ -631,6 +632,12 @@ def decode_args(*, query: int, out: int, kv_base: int, block_stride: int, batch:
 
 def paged_decode(args: DecodeArgs, stream=None) -> None:
     check(load().qvp_paged_decode(byref(args), _sp(stream)))
+
+
+def paged_decode_noalloc(args: DecodeArgs, stream=None) -> None:
+    """qvp_paged_decode_noalloc: the decode on the library's fixed device
+    scratch array, allocating nothing (args.workspace must be 0)."""
+    check(load().qvp_paged_decode_noalloc(byref(args), _sp(stream)))
 
 
 def copy_blocks(kv_base: int, block_stride: int, num_blocks: int, src, dst, copy_bytes: int, stream=None) -> None:
