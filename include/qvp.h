@@ -115,6 +115,9 @@ int qvp_event_create(void** event);
 int qvp_event_destroy(void* event);
 int qvp_event_record(void* event, void* stream);
 int qvp_event_synchronize(void* event);
+/* *complete = 1 when all work before the event's last record has finished
+ * (or it was never recorded), 0 while it is pending. */
+int qvp_event_query(void* event, int* complete);
 int qvp_stream_wait_event(void* stream, void* event);
 int qvp_event_elapsed_ms(float* ms, void* start, void* stop);
 

@@ -204,17 +204,9 @@ std::int64_t ref_element_offset(std::uint32_t tpb, std::uint32_t layers, std::ui
     return off.has_value() ? static_cast<std::int64_t>(*off) : -1;
 }
 
-// Runs the continuous-batching trace of trace_driver.h on the reference's own
-// Scheduler / KVCacheManager / MemoryAllocator / HostSwapBackend and copies the
-// event log into `out` (NUL-terminated, truncated to `cap`). Returns the full
-// log length.
-std::uint64_t ref_scheduler_trace(std::uint32_t requests, std::uint64_t seed, std::uint32_t pool_percent,
-                                  std::uint32_t watermark_blocks, char* out, std::uint64_t cap) {
-    trace::Config c;
-    c.requests = requests;
-    c.seed = seed;
-    c.pool_percent = pool_percent;
-    c.watermark_blocks = watermark_blocks;
+namespace {
+
+std::uint64_t run_reference_trace(const trace::Config& c, char* out, std::uint64_t cap) {
     AllocatorConfig config;
     config.block_shape.tokens_per_block = c.tokens_per_block;
     config.block_shape.num_layers = 1;
@@ -233,6 +225,45 @@ std::uint64_t ref_scheduler_trace(std::uint32_t requests, std::uint64_t seed, st
         out[n] = '\0';
     }
     return log.size();
+}
+
+}  // namespace
+
+// The trace with every parameter given: cfg = {requests, prompt_lo,
+// prompt_hi, output_lo, output_hi, arrivals_per_step, tokens_per_block,
+// pool_percent, watermark_blocks, max_active, max_batch_tokens, max_steps,
+// cancel_after_decodes}.
+std::uint64_t ref_scheduler_trace_config(const std::uint32_t* cfg, std::uint64_t seed, char* out, std::uint64_t cap) {
+    trace::Config c;
+    c.requests = cfg[0];
+    c.prompt_lo = cfg[1];
+    c.prompt_hi = cfg[2];
+    c.output_lo = cfg[3];
+    c.output_hi = cfg[4];
+    c.arrivals_per_step = cfg[5];
+    c.tokens_per_block = cfg[6];
+    c.pool_percent = cfg[7];
+    c.watermark_blocks = cfg[8];
+    c.max_active = cfg[9];
+    c.max_batch_tokens = cfg[10];
+    c.max_steps = cfg[11];
+    c.cancel_after_decodes = cfg[12] != 0;
+    c.seed = seed;
+    return run_reference_trace(c, out, cap);
+}
+
+// Runs the continuous-batching trace of trace_driver.h on the reference's own
+// Scheduler / KVCacheManager / MemoryAllocator / HostSwapBackend and copies the
+// event log into `out` (NUL-terminated, truncated to `cap`). Returns the full
+// log length.
+std::uint64_t ref_scheduler_trace(std::uint32_t requests, std::uint64_t seed, std::uint32_t pool_percent,
+                                  std::uint32_t watermark_blocks, char* out, std::uint64_t cap) {
+    trace::Config c;
+    c.requests = requests;
+    c.seed = seed;
+    c.pool_percent = pool_percent;
+    c.watermark_blocks = watermark_blocks;
+    return run_reference_trace(c, out, cap);
 }
 
 }  // extern "C"

@@ -36,6 +36,10 @@ struct Config {
     std::uint32_t max_batch_tokens{1024};
     std::uint32_t max_steps{2000};
     std::uint64_t seed{5};
+    // Requests that reach their output length are cancelled after every
+    // decoding request of the step was handled (an engine cancels after the
+    // step's decode ran over all of them), instead of inside the loop.
+    bool cancel_after_decodes{false};
 };
 
 struct RequestPlan {
@@ -93,6 +97,7 @@ std::string run(const Config& c, MemoryAllocator& allocator) {
     std::map<std::uint64_t, std::uint32_t> length;   // tokens held by a live sequence
     std::map<std::uint64_t, std::uint32_t> decoded;  // output tokens produced
     std::vector<std::uint64_t> parked;               // preemption order
+    std::vector<std::uint64_t> done;                 // finished this step (cancel_after_decodes)
     std::uint32_t arrived = 0, finished = 0;
     std::string log;
     char line[512];
@@ -154,6 +159,10 @@ std::string run(const Config& c, MemoryAllocator& allocator) {
             (void)cache.ensure_token_writable(id, pos);
             length[id] = pos + 1;
             if (++decoded[id] >= plans[id - 1].output) {
+                if (c.cancel_after_decodes) {
+                    done.push_back(id);
+                    continue;
+                }
                 sched.cancel(id);
                 length.erase(id);
                 decoded.erase(id);
@@ -161,6 +170,14 @@ std::string run(const Config& c, MemoryAllocator& allocator) {
                 events += " done=" + std::to_string(id);
             }
         }
+        for (std::uint64_t id : done) {
+            sched.cancel(id);
+            length.erase(id);
+            decoded.erase(id);
+            ++finished;
+            events += " done=" + std::to_string(id);
+        }
+        done.clear();
         Hash h;
         for (const auto& kv : length) {
             const auto view = cache.cache_view(kv.first);
@@ -176,9 +193,9 @@ std::string run(const Config& c, MemoryAllocator& allocator) {
         std::string pre, dec;
         for (std::uint64_t id : plan.prefill_requests) pre += std::to_string(id) + ",";
         for (std::uint64_t id : plan.decode_requests) dec += std::to_string(id) + ",";
-        std::snprintf(line, sizeof line, "%u P=%s D=%s tok=%u free=%u shared=%u swapped=%u h=%08x", step, pre.c_str(),
-                      dec.c_str(), plan.scheduled_tokens, st.free_blocks, st.shared_blocks, st.swapped_blocks, h.h);
-        log += line;
+        std::snprintf(line, sizeof line, " tok=%u free=%u shared=%u swapped=%u h=%08x", plan.scheduled_tokens,
+                      st.free_blocks, st.shared_blocks, st.swapped_blocks, h.h);
+        log += std::to_string(step) + " P=" + pre + " D=" + dec + line;
         log += events;
         log += "\n";
     }

@@ -7,11 +7,16 @@
 // between HBM and a pinned host arena, the GPU itself driving the host link.
 //
 // All three share one kernel: a list of (source, destination) segments of equal
-// length travels in the kernel arguments (no staging buffer, no extra copy), and
-// each workgroup moves a 16 KiB chunk of one segment with 16-byte accesses.
+// length travels in the kernel arguments (no staging buffer, no extra copy).
+// The segments are cut into 8 KiB chunks numbered across the whole list, and
+// a grid of at most two workgroups per CU walks the chunks with a stride of
+// the grid: short-lived workgroups (one chunk each) left the copy bound by how
+// fast workgroups can be dispatched, about 5.5 TB/s of reads plus writes on
+// 128 whole 7B frames against 6.4 TB/s this way.
 #include "common.h"
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 namespace {
@@ -20,40 +25,63 @@ using qvp::fail;
 
 constexpr int kSegmentsPerLaunch = 128;
 constexpr int kCopyThreads = 256;
-constexpr int kCopyUnroll = 4;
+constexpr int kCopyUnroll = 2;
 constexpr uint64_t kChunkBytes = static_cast<uint64_t>(kCopyThreads) * 16 * kCopyUnroll;
+constexpr uint32_t kWgsPerCu = 2;
 
 struct SegmentList {
     const uint8_t* src[kSegmentsPerLaunch];
     uint8_t* dst[kSegmentsPerLaunch];
 };
 
-__global__ __launch_bounds__(kCopyThreads) void copy_segments(SegmentList list, uint64_t bytes) {
-    const uint8_t* __restrict__ src = list.src[blockIdx.y];
-    uint8_t* __restrict__ dst = list.dst[blockIdx.y];
-    if (src == dst) return;
-    const uint64_t chunk0 = static_cast<uint64_t>(blockIdx.x) * kChunkBytes;
-    const uint64_t chunk_end = min(chunk0 + kChunkBytes, bytes);
-    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0;
-    if (vec && chunk_end - chunk0 == kChunkBytes) {
-        const uint4* s4 = reinterpret_cast<const uint4*>(src + chunk0);
-        uint4* d4 = reinterpret_cast<uint4*>(dst + chunk0);
-        uint4 r[kCopyUnroll];
-#pragma unroll
-        for (int u = 0; u < kCopyUnroll; ++u) r[u] = s4[threadIdx.x + u * kCopyThreads];
-#pragma unroll
-        for (int u = 0; u < kCopyUnroll; ++u) d4[threadIdx.x + u * kCopyThreads] = r[u];
-        return;
-    }
-    if (vec) {
-        const uint64_t vec_end = chunk0 + (chunk_end - chunk0) / 16 * 16;
-        for (uint64_t off = chunk0 + 16u * threadIdx.x; off < vec_end; off += 16u * kCopyThreads) {
-            *reinterpret_cast<uint4*>(dst + off) = *reinterpret_cast<const uint4*>(src + off);
+__global__ __launch_bounds__(kCopyThreads) void copy_segments(SegmentList list, uint64_t bytes,
+                                                              uint32_t chunks_per_segment, uint32_t total_chunks) {
+    static_assert(kCopyUnroll == 2, "the full-chunk path moves two 16-byte words per thread");
+    for (uint32_t c = blockIdx.x; c < total_chunks; c += gridDim.x) {
+        const uint32_t seg = c / chunks_per_segment;
+        const uint8_t* __restrict__ src = list.src[seg];
+        uint8_t* __restrict__ dst = list.dst[seg];
+        if (src == dst) continue;
+        const uint64_t chunk0 = static_cast<uint64_t>(c - seg * chunks_per_segment) * kChunkBytes;
+        const uint64_t chunk_end = min(chunk0 + kChunkBytes, bytes);
+        const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0;
+        if (vec && chunk_end - chunk0 == kChunkBytes) {
+            // Both loads issue before either store (two words in flight per
+            // thread); plain registers, so nothing is staged through LDS.
+            const uint4* s4 = reinterpret_cast<const uint4*>(src + chunk0);
+            uint4* d4 = reinterpret_cast<uint4*>(dst + chunk0);
+            const uint4 r0 = s4[threadIdx.x];
+            const uint4 r1 = s4[threadIdx.x + kCopyThreads];
+            d4[threadIdx.x] = r0;
+            d4[threadIdx.x + kCopyThreads] = r1;
+        } else if (vec) {
+            const uint64_t vec_end = chunk0 + (chunk_end - chunk0) / 16 * 16;
+            for (uint64_t off = chunk0 + 16u * threadIdx.x; off < vec_end; off += 16u * kCopyThreads) {
+                *reinterpret_cast<uint4*>(dst + off) = *reinterpret_cast<const uint4*>(src + off);
+            }
+            for (uint64_t off = vec_end + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
+        } else {
+            for (uint64_t off = chunk0 + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
         }
-        for (uint64_t off = vec_end + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
-        return;
     }
-    for (uint64_t off = chunk0 + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
+}
+
+// Compute units of the current device, cached per device ordinal.
+std::mutex g_cu_mutex;
+std::vector<uint32_t> g_cus;
+
+int device_cus(uint32_t* cus) {
+    int dev = 0;
+    QVP_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_cu_mutex);
+    if (g_cus.size() <= static_cast<size_t>(dev)) g_cus.resize(dev + 1, 0);
+    if (g_cus[dev] == 0) {
+        int n = 0;
+        QVP_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+        g_cus[dev] = static_cast<uint32_t>(std::max(n, 1));
+    }
+    *cus = g_cus[dev];
+    return QVP_OK;
 }
 
 // Enqueues segments [0, n) in launches of kSegmentsPerLaunch.
@@ -61,8 +89,10 @@ int launch_segments(const std::vector<const uint8_t*>& src, const std::vector<ui
                     uint64_t bytes, hipStream_t stream) {
     const size_t n = src.size();
     if (n == 0 || bytes == 0) return QVP_OK;
+    uint32_t cus = 0;
+    QVP_TRY(device_cus(&cus));
     const uint64_t chunks = (bytes + kChunkBytes - 1) / kChunkBytes;
-    if (chunks > 0x7fffffffu) return fail(QVP_ERR_INVALID_ARGUMENT, "segment too large");
+    if (chunks * kSegmentsPerLaunch > 0xffffffffull) return fail(QVP_ERR_INVALID_ARGUMENT, "segment too large");
     for (size_t first = 0; first < n; first += kSegmentsPerLaunch) {
         const size_t count = std::min<size_t>(kSegmentsPerLaunch, n - first);
         SegmentList list{};
@@ -70,8 +100,10 @@ int launch_segments(const std::vector<const uint8_t*>& src, const std::vector<ui
             list.src[i] = src[first + i];
             list.dst[i] = dst[first + i];
         }
-        hipLaunchKernelGGL(copy_segments, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(count)),
-                           dim3(kCopyThreads), 0, stream, list, bytes);
+        const uint64_t total = chunks * count;
+        const uint64_t grid = std::min<uint64_t>(total, static_cast<uint64_t>(cus) * kWgsPerCu);
+        hipLaunchKernelGGL(copy_segments, dim3(static_cast<unsigned>(grid)), dim3(kCopyThreads), 0, stream, list,
+                           bytes, static_cast<uint32_t>(chunks), static_cast<uint32_t>(total));
         QVP_HIP(hipGetLastError());
     }
     return QVP_OK;

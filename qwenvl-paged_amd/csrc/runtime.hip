@@ -166,6 +166,18 @@ int qvp_event_synchronize(void* event) {
     return QVP_OK;
 }
 
+int qvp_event_query(void* event, int* complete) {
+    if (complete == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "complete is NULL");
+    const hipError_t err = hipEventQuery(reinterpret_cast<hipEvent_t>(event));
+    if (err == hipErrorNotReady) {
+        *complete = 0;
+        return QVP_OK;
+    }
+    if (err != hipSuccess) return qvp::hip_fail(err, "hipEventQuery");
+    *complete = 1;
+    return QVP_OK;
+}
+
 int qvp_stream_wait_event(void* stream, void* event) {
     QVP_HIP(hipStreamWaitEvent(qvp::as_stream(stream), reinterpret_cast<hipEvent_t>(event), 0));
     return QVP_OK;
@@ -241,20 +253,21 @@ __global__ __launch_bounds__(kPullThreads) void pull_pinned_kernel(const uint4* 
                                                                    uint4* __restrict__ dst, size_t n16,
                                                                    const uint32_t* __restrict__ src_tail,
                                                                    uint32_t* __restrict__ dst_tail, uint32_t tail) {
+    static_assert(kPullUnroll == 4, "four words in flight per thread");
     const size_t step = static_cast<size_t>(gridDim.x) * kPullThreads;
-    for (size_t base = static_cast<size_t>(blockIdx.x) * kPullThreads + threadIdx.x; base < n16;
-         base += step * kPullUnroll) {
-        uint4 r[kPullUnroll];
-#pragma unroll
-        for (int u = 0; u < kPullUnroll; ++u) {
-            const size_t i = base + u * step;
-            if (i < n16) r[u] = src[i];
-        }
-#pragma unroll
-        for (int u = 0; u < kPullUnroll; ++u) {
-            const size_t i = base + u * step;
-            if (i < n16) dst[i] = r[u];
-        }
+    for (size_t i0 = static_cast<size_t>(blockIdx.x) * kPullThreads + threadIdx.x; i0 < n16;
+         i0 += step * kPullUnroll) {
+        // Separate registers, not an array: an indexed private array would be
+        // placed in LDS by the compiler.
+        const size_t i1 = i0 + step, i2 = i0 + 2 * step, i3 = i0 + 3 * step;
+        uint4 r0 = src[i0], r1{}, r2{}, r3{};
+        if (i1 < n16) r1 = src[i1];
+        if (i2 < n16) r2 = src[i2];
+        if (i3 < n16) r3 = src[i3];
+        dst[i0] = r0;
+        if (i1 < n16) dst[i1] = r1;
+        if (i2 < n16) dst[i2] = r2;
+        if (i3 < n16) dst[i3] = r3;
     }
     if (blockIdx.x == 0 && threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
 }

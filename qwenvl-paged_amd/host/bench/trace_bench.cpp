@@ -26,7 +26,17 @@
 // and the swap traffic's rate (plus, with --engine, prefill tokens and the
 // time of each phase).
 //
-// Usage: trace_bench [--requests N] [--seed S] [--pool-percent P] [--watermark B] [--engine 0|1]
+// With --log PATH the step-by-step decisions are written to PATH as an event
+// log: per step the admitted (P=) and decoding (D=) requests, the scheduled
+// tokens, the pool's free / shared / swapped counts, an FNV-1a hash over every
+// live sequence's page table (frame, swap slot and writable flag of each
+// entry) and the step's resume / preemption / completion events. Its format
+// is the one tests/golden/scheduler_trace_config5.txt.gz holds, written by
+// the reference's own Scheduler, KVCacheManager and MemoryAllocator for the
+// same requests, so equal logs mean equal decisions and equal frame and slot
+// ids.
+//
+// Usage: trace_bench [--requests N] [--seed S] [--pool-percent P] [--watermark B] [--engine 0|1] [--log PATH]
 #include "qvp.h"
 #include "qwenvl_paged/KVAppend.h"
 #include "qwenvl_paged/KVCacheManager.h"
@@ -67,14 +77,27 @@ void check(bool ok, const std::string& what) {
     if (!ok) die(what);
 }
 
+// FNV-1a over the four bytes of each 32-bit word.
+struct Fnv {
+    std::uint32_t h{2166136261u};
+    void add(std::uint32_t w) {
+        for (int i = 0; i < 4; ++i) h = (h ^ ((w >> (8 * i)) & 0xFFu)) * 16777619u;
+    }
+};
+
 }  // namespace
 
 int main(int argc, char** argv) {
     std::uint32_t requests = 200, pool_percent = 60, watermark = 64;
     std::uint64_t seed = 5;
     bool engine = false;
+    std::string log_path;
     for (int i = 1; i + 1 < argc; i += 2) {
         const std::string k = argv[i];
+        if (k == "--log") {
+            log_path = argv[i + 1];
+            continue;
+        }
         const std::uint64_t v = std::strtoull(argv[i + 1], nullptr, 10);
         if (k == "--requests") requests = static_cast<std::uint32_t>(v);
         else if (k == "--seed") seed = v;
@@ -186,8 +209,11 @@ int main(int argc, char** argv) {
     std::vector<std::uint32_t> lens;
     std::vector<std::uint64_t> ids;
     const auto t0 = std::chrono::steady_clock::now();
+    std::string log;
+    std::string events;
     while (finished < requests && steps < 200000) {
         ++steps;
+        events.clear();
         bool pending = false;
         for (std::uint32_t i = 0; i < requests && !pending; ++i) {
             const auto st = sched.state(i + 1);
@@ -200,6 +226,7 @@ int main(int argc, char** argv) {
                 parked.pop_front();
                 ++resumes;
                 swapped_in_blocks += blocks;
+                events += " resume=" + std::to_string(id);
             }
         }
         const BatchPlan plan = sched.schedule_next();
@@ -210,6 +237,7 @@ int main(int argc, char** argv) {
                 parked.push_back(i + 1);
                 ++preemptions;
                 swapped_out_blocks += sched.preemption_info(i + 1)->swapped_blocks;
+                events += " watermark_preempt=" + std::to_string(i + 1);
             }
         }
         app_seq.clear();
@@ -248,6 +276,7 @@ int main(int argc, char** argv) {
                 parked.push_back(id);
                 ++preemptions;
                 swapped_out_blocks += sched.preemption_info(id)->swapped_blocks;
+                events += " grow_preempt=" + std::to_string(id);
                 continue;
             }
             if (engine) {
@@ -330,10 +359,38 @@ int main(int argc, char** argv) {
                 length.erase(id);
                 produced.erase(id);
                 ++finished;
+                events += " done=" + std::to_string(id);
             }
+        }
+        if (!log_path.empty()) {
+            Fnv h;
+            for (std::uint32_t i = 1; i <= requests; ++i) {
+                const auto view = cache.cache_view(i);
+                if (!view) continue;
+                h.add(i);
+                for (const BlockTableEntry& e : view->block_table->entries()) {
+                    h.add(e.physical_id);
+                    h.add(e.swap_slot ? static_cast<std::uint32_t>(*e.swap_slot) : 0xFFFFFFFFu);
+                    h.add(e.writable ? 1u : 0u);
+                }
+            }
+            const AllocatorStats st = alloc.stats();
+            std::string pre, dec;
+            for (std::uint64_t id : plan.prefill_requests) pre += std::to_string(id) + ",";
+            for (std::uint64_t id : plan.decode_requests) dec += std::to_string(id) + ",";
+            char tail[160];
+            std::snprintf(tail, sizeof tail, " tok=%u free=%u shared=%u swapped=%u h=%08x", plan.scheduled_tokens,
+                          st.free_blocks, st.shared_blocks, st.swapped_blocks, h.h);
+            log += std::to_string(steps - 1) + " P=" + pre + " D=" + dec + tail + events + "\n";
         }
     }
     const double wall = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    if (!log_path.empty()) {
+        log += "finished=" + std::to_string(finished) + " of " + std::to_string(requests) + "\n";
+        std::FILE* f = std::fopen(log_path.c_str(), "w");
+        check(f != nullptr && std::fwrite(log.data(), 1, log.size(), f) == log.size() && std::fclose(f) == 0,
+              "writing " + log_path);
+    }
     check(alloc.synchronize(), "final sync");
     const AllocatorStats st = alloc.stats();
     const bool drained = st.free_blocks == st.total_blocks && swap.resident_slots() == 0;

@@ -117,7 +117,7 @@ def build() -> None:
             continue
         out = BUILD / "tests" / binary
         _run([CXX, "-o", str(out), str(test_src / "main.cpp"), f"-I{test_src}", *CXXFLAGS, *objs,
-              f"-L{PKG}", "-lqvp_host", "-lqvp", "-lpthread", *test_rpath])
+              f"-L{PKG}", "-lqvp_host", "-lqvp", "-lpthread", "-lz", *test_rpath])
 
 
 if __name__ == "__main__":

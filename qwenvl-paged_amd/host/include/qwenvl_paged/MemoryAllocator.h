@@ -24,6 +24,7 @@
 #include <array>
 #include <cstddef>
 #include <cstdint>
+#include <deque>
 #include <functional>
 #include <memory>
 #include <optional>
@@ -125,6 +126,15 @@ public:
     void enqueue_swap_gather(PhysicalBlockId frame, void* arena, std::size_t arena_bytes, std::size_t offset);
     void enqueue_swap_scatter(PhysicalBlockId frame, void* arena, std::size_t arena_bytes, std::size_t offset);
 
+    // Swap traffic runs on the side stream without holding up the engine
+    // stream; work the engine stream enqueues next must be ordered after the
+    // swaps it depends on. Call (after flush()) before enqueuing engine work
+    // that reads these frames (waits for scatters into them) or writes them
+    // (waits for gathers out of them and scatters into them). Only the batches
+    // still running are waited for, on the device.
+    bool order_frame_reads(const std::vector<PhysicalBlockId>& frames);
+    bool order_frame_writes(const std::vector<PhysicalBlockId>& frames);
+
 private:
     enum class OpKind : std::uint8_t { Copy, Gather, Scatter };
     struct DeviceOp {
@@ -136,9 +146,20 @@ private:
         std::size_t offset;
     };
 
+    // A swap batch on the side stream: its sequence number and the event
+    // recorded after it.
+    struct SwapBatchEvent {
+        std::uint64_t epoch;
+        void* event;
+    };
+
     bool fail(const std::string& what);
     bool run_batch(OpKind kind, const std::vector<DeviceOp>& ops);
-    void set_state(PhysicalBlockInfo& info, BlockState state) noexcept;
+    void set_ref_count(PhysicalBlockInfo& info, std::uint32_t count) noexcept;
+    // Makes the engine stream wait for the swap batches the frames depend on.
+    bool order_engine_after_swaps(const PhysicalBlockId* frames, std::size_t n, bool writes);
+    // Drops finished swap batches from the front of swap_events_.
+    bool retire_swap_batches();
 
     AllocatorConfig config_{};
     std::vector<std::unique_ptr<PhysicalBlock>> blocks_;
@@ -153,7 +174,16 @@ private:
     void* stream_{nullptr};
     void* side_stream_{nullptr};
     void* main_event_{nullptr};
-    void* side_event_{nullptr};
+    // Swap batches in launch order (the side stream runs them in order), the
+    // last batch that gathered out of / scattered into each frame, and the
+    // newest batch known finished or already waited for by the engine.
+    std::deque<SwapBatchEvent> swap_events_;
+    std::vector<void*> spare_events_;
+    std::vector<std::uint64_t> gather_epoch_;
+    std::vector<std::uint64_t> scatter_epoch_;
+    std::uint64_t swap_epoch_{0};
+    std::uint64_t completed_epoch_{0};
+    std::uint64_t engine_waited_epoch_{0};
     bool own_stream_{false};
     bool ok_{true};
     std::string last_error_;

@@ -44,7 +44,12 @@ public:
 private:
     std::size_t max_slots_{0};
     SwapSlotId next_slot_{1};
-    std::unordered_map<SwapSlotId, std::vector<std::byte>> slots_;
+    // Slot id -> buffer holding its bytes. Buffers of discarded slots are
+    // kept and reused by later stores (a swap store cycles through the same
+    // frame size), so a store allocates only while the store grows.
+    std::unordered_map<SwapSlotId, std::size_t> slot_buffer_;
+    std::vector<std::vector<std::byte>> buffers_;
+    std::vector<std::size_t> idle_buffers_;
 };
 
 // Swap space for a device-placement MemoryAllocator: max_slots frames of

@@ -102,8 +102,11 @@ bool KVAppendBatch::append(KVCacheManager& cache, MemoryAllocator& allocator, co
         return true;
     }
 
-    // The copies ensure_token_writable queued run first, on the same stream.
-    if (!allocator.flush()) return fail("flush: " + allocator.last_error());
+    // The copies ensure_token_writable queued run first, on the same stream,
+    // and the frames written here wait for any swap still moving them.
+    if (!allocator.flush() || !allocator.order_frame_writes(frames_)) {
+        return fail("flush: " + allocator.last_error());
+    }
     qvp_append_args a{};
     a.kv_base = allocator.device_base();
     a.block_stride = allocator.block_stride();

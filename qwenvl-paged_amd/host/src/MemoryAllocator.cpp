@@ -1,5 +1,7 @@
-// Physical block pool (src/MemoryAllocator.cpp of the reference), with a
-// device placement whose byte movements run as batched launches (libqvp).
+// Physical block pool (API: include/qwenvl_paged/MemoryAllocator.h of the
+// reference; decisions: src/MemoryAllocator.cpp), with a device placement
+// whose byte movements run as batched launches (libqvp): copies on the engine
+// stream, swap gathers and scatters on a side stream that runs beside it.
 #include "qwenvl_paged/MemoryAllocator.h"
 
 #include "qvp.h"
@@ -12,54 +14,50 @@
 namespace qwenvl_paged {
 
 MemoryAllocator::MemoryAllocator(AllocatorConfig config) : config_(config) {
+    const std::uint32_t n = config_.max_blocks;
     std::byte* base = nullptr;
     std::size_t stride = 0;
-    if (config_.placement == BlockPlacement::Device) {
-        if (config_.max_blocks == 0) {
-            // An empty device pool holds nothing to place on the device.
-            return;
-        }
-        const int st = qvp_pool_create(config_.max_blocks, config_.block_shape.byte_size(),
-                                       config_.memory_options.alignment_bytes, &pool_);
-        if (st != QVP_OK) {
+    if (config_.placement == BlockPlacement::Device && n > 0) {
+        // One pool allocation; frame i at base + i * stride.
+        if (qvp_pool_create(n, config_.block_shape.byte_size(), config_.memory_options.alignment_bytes, &pool_) !=
+            QVP_OK) {
             fail(std::string("qvp_pool_create: ") + qvp_last_error());
             return;
         }
         base = static_cast<std::byte*>(qvp_pool_base(pool_));
         stride = qvp_pool_block_stride(pool_);
-        if (config_.stream != nullptr) {
-            stream_ = config_.stream;
-        } else if (qvp_stream_create(&stream_) == QVP_OK) {
-            own_stream_ = true;
-        } else {
-            fail(std::string("qvp_stream_create: ") + qvp_last_error());
-            return;
-        }
-        if (qvp_stream_create(&side_stream_) != QVP_OK || qvp_event_create(&main_event_) != QVP_OK ||
-            qvp_event_create(&side_event_) != QVP_OK) {
+        own_stream_ = config_.stream == nullptr;
+        stream_ = config_.stream;
+        const bool streams = (!own_stream_ || qvp_stream_create(&stream_) == QVP_OK) &&
+                             qvp_stream_create(&side_stream_) == QVP_OK &&
+                             qvp_event_create(&main_event_) == QVP_OK;
+        if (!streams) {
             fail(std::string("stream/event setup: ") + qvp_last_error());
             return;
         }
+        gather_epoch_.assign(n, 0);
+        scatter_epoch_.assign(n, 0);
+    } else if (config_.placement == BlockPlacement::Device) {
+        // An empty device pool holds nothing to place on the device.
+        return;
     }
 
-    blocks_.reserve(config_.max_blocks);
-    infos_.reserve(config_.max_blocks);
-    free_list_.reserve(config_.max_blocks);
-    for (std::uint32_t i = 0; i < config_.max_blocks; ++i) {
-        if (config_.placement == BlockPlacement::Device) {
-            blocks_.push_back(std::make_unique<PhysicalBlock>(i, config_.block_shape, config_.memory_options,
-                                                              base + static_cast<std::size_t>(i) * stride, stride));
-        } else {
-            blocks_.push_back(std::make_unique<PhysicalBlock>(i, config_.block_shape, config_.memory_options));
-        }
-        PhysicalBlockInfo info;
-        info.id = i;
-        ++state_counts_[static_cast<std::size_t>(info.state)];
+    // Every frame starts free. The free list is a stack holding 0..N-1, so
+    // the first allocate() hands out frame N-1 and a released frame is the
+    // next one handed out.
+    infos_.resize(n);
+    free_list_.resize(n);
+    blocks_.reserve(n);
+    for (PhysicalBlockId id = 0; id < n; ++id) {
+        infos_[id].id = id;
+        free_list_[id] = id;
+        blocks_.push_back(config_.placement == BlockPlacement::Device
+                              ? std::make_unique<PhysicalBlock>(id, config_.block_shape, config_.memory_options,
+                                                                base + static_cast<std::size_t>(id) * stride, stride)
+                              : std::make_unique<PhysicalBlock>(id, config_.block_shape, config_.memory_options));
         bytes_reserved_ += blocks_.back()->size_bytes();
-        infos_.push_back(info);
-        // Free list 0..N-1, so allocate() pops N-1 first.
-        free_list_.push_back(i);
     }
+    state_counts_[static_cast<std::size_t>(BlockState::Free)] = n;
 }
 
 MemoryAllocator::~MemoryAllocator() {
@@ -68,17 +66,11 @@ MemoryAllocator::~MemoryAllocator() {
     // operations still queued are dropped with it.
     if (stream_ != nullptr) (void)qvp_stream_synchronize(stream_);
     if (side_stream_ != nullptr) (void)qvp_stream_synchronize(side_stream_);
+    for (SwapBatchEvent& b : swap_events_) (void)qvp_event_destroy(b.event);
     (void)qvp_event_destroy(main_event_);
-    (void)qvp_event_destroy(side_event_);
     (void)qvp_stream_destroy(side_stream_);
     if (own_stream_) (void)qvp_stream_destroy(stream_);
     (void)qvp_pool_destroy(pool_);
-}
-
-void MemoryAllocator::set_state(PhysicalBlockInfo& info, BlockState state) noexcept {
-    --state_counts_[static_cast<std::size_t>(info.state)];
-    ++state_counts_[static_cast<std::size_t>(state)];
-    info.state = state;
 }
 
 bool MemoryAllocator::fail(const std::string& what) {
@@ -87,48 +79,51 @@ bool MemoryAllocator::fail(const std::string& what) {
     return false;
 }
 
+// The one place a frame's reference count changes. Its state follows from the
+// count (0 free, 1 active, more shared), and the per-state counts behind
+// stats() move with it. Dropping to zero returns the frame to the top of the
+// free stack under a new generation, so ids held across the free are stale.
+void MemoryAllocator::set_ref_count(PhysicalBlockInfo& info, std::uint32_t count) noexcept {
+    const BlockState next = count == 0 ? BlockState::Free : (count == 1 ? BlockState::Active : BlockState::Shared);
+    --state_counts_[static_cast<std::size_t>(info.state)];
+    ++state_counts_[static_cast<std::size_t>(next)];
+    if (count == 0 && info.ref_count != 0) {
+        ++info.generation;
+        free_list_.push_back(info.id);
+    }
+    info.ref_count = count;
+    info.state = next;
+}
+
 std::optional<PhysicalBlockId> MemoryAllocator::allocate() {
     if (free_list_.empty()) return std::nullopt;
     const PhysicalBlockId id = free_list_.back();
     free_list_.pop_back();
-    PhysicalBlockInfo& info = infos_[id];
-    set_state(info, BlockState::Active);
-    info.ref_count = 1;
+    set_ref_count(infos_[id], 1);
     return id;
 }
 
 void MemoryAllocator::release(PhysicalBlockId id) {
-    if (id >= infos_.size()) return;
-    PhysicalBlockInfo& info = infos_[id];
-    if (info.ref_count == 0) return;
-    --info.ref_count;
-    if (info.ref_count == 0) {
-        set_state(info, BlockState::Free);
-        ++info.generation;
-        free_list_.push_back(id);
-    } else if (info.ref_count == 1) {
-        set_state(info, BlockState::Active);
-    }
+    PhysicalBlockInfo* held = id < infos_.size() ? &infos_[id] : nullptr;
+    if (held != nullptr && held->ref_count > 0) set_ref_count(*held, held->ref_count - 1);
 }
 
 void MemoryAllocator::retain(PhysicalBlockId id) {
-    if (id >= infos_.size()) return;
-    PhysicalBlockInfo& info = infos_[id];
-    if (info.ref_count == 0) return;
-    ++info.ref_count;
-    set_state(info, BlockState::Shared);
+    // Only a frame someone holds can gain a sharer.
+    PhysicalBlockInfo* held = id < infos_.size() ? &infos_[id] : nullptr;
+    if (held != nullptr && held->ref_count > 0) set_ref_count(*held, held->ref_count + 1);
 }
 
 void MemoryAllocator::copy_block(PhysicalBlockId source, PhysicalBlockId destination) {
-    PhysicalBlock* src = block(source);
-    PhysicalBlock* dst = block(destination);
-    if (src == nullptr || dst == nullptr) return;
+    PhysicalBlock* from = block(source);
+    PhysicalBlock* to = block(destination);
+    if (from == nullptr || to == nullptr) return;
     if (config_.placement == BlockPlacement::Device) {
+        // Queued; flush() runs the step's copies as one launch.
         if (source != destination) queue_.push_back(DeviceOp{OpKind::Copy, source, destination, nullptr, 0, 0});
         return;
     }
-    const std::size_t bytes = std::min(src->size_bytes(), dst->size_bytes());
-    std::memcpy(dst->data(), src->data(), bytes);
+    std::memcpy(to->data(), from->data(), std::min(from->size_bytes(), to->size_bytes()));
 }
 
 PhysicalBlock* MemoryAllocator::block(PhysicalBlockId id) noexcept {
@@ -150,33 +145,27 @@ void MemoryAllocator::detach_swap_backend(const SwapBackend* backend) noexcept {
 }
 
 std::optional<SwapSlotId> MemoryAllocator::swap_out(PhysicalBlockId id) {
-    if (swap_backend_ == nullptr || id >= infos_.size()) return std::nullopt;
-    PhysicalBlockInfo& info = infos_[id];
-    // A free block has nothing to evict; a shared one is still mapped by a
-    // sibling (src/MemoryAllocator.cpp:113-116).
-    if (info.ref_count != 1) return std::nullopt;
-    PhysicalBlock* frame = block(id);
-    if (frame == nullptr) return std::nullopt;
-    const std::optional<SwapSlotId> slot = swap_backend_->store(*frame);
-    if (!slot) return std::nullopt;
-    info.ref_count = 0;
-    set_state(info, BlockState::Free);
-    ++info.generation;
-    free_list_.push_back(id);
+    // Only a frame held by exactly one sequence can leave the pool: a free
+    // frame holds nothing and a shared one is still mapped by a sibling.
+    PhysicalBlockInfo* held = (swap_backend_ != nullptr && id < infos_.size()) ? &infos_[id] : nullptr;
+    if (held == nullptr || held->ref_count != 1 || block(id) == nullptr) return std::nullopt;
+    const std::optional<SwapSlotId> slot = swap_backend_->store(*block(id));
+    if (slot) set_ref_count(*held, 0);
     return slot;
 }
 
 std::optional<PhysicalBlockId> MemoryAllocator::swap_in(SwapSlotId slot) {
     if (swap_backend_ == nullptr) return std::nullopt;
-    const std::optional<PhysicalBlockId> id = allocate();
-    if (!id) return std::nullopt;
-    PhysicalBlock* frame = block(*id);
-    if (frame == nullptr || !swap_backend_->load(slot, *frame)) {
-        release(*id);
+    // The bytes come back into a freshly allocated frame; the slot is freed
+    // only once they are in (a failed load gives the frame back).
+    const std::optional<PhysicalBlockId> frame = allocate();
+    if (!frame) return std::nullopt;
+    if (!swap_backend_->load(slot, *block(*frame))) {
+        release(*frame);
         return std::nullopt;
     }
     swap_backend_->discard(slot);
-    return id;
+    return frame;
 }
 
 void MemoryAllocator::discard_swapped(SwapSlotId slot) {
@@ -245,6 +234,10 @@ bool MemoryAllocator::run_batch(OpKind kind, const std::vector<DeviceOp>& ops) {
         off[i] = ops[i].offset;
     }
     if (kind == OpKind::Copy) {
+        // Copies run on the engine stream: their sources may still be coming
+        // back from the swap store, their destinations may still be read by
+        // a gather.
+        if (!order_engine_after_swaps(a.data(), n, false) || !order_engine_after_swaps(b.data(), n, true)) return false;
         const int st = qvp_copy_blocks(qvp_pool_base(pool_), stride, config_.max_blocks, a.data(), b.data(), n, stride,
                                        stream_);
         if (st != QVP_OK) return fail(std::string("qvp_copy_blocks: ") + qvp_last_error());
@@ -252,7 +245,10 @@ bool MemoryAllocator::run_batch(OpKind kind, const std::vector<DeviceOp>& ops) {
         return true;
     }
     // Swap traffic runs on the side stream, after everything already on the
-    // engine stream, and the engine stream waits for it.
+    // engine stream (which wrote the frames a gather reads and may still read
+    // the frames a scatter overwrites). The engine stream does not wait for
+    // it here: a completion event per batch lets later engine work wait only
+    // where it touches a frame the batch moved (order_frame_reads / _writes).
     if (qvp_event_record(main_event_, stream_) != QVP_OK || qvp_stream_wait_event(side_stream_, main_event_) != QVP_OK) {
         return fail(std::string("swap ordering: ") + qvp_last_error());
     }
@@ -262,11 +258,71 @@ bool MemoryAllocator::run_batch(OpKind kind, const std::vector<DeviceOp>& ops) {
                        : qvp_swap_scatter(qvp_pool_base(pool_), stride, config_.max_blocks, a.data(), off.data(), n,
                                           ops[0].arena, ops[0].arena_bytes, stride, side_stream_);
     if (st != QVP_OK) return fail(std::string("swap launch: ") + qvp_last_error());
-    if (qvp_event_record(side_event_, side_stream_) != QVP_OK || qvp_stream_wait_event(stream_, side_event_) != QVP_OK) {
+    void* done = nullptr;
+    if (!spare_events_.empty()) {
+        done = spare_events_.back();
+        spare_events_.pop_back();
+    } else if (qvp_event_create(&done) != QVP_OK) {
+        return fail(std::string("swap event: ") + qvp_last_error());
+    }
+    if (qvp_event_record(done, side_stream_) != QVP_OK) {
+        (void)qvp_event_destroy(done);
         return fail(std::string("swap ordering: ") + qvp_last_error());
     }
+    const std::uint64_t epoch = ++swap_epoch_;
+    swap_events_.push_back(SwapBatchEvent{epoch, done});
+    std::vector<std::uint64_t>& moved = kind == OpKind::Gather ? gather_epoch_ : scatter_epoch_;
+    for (const DeviceOp& op : ops) moved[op.frame_a] = epoch;
     ++swap_launches_;
     return true;
+}
+
+bool MemoryAllocator::retire_swap_batches() {
+    while (!swap_events_.empty()) {
+        int complete = 0;
+        if (qvp_event_query(swap_events_.front().event, &complete) != QVP_OK) {
+            return fail(std::string("swap event query: ") + qvp_last_error());
+        }
+        if (complete == 0) break;
+        completed_epoch_ = swap_events_.front().epoch;
+        spare_events_.push_back(swap_events_.front().event);
+        swap_events_.pop_front();
+    }
+    return true;
+}
+
+bool MemoryAllocator::order_engine_after_swaps(const PhysicalBlockId* frames, std::size_t n, bool writes) {
+    if (config_.placement != BlockPlacement::Device || swap_events_.empty()) return true;
+    // A read depends on the last scatter into the frame; a write also on the
+    // last gather out of it (which must have read the old bytes first).
+    std::uint64_t need = 0;
+    for (std::size_t k = 0; k < n; ++k) {
+        if (frames[k] >= scatter_epoch_.size()) continue;
+        need = std::max(need, scatter_epoch_[frames[k]]);
+        if (writes) need = std::max(need, gather_epoch_[frames[k]]);
+    }
+    if (need <= std::max(completed_epoch_, engine_waited_epoch_)) return true;
+    if (!retire_swap_batches()) return false;
+    if (need <= completed_epoch_) return true;
+    // Batches finish in launch order, so waiting for batch `need` covers
+    // every earlier one.
+    for (const SwapBatchEvent& b : swap_events_) {
+        if (b.epoch != need) continue;
+        if (qvp_stream_wait_event(stream_, b.event) != QVP_OK) {
+            return fail(std::string("swap ordering: ") + qvp_last_error());
+        }
+        engine_waited_epoch_ = need;
+        return true;
+    }
+    return fail("swap batch event missing");
+}
+
+bool MemoryAllocator::order_frame_reads(const std::vector<PhysicalBlockId>& frames) {
+    return order_engine_after_swaps(frames.data(), frames.size(), false);
+}
+
+bool MemoryAllocator::order_frame_writes(const std::vector<PhysicalBlockId>& frames) {
+    return order_engine_after_swaps(frames.data(), frames.size(), true);
 }
 
 bool MemoryAllocator::flush() {
@@ -327,7 +383,7 @@ bool MemoryAllocator::write_block_bytes(PhysicalBlockId id, std::size_t offset, 
         std::memcpy(b->data() + offset, src, bytes);
         return true;
     }
-    if (!flush()) return false;
+    if (!flush() || !order_engine_after_swaps(&id, 1, true)) return false;
     if (qvp_pool_write(pool_, id, offset, src, bytes, stream_) != QVP_OK || qvp_stream_synchronize(stream_) != QVP_OK) {
         return fail(std::string("block write: ") + qvp_last_error());
     }
@@ -341,7 +397,7 @@ bool MemoryAllocator::read_block_bytes(PhysicalBlockId id, std::size_t offset, v
         std::memcpy(dst, b->data() + offset, bytes);
         return true;
     }
-    if (!flush()) return false;
+    if (!flush() || !order_engine_after_swaps(&id, 1, false)) return false;
     if (qvp_pool_read(pool_, id, offset, dst, bytes, stream_) != QVP_OK || qvp_stream_synchronize(stream_) != QVP_OK) {
         return fail(std::string("block read: ") + qvp_last_error());
     }
@@ -353,7 +409,7 @@ bool MemoryAllocator::synchronize() {
     const bool flushed = flush();
     if (stream_ != nullptr && qvp_stream_synchronize(stream_) != QVP_OK) return fail(qvp_last_error());
     if (side_stream_ != nullptr && qvp_stream_synchronize(side_stream_) != QVP_OK) return fail(qvp_last_error());
-    return flushed;
+    return retire_swap_batches() && flushed;
 }
 
 }  // namespace qwenvl_paged

@@ -179,7 +179,8 @@ bool PagedAttentionBatch::pack(const std::vector<CacheView>& views, const std::v
     // Queued copy-on-write copies and swap traffic land before the kernels
     // read any frame.
     MemoryAllocator* mut = const_cast<MemoryAllocator*>(allocator);
-    if (!mut->flush()) return fail("flush: " + mut->last_error());
+    // The frames read here may still be coming back from the swap store.
+    if (!mut->flush() || !mut->order_frame_reads(ids_)) return fail("flush: " + mut->last_error());
     stream = allocator->stream();
     const PhysicalBlock* frame0 = allocator->block(0);
     const std::uint32_t num_blocks = static_cast<std::uint32_t>(allocator->stats().total_blocks);

@@ -1,10 +1,12 @@
-// Swap stores: host memory (src/SwapBackend.cpp of the reference) and the
+// Swap stores: host memory (API: include/qwenvl_paged/SwapBackend.h of the
+// reference; slot numbering and capacity rules: src/SwapBackend.cpp) and the
 // pinned-arena backend of the device allocator.
 #include "qwenvl_paged/SwapBackend.h"
 
 #include "qvp.h"
 #include "qwenvl_paged/MemoryAllocator.h"
 
+#include <algorithm>
 #include <cstring>
 #include <utility>
 
@@ -13,25 +15,40 @@ namespace qwenvl_paged {
 HostSwapBackend::HostSwapBackend(std::size_t max_slots) : max_slots_(max_slots) {}
 
 std::optional<SwapSlotId> HostSwapBackend::store(const PhysicalBlock& block) {
-    if (slots_.size() >= max_slots_) return std::nullopt;
-    std::vector<std::byte> bytes(block.size_bytes());
-    if (!bytes.empty()) std::memcpy(bytes.data(), block.data(), bytes.size());
-    const SwapSlotId slot = next_slot_++;
-    slots_.emplace(slot, std::move(bytes));
-    return slot;
+    // Capacity counts resident slots; slot ids count up from 1 and are never
+    // reused, so a stale id can never name newer bytes.
+    if (slot_buffer_.size() >= max_slots_) return std::nullopt;
+    std::size_t buf = buffers_.size();
+    if (idle_buffers_.empty()) {
+        buffers_.emplace_back();
+    } else {
+        buf = idle_buffers_.back();
+        idle_buffers_.pop_back();
+    }
+    std::vector<std::byte>& bytes = buffers_[buf];
+    bytes.assign(block.data(), block.data() + block.size_bytes());
+    slot_buffer_.emplace(next_slot_, buf);
+    return next_slot_++;
 }
 
 bool HostSwapBackend::load(SwapSlotId slot, PhysicalBlock& block) {
-    auto it = slots_.find(slot);
-    if (it == slots_.end()) return false;
-    const std::vector<std::byte>& bytes = it->second;
-    if (block.size_bytes() < bytes.size()) return false;
-    if (!bytes.empty()) std::memcpy(block.data(), bytes.data(), bytes.size());
+    // The slot stays resident after a load; discard() frees it.
+    const auto it = slot_buffer_.find(slot);
+    if (it == slot_buffer_.end()) return false;
+    const std::vector<std::byte>& bytes = buffers_[it->second];
+    if (bytes.size() > block.size_bytes()) return false;
+    std::copy(bytes.begin(), bytes.end(), block.data());
     return true;
 }
 
-void HostSwapBackend::discard(SwapSlotId slot) { slots_.erase(slot); }
-std::size_t HostSwapBackend::resident_slots() const noexcept { return slots_.size(); }
+void HostSwapBackend::discard(SwapSlotId slot) {
+    const auto it = slot_buffer_.find(slot);
+    if (it == slot_buffer_.end()) return;
+    idle_buffers_.push_back(it->second);
+    slot_buffer_.erase(it);
+}
+
+std::size_t HostSwapBackend::resident_slots() const noexcept { return slot_buffer_.size(); }
 std::size_t HostSwapBackend::capacity_slots() const noexcept { return max_slots_; }
 
 // ---------------------------------------------------------------------------

@@ -170,6 +170,7 @@ SIGNATURES = {
     "qvp_event_record": (c_int, [c_void_p, c_void_p]),
     "qvp_event_synchronize": (c_int, [c_void_p]),
     "qvp_stream_wait_event": (c_int, [c_void_p, c_void_p]),
+    "qvp_event_query": (c_int, [c_void_p, POINTER(c_int)]),
     "qvp_event_elapsed_ms": (c_int, [POINTER(c_float), c_void_p, c_void_p]),
     "qvp_pool_create": (c_int, [c_uint32, c_size_t, c_size_t, POINTER(c_void_p)]),
     "qvp_pool_destroy": (c_int, [c_void_p]),

@@ -328,3 +328,34 @@ TEST(DeviceAllocatorTest, DeviceEngineReproducesTheReferenceSchedulerTrace) {
         EXPECT_GT(allocator.swap_launches(), 0u);
     }
 }
+
+TEST(DeviceAllocatorTest, DeviceEngineReproducesTheConfig5Trace) {
+    // The fifth benchmark configuration's trace at full size (200 requests,
+    // pool 60 % of demand, watermark 64; tests/golden/make_golden.py
+    // CONFIG5_PARAMS), on device frames and the pinned arena.
+    trace::Config c;
+    c.requests = 200;
+    c.prompt_lo = 128;
+    c.prompt_hi = 8192;
+    c.output_lo = 32;
+    c.output_hi = 1024;
+    c.arrivals_per_step = 200;
+    c.pool_percent = 60;
+    c.watermark_blocks = 64;
+    c.max_active = 256;
+    c.max_batch_tokens = 16384;
+    c.max_steps = 200000;
+    c.cancel_after_decodes = true;
+    c.seed = 5;
+    std::string expected;
+    ASSERT_TRUE(golden::read_gz("scheduler_trace_config5.txt.gz", expected));
+    MemoryAllocator allocator(device_config(shape_of(c.tokens_per_block, 1, 1, 8, 4), trace::pool_blocks(c)));
+    PinnedSwapBackend swap(allocator, trace::pool_blocks(c));
+    ASSERT_TRUE(allocator.ok() && swap.ok());
+    allocator.set_swap_backend(&swap);
+    const std::string log =
+        trace::run<MemoryAllocator, KVCacheManager, Scheduler, SchedulerConfig, Request, RequestState>(c, allocator);
+    EXPECT_TRUE(log == expected) << golden::first_difference(log, expected);
+    EXPECT_TRUE(allocator.synchronize());
+    EXPECT_GT(allocator.swap_launches(), 0u);
+}

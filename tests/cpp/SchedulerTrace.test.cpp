@@ -39,14 +39,18 @@ AllocatorConfig trace_pool(const trace::Config& c) {
 
 void check_trace(const char* fixture, const trace::Config& c) {
     std::string expected;
-    ASSERT_TRUE(golden::read(fixture, expected)) << "missing fixture " << golden::dir() << "/" << fixture;
+    const std::string name = fixture;
+    const bool gz = name.size() > 3 && name.compare(name.size() - 3, 3, ".gz") == 0;
+    ASSERT_TRUE(gz ? golden::read_gz(name, expected) : golden::read(name, expected))
+        << "missing fixture " << golden::dir() << "/" << fixture;
     MemoryAllocator allocator(trace_pool(c));
     HostSwapBackend swap(1u << 20);
     allocator.set_swap_backend(&swap);
     const std::string log =
         trace::run<MemoryAllocator, KVCacheManager, Scheduler, SchedulerConfig, Request, RequestState>(c, allocator);
     EXPECT_TRUE(log == expected) << golden::first_difference(log, expected);
-    EXPECT_NE(log.find("finished=32 of 32"), std::string::npos);
+    const std::string all = "finished=" + std::to_string(c.requests) + " of " + std::to_string(c.requests);
+    EXPECT_NE(log.find(all), std::string::npos);
 }
 
 }  // namespace
@@ -57,4 +61,28 @@ TEST(SchedulerTraceTest, WatermarkTraceMatchesTheReference) {
 
 TEST(SchedulerTraceTest, GrowthPreemptionTraceMatchesTheReference) {
     check_trace("scheduler_trace_w0.txt", trace_config(11, 30, 0));
+}
+
+// The fifth benchmark configuration at full size (the settings of
+// tests/golden/make_golden.py's CONFIG5_PARAMS): 200 requests at once, prompts
+// [128, 8192], outputs [32, 1024], pool 60 % of demand, watermark 64 blocks,
+// 256 active requests, 16384 scheduled tokens, cancels after the step's
+// decodes.
+TEST(SchedulerTraceTest, Config5TraceMatchesTheReference) {
+    trace::Config c;
+    c.requests = 200;
+    c.prompt_lo = 128;
+    c.prompt_hi = 8192;
+    c.output_lo = 32;
+    c.output_hi = 1024;
+    c.arrivals_per_step = 200;
+    c.tokens_per_block = 16;
+    c.pool_percent = 60;
+    c.watermark_blocks = 64;
+    c.max_active = 256;
+    c.max_batch_tokens = 16384;
+    c.max_steps = 200000;
+    c.cancel_after_decodes = true;
+    c.seed = 5;
+    check_trace("scheduler_trace_config5.txt.gz", c);
 }

@@ -9,6 +9,7 @@
 
 #include <limits.h>
 #include <unistd.h>
+#include <zlib.h>
 
 namespace golden {
 
@@ -29,6 +30,19 @@ inline bool read(const std::string& name, std::string& out) {
     ss << f.rdbuf();
     out = ss.str();
     return true;
+}
+
+// A gzip-compressed fixture, decompressed.
+inline bool read_gz(const std::string& name, std::string& out) {
+    gzFile f = gzopen((dir() + "/" + name).c_str(), "rb");
+    if (f == nullptr) return false;
+    out.clear();
+    char buf[1 << 16];
+    int n = 0;
+    while ((n = gzread(f, buf, sizeof buf)) > 0) out.append(buf, static_cast<std::size_t>(n));
+    const bool ok = n == 0;
+    gzclose(f);
+    return ok;
 }
 
 // First differing line of two logs, for the failure message.

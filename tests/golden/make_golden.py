@@ -15,11 +15,15 @@ Fixtures (data only: inputs are regenerated from seeds, outputs stored):
   scheduler_trace_w0.txt   oracle/trace_driver.h on the reference's Scheduler /
                            KVCacheManager / MemoryAllocator / HostSwapBackend
                            (preemption watermark 4 and 0 blocks)
+  scheduler_trace_config5.txt.gz
+                           the same trace at the fifth benchmark configuration
+                           (200 requests, pool 60 % of demand, watermark 64)
 """
 
 from __future__ import annotations
 
 import ctypes
+import gzip
 import hashlib
 import sys
 from pathlib import Path
@@ -37,6 +41,18 @@ HERE = Path(__file__).resolve().parent
 # Trace settings shared with tests/cpp/SchedulerTrace.test.cpp.
 TRACES = {"scheduler_trace_w4.txt": dict(requests=32, seed=5, pool_percent=30, watermark=4),
           "scheduler_trace_w0.txt": dict(requests=32, seed=11, pool_percent=30, watermark=0)}
+
+# The fifth benchmark configuration's trace (qwenvl-paged_amd/host/bench/
+# trace_bench.cpp): 200 requests arriving at once, prompts uniform on
+# [128, 8192], outputs on [32, 1024], seed 5, block 16, pool 60 % of demand,
+# watermark 64 blocks, up to 256 active requests and 16384 scheduled tokens,
+# finished requests cancelled after the step's decodes. Order: requests,
+# prompt_lo, prompt_hi, output_lo, output_hi, arrivals_per_step,
+# tokens_per_block, pool_percent, watermark_blocks, max_active,
+# max_batch_tokens, max_steps, cancel_after_decodes.
+CONFIG5_TRACE = "scheduler_trace_config5.txt.gz"
+CONFIG5_PARAMS = (200, 128, 8192, 32, 1024, 200, 16, 60, 64, 256, 16384, 200000, 1)
+CONFIG5_SEED = 5
 
 
 def golden_workloads() -> dict[str, W.Workload]:
@@ -79,6 +95,19 @@ def reference_trace(requests: int, seed: int, pool_percent: int, watermark: int)
     return buf.value.decode()
 
 
+def reference_trace_config(params, seed: int) -> str:
+    lib = O.reference()
+    lib.ref_scheduler_trace_config.restype = ctypes.c_uint64
+    lib.ref_scheduler_trace_config.argtypes = [ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint64, ctypes.c_char_p,
+                                               ctypes.c_uint64]
+    cfg = (ctypes.c_uint32 * len(params))(*params)
+    cap = 1 << 26
+    buf = ctypes.create_string_buffer(cap)
+    n = lib.ref_scheduler_trace_config(cfg, seed, buf, cap)
+    assert n < cap
+    return buf.value.decode()
+
+
 def main() -> None:
     if not O.reference_available():
         raise SystemExit("oracle/_ref/libqvp_ref.so is missing: run `make -C oracle` with the reference tree present")
@@ -89,7 +118,10 @@ def main() -> None:
     np.savez_compressed(HERE / "decode_goldens.npz", **arrays)
     for fname, t in TRACES.items():
         (HERE / fname).write_text(reference_trace(t["requests"], t["seed"], t["pool_percent"], t["watermark"]))
-    print("wrote", ", ".join(["decode_goldens.npz", *TRACES]))
+    # mtime 0 keeps the compressed bytes a function of the log alone.
+    (HERE / CONFIG5_TRACE).write_bytes(
+        gzip.compress(reference_trace_config(CONFIG5_PARAMS, CONFIG5_SEED).encode(), mtime=0))
+    print("wrote", ", ".join(["decode_goldens.npz", *TRACES, CONFIG5_TRACE]))
 
 
 if __name__ == "__main__":

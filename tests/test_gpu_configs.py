@@ -1,19 +1,30 @@
-"""The copy-on-write and continuous-batching configurations on the GPU, at
-reduced sizes, through their C++ drivers (qwenvl-paged_amd/host/bench): the
-device allocator's decisions and bytes equal the host allocator's, copied
-frames equal their sources, sampled decodes match float64 attention, and a
-scheduler trace with preemption and swap drains completely."""
+"""The copy-on-write (config4) and continuous-batching (config5)
+configurations on the GPU at their full sizes, through their C++ drivers
+(qwenvl-paged_amd/host/bench): the device allocator's decisions and bytes
+equal the host allocator's, copied frames equal their sources, sampled
+decodes match float64 attention, the 200-request trace writes the event log
+the reference's own Scheduler / KVCacheManager / MemoryAllocator wrote for the
+same requests (tests/golden/scheduler_trace_config5.txt.gz) and drains
+completely. A config4-shaped step through the C ABI is compared with the
+oracle element by element."""
 
 from __future__ import annotations
 
+import gzip
 import json
 import subprocess
 from pathlib import Path
 
+import numpy as np
 import pytest
+
+import qvp
+import workloads as W
+from helpers import assert_close_16bit, assert_close_bf16, oracle_decode, to_f32
 
 ROOT = Path(__file__).resolve().parents[1]
 BENCH = ROOT / "build" / "bench"
+GOLDEN = ROOT / "tests" / "golden"
 
 
 def run(name: str, *args: str) -> dict:
@@ -27,19 +38,104 @@ def run(name: str, *args: str) -> dict:
 
 
 @pytest.mark.gpu
-def test_copy_on_write_configuration_small():
-    r = run("cow_bench", "--prompts", "4", "--branches", "8", "--reps", "3")
-    assert r["cow_pairs"] == 32
-    assert r["pending_before_flush"] == 32
+def test_copy_on_write_configuration_full_size():
+    """config4 as specified: 16 prompts x 8 branches, 128 copy-on-write pairs
+    in one batched copy, decode over the 128 branches."""
+    r = run("cow_bench")
+    assert r["cow_pairs"] == 128
+    assert r["pending_before_flush"] == 128
     assert r["copy_launches"] == 1
     assert r["frames_equal_host_allocator"] and r["copies_equal_source"]
     assert r["decode_within_tolerance"] and r["checked_elements"] > 0
 
 
+def _reference_config5_log() -> str:
+    return gzip.decompress((GOLDEN / "scheduler_trace_config5.txt.gz").read_bytes()).decode()
+
+
+def _first_difference(a: str, b: str) -> str:
+    for k, (x, y) in enumerate(zip(a.splitlines(), b.splitlines())):
+        if x != y:
+            return f"line {k + 1}:\n  expected {y[:300]}\n  actual   {x[:300]}"
+    return f"lengths differ: {len(a.splitlines())} vs {len(b.splitlines())} lines"
+
+
 @pytest.mark.gpu
-def test_continuous_batching_trace_small():
-    r = run("trace_bench", "--requests", "24", "--seed", "7")
-    assert r["finished"] == 24 and r["drained"]
+@pytest.mark.parametrize("engine", ["0", "1"], ids=["decode-only", "full-engine-step"])
+def test_continuous_batching_trace_full_size_matches_the_reference(tmp_path, engine):
+    """config5 as specified: 200 requests, pool 60 % of demand, watermark 64.
+    The step log (admissions, preemptions, resumes, completions, frame and
+    swap-slot ids hashed per step) equals the reference's; every request
+    finishes and the pool and the swap arena drain. With the full engine step
+    (append, prefill, M-RoPE, decode) the decisions are the same."""
+    log = tmp_path / "trace.log"
+    r = run("trace_bench", "--requests", "200", "--seed", "5", "--engine", engine, "--log", str(log))
+    assert r["finished"] == 200 and r["drained"]
     assert r["decode_tokens"] == r["expected_decode_tokens"]
     assert r["preemptions"] > 0 and r["resumes"] > 0
     assert r["swapped_out_blocks"] > 0 and r["swapped_in_blocks"] > 0
+    got, expected = log.read_text(), _reference_config5_log()
+    assert got == expected, _first_difference(got, expected)
+
+
+@pytest.mark.gpu
+def test_config4_step_through_the_abi_matches_the_oracle():
+    """The config4 step on the C ABI at full size: 16 prompts of 2048 tokens
+    (2049 slots reserved, so logical block 128 is a partly filled tail), 8
+    branches each sharing the 128 full blocks; one qvp_copy_blocks gives every
+    branch a private copy of its prompt's tail (128 pairs, checked byte for
+    byte), each branch writes its first decode token into the copy, and one
+    decode runs over the 128 branches (context 2049) -- compared with the
+    oracle on every output element."""
+    prompts, branches, full = 16, 8, 128
+    w_shape = W.custom([16], 28, 4, 128)
+    block = w_shape.block_bytes
+    frames = prompts * (full + 1) + prompts * branches
+    rng = np.random.default_rng(44)
+    image = W.f32_to_bf16_bits(rng.normal(0.0, 0.5, frames * block // 2).astype(np.float32)).view(np.uint8)
+    pool = qvp.BlockPool(frames, block)
+    pool.upload_all(image)
+    prompt_frames = np.arange(prompts * (full + 1), dtype=np.uint32).reshape(prompts, full + 1)
+    branch_tail = np.arange(prompts * (full + 1), frames, dtype=np.uint32).reshape(prompts, branches)
+    src = np.repeat(prompt_frames[:, full], branches)
+    dst = branch_tail.reshape(-1)
+    print("case: config4 copy of 128 shared tails", flush=True)
+    qvp.copy_blocks(pool.base, pool.stride, frames, src, dst, pool.stride)
+    # Each branch's first decode token: position 2048, slot 0 of its tail copy.
+    st = qvp.layout_strides(16, 1, 4, 128)
+    k_new = W.f32_to_bf16_bits(rng.normal(0.0, 0.5, (prompts * branches, 4 * 128)).astype(np.float32))
+    v_new = W.f32_to_bf16_bits(rng.normal(0.0, 0.5, (prompts * branches, 4 * 128)).astype(np.float32))
+    for i, f in enumerate(dst):
+        pool.write(int(f), k_new[i].view(np.uint8), offset=0)
+        pool.write(int(f), v_new[i].view(np.uint8), offset=st["stream_stride"] * 2)
+    qvp.synchronize()
+    got_image = pool.download_all()
+    expect = image.reshape(frames, block).copy()
+    expect[dst] = expect[src]
+    for i, f in enumerate(dst):
+        expect[f, : 4 * 128 * 2] = k_new[i].view(np.uint8)
+        off = st["stream_stride"] * 2
+        expect[f, off: off + 4 * 128 * 2] = v_new[i].view(np.uint8)
+    assert np.array_equal(got_image.reshape(frames, block), expect), "copy-on-write frames differ"
+    ids = np.concatenate([np.concatenate([prompt_frames[p, :full], [branch_tail[p, b]]])
+                          for p in range(prompts) for b in range(branches)]).astype(np.uint32)
+    cu = np.arange(0, (full + 1) * prompts * branches + 1, full + 1, dtype=np.uint32)
+    w = W.custom([2049] * (prompts * branches), 28, 4, 128, seed=45)
+    w.ids, w.cu_blocks, w.num_pool_blocks = ids, cu, frames
+    query = w.query()
+    q = qvp.DeviceBuffer.from_array(query)
+    batch = qvp.Batch()
+    batch.pack(ids, cu, w.context_lens, 16, frames)
+    outs = {}
+    for od in (qvp.DTYPE_F32, qvp.DTYPE_BF16):
+        out = qvp.DeviceBuffer(w.num_seqs * 28 * 128 * qvp.DTYPE_BYTES[od])
+        args = qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=pool.base, block_stride=pool.stride, batch=batch,
+                               kv_dtype=qvp.DTYPE_BF16, out_dtype=od, layer=0, num_layers=1, num_query_heads=28,
+                               num_kv_heads=4, head_dim=128, tokens_per_block=16, scale=w.scale, strides=st)
+        print(f"case: config4 decode over 128 branches, out dtype {od}", flush=True)
+        qvp.paged_decode(args)
+        outs[od] = out.download(np.float32 if od == qvp.DTYPE_F32 else np.uint16, (w.num_seqs, 28, 128))
+    ref_out, ref32 = oracle_decode(w, got_image, query)
+    assert_close_bf16(outs[qvp.DTYPE_F32], ref32, "config4 fp32 out")
+    assert_close_16bit(outs[qvp.DTYPE_BF16], ref32, qvp.DTYPE_BF16, "config4 bf16 out")
+    assert_close_16bit(outs[qvp.DTYPE_BF16], to_f32(ref_out, qvp.DTYPE_BF16), qvp.DTYPE_BF16, "config4 vs oracle T")

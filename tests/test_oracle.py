@@ -147,6 +147,9 @@ def test_live_reference_reproduces_the_committed_fixtures():
     for fname, t in make_golden.TRACES.items():
         assert make_golden.reference_trace(t["requests"], t["seed"], t["pool_percent"], t["watermark"]) == \
             (GOLDEN / fname).read_text()
+    import gzip
+    assert make_golden.reference_trace_config(make_golden.CONFIG5_PARAMS, make_golden.CONFIG5_SEED) == \
+        gzip.decompress((GOLDEN / make_golden.CONFIG5_TRACE).read_bytes()).decode()
 
 
 # ---------------------------------------------------------------------------
