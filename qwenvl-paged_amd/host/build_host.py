@@ -9,6 +9,7 @@ Outputs (git-ignored, shipped with the tree):
   build/tests/device_tests          suites that run on device-placed frames (GPU)
   build/bench/cow_bench             copy-on-write configuration driver (GPU)
   build/bench/trace_bench           continuous-batching trace driver (GPU)
+  build/bench/config3_bench         long-context multimodal decode driver (GPU)
 
 libqvp.so must be built first (qwenvl-paged_amd/build.py does both).
 """
@@ -50,6 +51,7 @@ TEST_BINARIES = {
         "KVCacheManager.test.cpp",
         "Scheduler.test.cpp",
         "SchedulerTrace.test.cpp",
+        "ElementType.test.cpp",
     ],
     "device_tests": [
         "DeviceAllocator.test.cpp",
@@ -63,7 +65,7 @@ TEST_BINARIES = {
 
 
 # Benchmark drivers of the copy-on-write and continuous-batching configurations.
-BENCH_BINARIES = {"cow_bench": "cow_bench.cpp", "trace_bench": "trace_bench.cpp"}
+BENCH_BINARIES = {"cow_bench": "cow_bench.cpp", "trace_bench": "trace_bench.cpp", "config3_bench": "config3_bench.cpp"}
 
 
 def _run(cmd: list[str]) -> None:

@@ -7,10 +7,12 @@
 // pointer, sizeof(T) != bytes_per_element, context_len == 0, a layer outside
 // the shape, query heads that do not group onto the kv heads, or a needed block
 // that is unmapped or swapped out (PagedAttention.h:50-89). Otherwise the
-// computation runs on the GPU (libqvp: pack, then the split-K decode) and the
-// result is copied back. There is no CPU path: a view over host-placed frames
-// is refused. PagedAttentionBatch decodes many sequences in one launch from
-// device buffers; that is the engine's per-step entry point.
+// computation runs on the GPU (libqvp: pack, then the decode) and the result
+// is copied back. A view over host-placed frames (the reference's own
+// allocator) is decoded the same way: the layer's K/V slice of each block the
+// context needs is staged through pinned memory into device frames first.
+// There is no CPU path. PagedAttentionBatch decodes many sequences in one
+// launch from device buffers; that is the engine's per-step entry point.
 
 #include "qwenvl_paged/CacheLayout.h"
 #include "qwenvl_paged/KVCacheManager.h"
@@ -41,11 +43,23 @@ struct bf16 {
 };
 static_assert(sizeof(bf16) == 2, "bf16 must be two bytes");
 
+// IEEE binary16 cache element: two bytes, explicit conversions (float -> f16
+// rounds to nearest, ties to even, overflowing to infinity, with subnormal
+// results; NaN stays NaN).
+struct f16 {
+    std::uint16_t bits{0};
+    f16() = default;
+    explicit f16(float f) noexcept;
+    explicit operator float() const noexcept;
+};
+static_assert(sizeof(f16) == 2, "f16 must be two bytes");
+
 // Element type codes (values of qvp_dtype).
 enum class ElementType : int { F32 = 0, BF16 = 1, F16 = 2 };
 
 // Decodes one query token (query, out: host arrays of num_query_heads *
-// head_dim elements, head-major). T is float or bf16.
+// head_dim elements, head-major). T is float, bf16 or f16; a two-byte T also
+// names how the cache's elements are read.
 template <typename T>
 [[nodiscard]] bool paged_attention_decode(const CacheView& view, const T* query, const PagedAttentionParams& params,
                                           T* out);

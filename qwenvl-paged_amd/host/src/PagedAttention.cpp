@@ -28,6 +28,59 @@ bf16::operator float() const noexcept {
     return f;
 }
 
+// binary16 from float, rounding to nearest even at the 13 dropped mantissa
+// bits (normal results) or at the bits below 2^-24 (subnormal results).
+f16::f16(float f) noexcept {
+    std::uint32_t u;
+    std::memcpy(&u, &f, sizeof u);
+    const std::uint32_t sign = (u >> 16) & 0x8000u;
+    const std::uint32_t mag = u & 0x7fffffffu;
+    if (mag > 0x7f800000u) {
+        bits = static_cast<std::uint16_t>(sign | 0x7e00u | ((mag >> 13) & 0x3ffu));  // quiet NaN
+    } else if (mag >= 0x477ff000u) {
+        bits = static_cast<std::uint16_t>(sign | 0x7c00u);  // at or past 65520: infinity
+    } else if (mag >= 0x38800000u) {
+        // Normal: rebias the exponent (127 -> 15) after rounding; a carry out
+        // of the mantissa moves into the exponent, as it should.
+        const std::uint32_t r = mag + 0xfffu + ((mag >> 13) & 1u);
+        bits = static_cast<std::uint16_t>(sign | ((r - 0x38000000u) >> 13));
+    } else {
+        // Subnormal or zero: the value in units of 2^-24 is the full
+        // mantissa shifted right by 126 - exponent.
+        const std::uint32_t e = mag >> 23;
+        const std::uint32_t shift = 126u - e;
+        std::uint32_t m = 0;
+        if (shift < 25u) {
+            const std::uint32_t full = (mag & 0x7fffffu) | 0x800000u;
+            m = full >> shift;
+            const std::uint32_t rem = full & ((1u << shift) - 1u);
+            const std::uint32_t half = 1u << (shift - 1u);
+            if (rem > half || (rem == half && (m & 1u))) ++m;
+        }
+        bits = static_cast<std::uint16_t>(sign | m);
+    }
+}
+
+f16::operator float() const noexcept {
+    const std::uint32_t sign = static_cast<std::uint32_t>(bits & 0x8000u) << 16;
+    const std::uint32_t e = (bits >> 10) & 0x1fu;
+    const std::uint32_t m = bits & 0x3ffu;
+    std::uint32_t u;
+    if (e == 0x1fu) {
+        u = sign | 0x7f800000u | (m << 13);
+    } else if (e != 0) {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    } else {
+        // Subnormal: m x 2^-24, exact in float.
+        const float v = static_cast<float>(m) * 5.9604644775390625e-8f;
+        std::memcpy(&u, &v, sizeof u);
+        u |= sign;
+    }
+    float f;
+    std::memcpy(&f, &u, sizeof f);
+    return f;
+}
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -48,41 +101,131 @@ void collect_blocks(const CacheView& view, std::uint32_t context_len, std::vecto
     }
 }
 
-// Device staging for the single-sequence entry point, one per thread.
+// Grows a device (or pinned host) buffer to at least `bytes`.
+bool grow(void*& ptr, std::size_t& have, std::size_t bytes, bool pinned) {
+    if (have >= bytes) return true;
+    (void)(pinned ? qvp_host_free(ptr) : qvp_free(ptr));
+    ptr = nullptr;
+    have = 0;
+    if ((pinned ? qvp_host_alloc(&ptr, bytes) : qvp_malloc(&ptr, bytes)) != QVP_OK) return false;
+    have = bytes;
+    return true;
+}
+
+// Device staging for the single-sequence entry point, one per thread: query
+// and output buffers, and for views over host-placed frames a pinned and a
+// device copy of the frames' layer slices, their packed batch and a stream.
 struct SingleScratch {
     PagedAttentionBatch batch;
     void* dq{nullptr};
     void* dout{nullptr};
     std::size_t dq_bytes{0};
     std::size_t dout_bytes{0};
+    void* host_slices{nullptr};
+    void* dev_slices{nullptr};
+    std::size_t host_slice_bytes{0};
+    std::size_t dev_slice_bytes{0};
+    qvp_batch* staged{nullptr};
+    void* stream{nullptr};
 
     ~SingleScratch() {
+        if (stream != nullptr) (void)qvp_stream_synchronize(stream);
+        (void)qvp_batch_destroy(staged);
         (void)qvp_free(dq);
         (void)qvp_free(dout);
+        (void)qvp_host_free(host_slices);
+        (void)qvp_free(dev_slices);
+        if (stream != nullptr) (void)qvp_stream_destroy(stream);
     }
 
     bool ensure(std::size_t q_bytes, std::size_t o_bytes) {
-        if (dq_bytes < q_bytes) {
-            (void)qvp_free(dq);
-            dq = nullptr;
-            dq_bytes = 0;
-            if (qvp_malloc(&dq, q_bytes) != QVP_OK) return false;
-            dq_bytes = q_bytes;
-        }
-        if (dout_bytes < o_bytes) {
-            (void)qvp_free(dout);
-            dout = nullptr;
-            dout_bytes = 0;
-            if (qvp_malloc(&dout, o_bytes) != QVP_OK) return false;
-            dout_bytes = o_bytes;
-        }
-        return true;
+        return grow(dq, dq_bytes, q_bytes, false) && grow(dout, dout_bytes, o_bytes, false);
     }
 };
 
 template <typename T>
 constexpr ElementType element_type_of() {
-    return std::is_same<T, float>::value ? ElementType::F32 : ElementType::BF16;
+    return std::is_same<T, float>::value ? ElementType::F32
+                                         : (std::is_same<T, f16>::value ? ElementType::F16 : ElementType::BF16);
+}
+
+// Decode over host-placed frames: the layer's K/V slice of every block the
+// context needs (one contiguous run per block in the [layer][K|V][token]
+// [head][dim] order) is copied into pinned memory, uploaded in one transfer
+// and decoded as a pool of those slices (block i of the context is slice i,
+// one layer per slice). The checks already ran; every block is resolved
+// before anything is copied, so a refusal leaves `out` untouched.
+template <typename T>
+bool decode_host_frames(const CacheView& view, const T* query, const PagedAttentionParams& params, T* out,
+                        SingleScratch& scratch) {
+    const KVBlockLayout& layout = view.layout;
+    const BlockShape& shape = layout.shape;
+    const std::uint32_t tpb = shape.tokens_per_block;
+    const std::uint32_t needed = (params.context_len + tpb - 1) / tpb;
+    const std::size_t slice = layout.layer_stride() * shape.bytes_per_element;
+    const std::size_t layer_offset = static_cast<std::size_t>(params.layer) * slice;
+    std::vector<const std::byte*> frames(needed, nullptr);
+    for (std::uint32_t j = 0; j < needed; ++j) {
+        const BlockTableEntry* e = view.block_table->entry(j);
+        const PhysicalBlock* b = (e == nullptr || e->swap_slot) ? nullptr : view.allocator->block(e->physical_id);
+        if (b == nullptr || b->data() == nullptr || b->size_bytes() < layer_offset + slice) {
+            return refuse("a block of the context is unmapped or swapped out");
+        }
+        frames[j] = b->data() + layer_offset;
+    }
+    if (scratch.stream == nullptr && qvp_stream_create(&scratch.stream) != QVP_OK) {
+        return refuse(std::string("stream: ") + qvp_last_error());
+    }
+    if (scratch.staged == nullptr && qvp_batch_create(&scratch.staged) != QVP_OK) {
+        return refuse(std::string("batch: ") + qvp_last_error());
+    }
+    const std::size_t total = slice * needed;
+    if (!grow(scratch.host_slices, scratch.host_slice_bytes, total, true) ||
+        !grow(scratch.dev_slices, scratch.dev_slice_bytes, total, false)) {
+        return refuse(std::string("frame staging: ") + qvp_last_error());
+    }
+    // The previous call synchronized its stream before returning, so the
+    // pinned buffer is free to refill.
+    auto* staging = static_cast<std::byte*>(scratch.host_slices);
+    for (std::uint32_t j = 0; j < needed; ++j) std::memcpy(staging + j * slice, frames[j], slice);
+    const std::size_t bytes = static_cast<std::size_t>(params.num_query_heads) * shape.head_dim * sizeof(T);
+    void* stream = scratch.stream;
+    if (qvp_memcpy_htod(scratch.dev_slices, staging, total, stream) != QVP_OK ||
+        qvp_memcpy_htod(scratch.dq, query, bytes, stream) != QVP_OK) {
+        return refuse(std::string("upload: ") + qvp_last_error());
+    }
+    std::vector<std::uint32_t> ids(needed);
+    for (std::uint32_t j = 0; j < needed; ++j) ids[j] = j;
+    const std::uint32_t cu[2] = {0, needed};
+    const std::uint32_t lens[1] = {params.context_len};
+    qvp_decode_args args{};
+    args.query = scratch.dq;
+    args.out = scratch.dout;
+    args.kv_base = scratch.dev_slices;
+    args.block_stride = slice;
+    args.batch = scratch.staged;
+    args.kv_dtype = static_cast<std::uint32_t>(element_type_of<T>());
+    args.out_dtype = args.kv_dtype;
+    args.layer = 0;
+    args.num_layers = 1;
+    args.num_query_heads = params.num_query_heads;
+    args.num_kv_heads = shape.num_kv_heads;
+    args.head_dim = shape.head_dim;
+    args.tokens_per_block = tpb;
+    args.head_stride = layout.head_stride();
+    args.token_stride = layout.token_stride();
+    args.stream_stride = layout.stream_stride();
+    args.layer_stride = layout.layer_stride();
+    args.scale = params.scale;
+    if (qvp_pack_for_decode(scratch.staged, 1, ids.data(), cu, lens, tpb, needed, 0, &args, stream) != QVP_OK ||
+        qvp_paged_decode(&args, stream) != QVP_OK) {
+        (void)qvp_stream_synchronize(stream);
+        return refuse(std::string("decode: ") + qvp_last_error());
+    }
+    if (qvp_memcpy_dtoh(out, scratch.dout, bytes, stream) != QVP_OK || qvp_stream_synchronize(stream) != QVP_OK) {
+        return refuse(std::string("result download: ") + qvp_last_error());
+    }
+    return true;
 }
 
 }  // namespace
@@ -100,12 +243,13 @@ bool paged_attention_decode(const CacheView& view, const T* query, const PagedAt
     if (params.num_query_heads == 0 || params.num_query_heads % shape.num_kv_heads != 0) {
         return refuse("query heads do not group onto the kv heads");
     }
-    if (view.allocator->placement() != BlockPlacement::Device) {
-        return refuse("the view's frames are host memory; the decode runs on the GPU only");
-    }
     thread_local SingleScratch scratch;
     const std::size_t bytes = static_cast<std::size_t>(params.num_query_heads) * shape.head_dim * sizeof(T);
     if (!scratch.ensure(bytes, bytes)) return refuse(std::string("device staging: ") + qvp_last_error());
+    if (view.allocator->placement() != BlockPlacement::Device) {
+        return decode_host_frames(view, query, params, out, scratch);
+    }
+    scratch.batch.set_cache_element_type(element_type_of<T>());
     void* stream = view.allocator->stream();
     if (qvp_memcpy_htod(scratch.dq, query, bytes, stream) != QVP_OK) {
         return refuse(std::string("query upload: ") + qvp_last_error());
@@ -122,6 +266,7 @@ bool paged_attention_decode(const CacheView& view, const T* query, const PagedAt
 
 template bool paged_attention_decode<float>(const CacheView&, const float*, const PagedAttentionParams&, float*);
 template bool paged_attention_decode<bf16>(const CacheView&, const bf16*, const PagedAttentionParams&, bf16*);
+template bool paged_attention_decode<f16>(const CacheView&, const f16*, const PagedAttentionParams&, f16*);
 
 // ---------------------------------------------------------------------------
 

@@ -1,5 +1,5 @@
-// paged_attention_decode<T> and PagedAttentionBatch on device frames, held to
-// the reference's contract (include/qwenvl_paged/PagedAttention.h:53-127; its
+// paged_attention_decode<T> (float, bf16, f16; device frames and host frames)
+// and PagedAttentionBatch, held to the reference's contract (include/qwenvl_paged/PagedAttention.h:53-127; its
 // suite tests/PagedAttention.test.cpp:255-566 states the same refusals and the
 // same closed-form cases). Expected values are float64 textbook attention; the
 // fp32 tolerance is 1e-5 absolute, bf16 outputs are checked against the
@@ -29,7 +29,8 @@ float pat(std::uint32_t layer, KVStream s, std::uint32_t token, std::uint32_t he
     return mix_pattern({layer, s == KVStream::Key ? 0u : 1u, token, head, dim});
 }
 
-bool fill_pattern(DeviceHarness& h, SequenceId seq, std::uint32_t ctx) {
+template <typename Harness>
+bool fill_pattern(Harness& h, SequenceId seq, std::uint32_t ctx) {
     const BlockShape& s = h.layout.shape;
     for (std::uint32_t layer = 0; layer < s.num_layers; ++layer) {
         for (KVStream st : {KVStream::Key, KVStream::Value}) {
@@ -47,7 +48,8 @@ bool fill_pattern(DeviceHarness& h, SequenceId seq, std::uint32_t ctx) {
 
 // `blocks` blocks for `seq` interleaved with a spacer sequence that is then
 // released, so the frames of `seq` are not one contiguous run.
-void reserve_interleaved(DeviceHarness& h, SequenceId seq, SequenceId spacer, std::uint32_t blocks) {
+template <typename Harness>
+void reserve_interleaved(Harness& h, SequenceId seq, SequenceId spacer, std::uint32_t blocks) {
     const std::uint32_t tpb = h.layout.shape.tokens_per_block;
     ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{spacer, spacer, {}, {}}));
     for (std::uint32_t i = 0; i < blocks; ++i) {
@@ -88,13 +90,52 @@ TEST(PagedAttentionTest, RefusalsLeaveTheOutputUntouched) {
     EXPECT_FALSE(paged_attention_last_error().empty());
 }
 
-TEST(PagedAttentionTest, HostFramesAreRefused) {
-    HostHarness h(shape_of(4, 1, 1, 4), 4);
+TEST(PagedAttentionTest, HostFramesMatchTextbookAttention) {
+    // The reference's own placement: frames in host memory, scattered, two
+    // layers, grouped query heads. The layer's slices are staged to the GPU.
+    HostHarness h(shape_of(4, 2, 2, 4), 16);
     ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{1, 1, {}, {}}));
-    ASSERT_TRUE(h.cache.reserve_tokens(1, 4));
+    ASSERT_NO_FATAL_FAILURE(reserve_interleaved(h, 1, 99, 3));
+    ASSERT_TRUE(fill_pattern(h, 1, 10));
+    ASSERT_TRUE(scattered(*h.cache.cache_view(1)->block_table));
+    for (std::uint32_t heads : {2u, 4u}) {
+        for (std::uint32_t layer = 0; layer < 2; ++layer) {
+            for (std::uint32_t ctx : {1u, 4u, 5u, 10u}) {
+                std::vector<float> q(heads * 4);
+                for (std::size_t i = 0; i < q.size(); ++i) q[i] = 0.3f * float(i % 7) - 0.8f;
+                std::vector<float> out(q.size(), 0.0f);
+                ASSERT_TRUE(paged_attention_decode<float>(*h.cache.cache_view(1), q.data(),
+                                                          params(layer, heads, ctx, 0.5f), out.data()))
+                    << paged_attention_last_error();
+                const auto expect = textbook_attention(
+                    q, heads, 2, 4, ctx, 0.5f, [&](auto t, auto kh, auto d) { return pat(layer, KVStream::Key, t, kh, d); },
+                    [&](auto t, auto kh, auto d) { return pat(layer, KVStream::Value, t, kh, d); });
+                for (std::size_t i = 0; i < out.size(); ++i) {
+                    EXPECT_NEAR(out[i], expect[i], kF32Tol)
+                        << "heads " << heads << " layer " << layer << " ctx " << ctx << " element " << i;
+                }
+            }
+        }
+    }
+}
+
+TEST(PagedAttentionTest, HostFrameRefusalsLeaveTheOutputUntouched) {
+    HostHarness h(shape_of(4, 1, 1, 4), 8);
+    ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{1, 1, {}, {}}));
+    ASSERT_TRUE(h.cache.reserve_tokens(1, 8));
+    ASSERT_TRUE(fill_pattern(h, 1, 8));
     std::vector<float> q(4, 1.0f), out(4, -1.0f);
-    EXPECT_FALSE(paged_attention_decode<float>(*h.cache.cache_view(1), q.data(), params(0, 1, 4, 1.0f), out.data()));
-    EXPECT_EQ(out[0], -1.0f);
+    EXPECT_FALSE(paged_attention_decode<float>(*h.cache.cache_view(1), q.data(), params(0, 1, 9, 1.0f), out.data()))
+        << "context past the mapped blocks";
+    EXPECT_FALSE(paged_attention_decode<float>(*h.cache.cache_view(1), q.data(), params(1, 1, 4, 1.0f), out.data()))
+        << "layer outside the shape";
+    ASSERT_EQ(h.cache.swap_out_sequence(1), 2u);
+    EXPECT_FALSE(paged_attention_decode<float>(*h.cache.cache_view(1), q.data(), params(0, 1, 8, 1.0f), out.data()))
+        << "swapped-out context";
+    for (float v : out) EXPECT_EQ(v, -1.0f);
+    ASSERT_TRUE(h.cache.swap_in_sequence(1));
+    ASSERT_TRUE(paged_attention_decode<float>(*h.cache.cache_view(1), q.data(), params(0, 1, 8, 1.0f), out.data()))
+        << paged_attention_last_error();
 }
 
 TEST(PagedAttentionTest, EqualKeysGiveTheMeanOfTheValues) {
@@ -205,11 +246,14 @@ TEST(PagedAttentionTest, ForkedBranchesReadTheirOwnCopies) {
     }
 }
 
-TEST(PagedAttentionTest, Bf16HeadDim128MatchesTextbookAttention) {
-    // The Qwen2-VL-7B head shape: Hq 28 over Hkv 4, head_dim 128, 16 tokens per
-    // block, bf16 cache, runs the matrix-core kernel.
-    DeviceHarness h(shape_of(16, 1, 4, 128, 2), 64);
-    ASSERT_TRUE(h.ready());
+namespace {
+
+// The Qwen2-VL-7B head shape (Hq 28 over Hkv 4, head_dim 128, 16 tokens per
+// block) with a two-byte element type T on harness H, against float64
+// attention over the same rounded values: tolerance 2e-3 absolute plus one
+// rounding step of T (2^-8 relative for bf16, 2^-11 for f16).
+template <typename T, typename Harness>
+void two_byte_head_dim_128(Harness& h, double rel) {
     ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{1, 1, {}, {}}));
     ASSERT_NO_FATAL_FAILURE(reserve_interleaved(h, 1, 99, 20));
     const std::uint32_t ctx = 20 * 16 - 7;
@@ -218,12 +262,12 @@ TEST(PagedAttentionTest, Bf16HeadDim128MatchesTextbookAttention) {
     std::vector<std::vector<float>> K(ctx * 4), V(ctx * 4);
     for (std::uint32_t t = 0; t < ctx; ++t) {
         for (std::uint32_t kh = 0; kh < 4; ++kh) {
-            std::vector<bf16> kb(128), vb(128);
+            std::vector<T> kb(128), vb(128);
             K[t * 4 + kh].resize(128);
             V[t * 4 + kh].resize(128);
             for (std::uint32_t d = 0; d < 128; ++d) {
-                kb[d] = bf16(nd(rng));
-                vb[d] = bf16(nd(rng));
+                kb[d] = T(nd(rng));
+                vb[d] = T(nd(rng));
                 K[t * 4 + kh][d] = float(kb[d]);
                 V[t * 4 + kh][d] = float(vb[d]);
             }
@@ -231,14 +275,14 @@ TEST(PagedAttentionTest, Bf16HeadDim128MatchesTextbookAttention) {
             ASSERT_TRUE(write_head(h, 1, KVStream::Value, 0, t, kh, vb));
         }
     }
-    std::vector<bf16> qb(28 * 128), out(28 * 128);
+    std::vector<T> qb(28 * 128), out(28 * 128);
     std::vector<float> qf(qb.size());
     for (std::size_t i = 0; i < qb.size(); ++i) {
-        qb[i] = bf16(nd(rng));
+        qb[i] = T(nd(rng));
         qf[i] = float(qb[i]);
     }
     const float scale = 1.0f / std::sqrt(128.0f);
-    ASSERT_TRUE(paged_attention_decode<bf16>(*h.cache.cache_view(1), qb.data(), params(0, 28, ctx, scale), out.data()))
+    ASSERT_TRUE(paged_attention_decode<T>(*h.cache.cache_view(1), qb.data(), params(0, 28, ctx, scale), out.data()))
         << paged_attention_last_error();
     const auto expect = textbook_attention(
         qf, 28, 4, 128, ctx, scale, [&](auto t, auto kh, auto d) { return double(K[t * 4 + kh][d]); },
@@ -246,11 +290,38 @@ TEST(PagedAttentionTest, Bf16HeadDim128MatchesTextbookAttention) {
     double worst = 0.0;
     for (std::size_t i = 0; i < out.size(); ++i) {
         const double got = float(out[i]);
-        const double tol = 2e-3 + std::fabs(expect[i]) * (1.0 / 256.0);
+        const double tol = 2e-3 + std::fabs(expect[i]) * rel;
         worst = std::max(worst, std::fabs(got - expect[i]) - tol);
         ASSERT_NEAR(got, expect[i], tol) << "element " << i;
     }
     EXPECT_LE(worst, 0.0);
+}
+
+}  // namespace
+
+TEST(PagedAttentionTest, Bf16HeadDim128MatchesTextbookAttention) {
+    // Device frames: the matrix-core kernel over the pool.
+    DeviceHarness h(shape_of(16, 1, 4, 128, 2), 64);
+    ASSERT_TRUE(h.ready());
+    ASSERT_NO_FATAL_FAILURE(two_byte_head_dim_128<bf16>(h, 1.0 / 256.0));
+}
+
+TEST(PagedAttentionTest, Bf16HeadDim128OnHostFramesMatchesTextbookAttention) {
+    // Host frames: the same kernel over the staged layer slices.
+    HostHarness h(shape_of(16, 2, 4, 128, 2), 64);
+    ASSERT_NO_FATAL_FAILURE(two_byte_head_dim_128<bf16>(h, 1.0 / 256.0));
+}
+
+TEST(PagedAttentionTest, F16HeadDim128MatchesTextbookAttention) {
+    // An IEEE half cache read as f16 (the element type names the format).
+    DeviceHarness h(shape_of(16, 1, 4, 128, 2), 64);
+    ASSERT_TRUE(h.ready());
+    ASSERT_NO_FATAL_FAILURE(two_byte_head_dim_128<f16>(h, 1.0 / 2048.0));
+}
+
+TEST(PagedAttentionTest, F16HeadDim128OnHostFramesMatchesTextbookAttention) {
+    HostHarness h(shape_of(16, 1, 4, 128, 2), 64);
+    ASSERT_NO_FATAL_FAILURE(two_byte_head_dim_128<f16>(h, 1.0 / 2048.0));
 }
 
 TEST(PagedAttentionBatchTest, OneLaunchDecodesEveryViewLikeTheSingleCalls) {

@@ -1,5 +1,6 @@
-"""The copy-on-write (config4) and continuous-batching (config5)
-configurations on the GPU at their full sizes, through their C++ drivers
+"""The long-context multimodal (config3), copy-on-write (config4) and
+continuous-batching (config5) configurations on the GPU at their full sizes,
+through their C++ drivers
 (qwenvl-paged_amd/host/bench): the device allocator's decisions and bytes
 equal the host allocator's, copied frames equal their sources, sampled
 decodes match float64 attention, the 200-request trace writes the event log
@@ -76,6 +77,23 @@ def test_continuous_batching_trace_full_size_matches_the_reference(tmp_path, eng
     assert r["swapped_out_blocks"] > 0 and r["swapped_in_blocks"] > 0
     got, expected = log.read_text(), _reference_config5_log()
     assert got == expected, _first_difference(got, expected)
+
+
+@pytest.mark.gpu
+def test_long_context_multimodal_configuration_full_size():
+    """config3 as specified, through the host API: 32 Qwen2-VL-72B-shaped
+    sequences with contexts on [8192, 32768], each created with an image span
+    over its first quarter (MultimodalSpan + Image2D positional span on a
+    patch grid, then a Text1D span). metadata() returns what was given, the
+    M-RoPE positions of every token equal the closed form, the decode over the
+    tagged sequences equals the decode over untagged forks bit for bit, and
+    sampled heads match float64 attention."""
+    r = run("config3_bench")
+    assert r["sequences"] == 32 and r["image_tokens"] > 0
+    assert r["metadata_roundtrip"] and r["positions_match_closed_form"]
+    assert r["tagged_equals_untagged_bitwise"]
+    assert r["decode_within_tolerance"] and r["checked_elements"] == 4 * 8 * 128
+    assert r["plan"]["query_group"] == 8
 
 
 @pytest.mark.gpu

@@ -19,7 +19,7 @@ SUITES = [
     "CacheViewStaticTest", "CacheViewTest", "MemoryAllocatorTest", "MemoryAllocatorSwapTest",
     "MemoryAllocatorEvictionTest", "HostSwapBackendTest", "KVCacheManagerTest", "KVCacheSwapTest",
     "KVCacheSwapSingleFrameTest", "SchedulerTest", "SchedulerPressureTest", "SchedulerWatermarkTest",
-    "SchedulerTraceTest",
+    "SchedulerTraceTest", "ElementTypeTest",
 ]
 
 
