@@ -117,7 +117,7 @@ def cpu_baseline(w: W.Workload, image: np.ndarray, query: np.ndarray, reps: int)
 
 
 # The decode kernel's sources: a traffic profile holds for the build of these.
-KERNEL_SOURCES = ["decode_mfma.hip", "mfma_tile.h", "decode_common.h", "common.h", "batch.h"]
+KERNEL_SOURCES = ["decode_mfma.hip", "mfma_tile.h", "valu_tile.h", "decode_common.h", "common.h", "batch.h"]
 
 
 def kernel_source_digest() -> str:
@@ -571,6 +571,59 @@ def fp32_bench(steps: int, warmup: int, cpu_reps: int, with_cpu: bool) -> int:
     return 0
 
 
+def tiles_bench(steps: int, warmup: int, pools_n: int) -> int:
+    """Matrix-core against vector-ALU tiles of the persistent bf16 decode on
+    the config2 batch (64 contexts U[512, 4096], Hkv 4, D 128, block 16) with
+    GQA groups of 1, 2 and 7 query heads per kv head (Hq 4, 8, 28; vector
+    tiles take groups of at most 2). One line: per (group, engine) the event-
+    timed kernel average over `steps` launches rotating `pools_n` pool copies."""
+    c2 = W.config2()
+    cases = []
+    image = None
+    for hq in (4, 8, 28):
+        w = W.custom(list(c2.context_lens), hq, 4, 128, seed=2, spare=0.1)
+        if image is None:
+            image = w.pool_image()
+        pools = []
+        for _ in range(max(1, pools_n)):
+            p = qvp.BlockPool(w.num_pool_blocks, w.block_bytes)
+            p.upload_all(image)
+            pools.append(p)
+        q = qvp.DeviceBuffer.from_array(w.query())
+        out = qvp.DeviceBuffer(w.num_seqs * hq * 128 * 2)
+        stream = qvp.Stream()
+        batch = qvp.Batch()
+        batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks, 512, stream)
+        ws = qvp.DeviceBuffer(batch.workspace_bytes(hq, 128))
+        engines = [qvp.TILE_MATRIX] + ([qvp.TILE_VECTOR] if hq // 4 <= 2 else [])
+        for engine in engines:
+            args = [qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=p.base, block_stride=p.stride, batch=batch,
+                                    kv_dtype=qvp.DTYPE_BF16, out_dtype=qvp.DTYPE_BF16, layer=0, num_layers=1,
+                                    num_query_heads=hq, num_kv_heads=4, head_dim=128, tokens_per_block=16,
+                                    scale=w.scale, workspace=ws.ptr, workspace_bytes=ws.nbytes, tile_engine=engine)
+                    for p in pools]
+            for i in range(warmup):
+                qvp.paged_decode(args[i % len(args)], stream)
+            stream.synchronize()
+            e0, e1 = qvp.Event(), qvp.Event()
+            e0.record(stream)
+            for i in range(steps):
+                qvp.paged_decode(args[i % len(args)], stream)
+            e1.record(stream)
+            stream.synchronize()
+            ms = e0.elapsed_ms(e1) / steps
+            kv = w.kv_bytes()
+            plan = batch.decode_plan()
+            cases.append({"query_group": hq // 4, "num_query_heads": hq, "engine": plan["tile_engine"],
+                          "kernel_us": round(ms * 1e3, 2), "kv_GBps": round(kv / (ms * 1e-3) / 1e9, 1),
+                          "frac_of_8TBps": round(kv / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                          "kv_heads_per_segment": plan["kv_heads_per_segment"]})
+            print(json.dumps(cases[-1]), flush=True)
+    print(json.dumps({"mode": "tiles", "workload": "config2 contexts (B=64, ctx U[512,4096]), Hkv 4, D 128, bf16",
+                      "steps": steps, "cases": cases}))
+    return 0
+
+
 def append_bench(steps: int, warmup: int) -> int:
     w = W.config2()
     cases = [append_case("config2 step, one layer", w, 1, 0, 1, steps, warmup),
@@ -599,6 +652,8 @@ def main() -> int:
     ap.add_argument("--swap", action="store_true", help="time swap-out / swap-in of whole 7B frames")
     ap.add_argument("--copy", action="store_true", help="time copy_blocks of 128 frame pairs at 7B frame sizes")
     ap.add_argument("--fp32", action="store_true", help="time the config2 batch with an fp32 cache")
+    ap.add_argument("--tiles", action="store_true",
+                    help="time matrix-core against vector-ALU decode tiles at GQA groups 1, 2 and 7")
     ap.add_argument("--torch-sdpa", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="instead of the decode, run the plain block-copy kernel over 256 MiB (known bytes, "
@@ -624,6 +679,8 @@ def main() -> int:
         return swap_bench(args.steps, args.warmup)
     if args.fp32:
         return fp32_bench(args.steps, args.warmup, args.cpu_reps, not args.no_cpu)
+    if args.tiles:
+        return tiles_bench(args.steps, args.warmup, args.pools)
     if args.torch_sdpa:
         print(json.dumps({"ms": torch_sdpa_ms(4, 2048, 28, 4, 128, args.steps, args.warmup)}))
         return 0

@@ -238,6 +238,16 @@ int qvp_batch_view(const qvp_batch* batch, qvp_packed_view* view);
  * element offset layer * layer_stride + {0 | stream_stride} +
  * (t % tpb) * token_stride + g * head_stride (CacheLayout.cpp:25-38); head_dim
  * elements are contiguous. */
+/* Arithmetic of the persistent bf16 decode's 32-token tiles. No reference
+ * counterpart (the reference's decode is a scalar loop, PagedAttention.h:
+ * 94-124): both engines read each K/V byte once per GQA group. */
+typedef enum qvp_tile_engine {
+    QVP_TILE_AUTO = 0,    /* the library's choice for the query group */
+    QVP_TILE_MATRIX = 1,  /* matrix cores: v_mfma_f32_16x16x32_bf16, the group in the columns */
+    QVP_TILE_VECTOR = 2   /* vector ALUs: the group folded into each lane's fp32 dot
+                             products (groups of at most 2; refused otherwise) */
+} qvp_tile_engine;
+
 typedef struct qvp_decode_args {
     const void* query;          /* device, [num_seqs][num_query_heads][head_dim], kv_dtype */
     void* out;                  /* device, [num_seqs][num_query_heads][head_dim], out_dtype */
@@ -262,6 +272,8 @@ typedef struct qvp_decode_args {
     void* split_event;          /* optional hipEvent_t recorded on `stream` after the
                                    split kernel and before the merge kernel (lets a
                                    caller time the two kernels apart), or NULL */
+    uint32_t tile_engine;       /* qvp_tile_engine of the persistent bf16 kernel;
+                                   0 (automatic) for the library's choice */
 } qvp_decode_args;
 
 /* Bytes of workspace qvp_paged_decode needs for this batch and head shape. */
@@ -329,6 +341,7 @@ typedef struct qvp_decode_plan {
                                    ranges are cut by cost, not by a partition size) */
     uint32_t deferred_results;  /* MFMA: 1 when piece results wait in LDS until a range ends */
     uint32_t query_group;       /* query heads per kv head of that decode */
+    uint32_t tile_engine;       /* MFMA kernel: the qvp_tile_engine that ran (1 or 2) */
 } qvp_decode_plan;
 
 int qvp_decode_plan_info(const qvp_batch* batch, qvp_decode_plan* plan);

@@ -53,6 +53,7 @@ struct qvp_schedule {
     uint32_t num_slots{0};
     uint32_t max_partial_pieces_per_wg{0};
     uint32_t hps{1};  // kv heads per segment
+    uint32_t tile_group{0};  // DecodeGeometry::tile_group the LDS budget was planned for
     std::vector<double> weights;  // streaming weight per kv-head group the ranges were cut for
     bool defer{false};            // piece results held in LDS until a range is done
     uint32_t lds_bytes{0};        // dynamic LDS per workgroup for them

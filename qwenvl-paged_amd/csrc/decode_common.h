@@ -31,6 +31,9 @@ struct DecodeGeometry {
     uint32_t group;
     uint32_t head_dim;
     float scale_log2;       // scale * log2(e)
+    // Persistent kernel: 0 for matrix-core tiles, else vector tiles for query
+    // groups up to this bound (1, 2, 4 or 8).
+    uint32_t tile_group;
 };
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -63,6 +66,12 @@ bool f32_grouped_supported(const DecodeGeometry& g, uint32_t kv_dtype, uint32_t 
                            uintptr_t kv_base_addr);
 int launch_f32_grouped_decode(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t out_dtype, void* out,
                               void* workspace, hipEvent_t split_event, hipStream_t stream);
+
+// Vector tiles of the persistent kernel take query groups up to this size;
+// the automatic choice uses them for groups up to kVectorTilesUpToGroup (0:
+// never, matrix-core tiles for every group).
+constexpr uint32_t kVectorTileMaxGroup = 2;
+constexpr uint32_t kVectorTilesUpToGroup = 0;
 
 // Validates decode arguments against a packed view (every refusal of
 // qvp_paged_decode) and fills the kernels' geometry. *supported_mfma tells

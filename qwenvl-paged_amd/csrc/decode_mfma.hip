@@ -48,6 +48,7 @@
 //   keeps the weights at about 2^-16 relative error. C register r of PV MFMA n
 //   in lane (c, j) is O[head c][dim 32j + 8r + n].
 #include "mfma_tile.h"
+#include "valu_tile.h"
 
 #include <algorithm>
 #include <mutex>
@@ -199,8 +200,10 @@ __device__ inline void load_tile(const DecodeGeometry& p, const TileRef& r, int 
     }
 }
 
-template <typename OutT>
+// kVG = 0: matrix-core tiles; 1, 2: vector tiles for query groups up to kVG.
+template <typename OutT, int kVG>
 __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(DecodeGeometry p, MfmaArgs a) {
+    __shared__ VectorTileLds<kVG> vt;
     __shared__ float sm_m[kWaves][16];
     __shared__ float sm_l[kWaves][16];
     __shared__ float sm_o[kWaves][16][kRowPad];
@@ -310,30 +313,74 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         for (int i = 0; i < 4; ++i) qop[i] = qnext[i];
         if (pi + 1 < pe) load_query(pi + 1, qnext);
 
-        floatx4 o[8];
+        if constexpr (kVG == 0) {
+            floatx4 o[8];
 #pragma unroll
-        for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-        float m_run = -INFINITY;
-        float l_run = 0.f;
+            for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+            float m_run = -INFINITY;
+            float l_run = 0.f;
 
-        for (int t = d.t0 + tlane; t < d.t1; t += tl) {
-            KvTile cur = nxt;
-            if (has2) load_tile(p, r2, c, j, nxt);
-            has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
-            if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
-            compute_tile(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
-        }
+            for (int t = d.t0 + tlane; t < d.t1; t += tl) {
+                KvTile cur = nxt;
+                if (has2) load_tile(p, r2, c, j, nxt);
+                has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
+                if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
+                compute_tile(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
+            }
 
-        // This wave's state for (piece, head g) goes to LDS in row layout.
-        l_run = sum_over_j(l_run);
-        if (j == 0) {
-            sm_m[wave][c] = m_run;
-            sm_l[wave][c] = l_run;
+            // This wave's state for (piece, head g) goes to LDS in row layout.
+            l_run = sum_over_j(l_run);
+            if (j == 0) {
+                sm_m[wave][c] = m_run;
+                sm_l[wave][c] = l_run;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int n = 0; n < 8; ++n) sm_o[wave][c][32 * j + 8 * r + n] = o[n][r];
+        } else {
+            // The piece's query to LDS as [dim][head]; every wave of this kv
+            // head writes the same values and reads only what it wrote (the
+            // previous piece's reads ended at its closing barrier).
+            stage_query<kVG>(vt.q[hl], qop, c, j);
+            __builtin_amdgcn_wave_barrier();
+            float o[kVG][8];
+            float m_run[kVG];
+            float l_part[kVG];
+#pragma unroll
+            for (int h = 0; h < kVG; ++h) {
+                m_run[h] = -INFINITY;
+                l_part[h] = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[h][e] = 0.f;
+            }
+
+            for (int t = d.t0 + tlane; t < d.t1; t += tl) {
+                KvTile cur = nxt;
+                if (has2) load_tile(p, r2, c, j, nxt);
+                has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
+                if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
+                compute_tile_vector<kVG>(cur, vt.q[hl], vt.p[wave], t * kTileTokens, ctx - 1, ctx, p.scale_log2, c,
+                                         j, m_run, l_part, o);
+            }
+
+            // The same row layout as the matrix-core state: the running sum
+            // adds the 16 lanes c (the j rows agree), the outputs the four
+            // j lanes' token classes.
+#pragma unroll
+            for (int h = 0; h < kVG; ++h) {
+                const float lsum = sum_over_c(l_part[h]);
+                if (lane == 0) {
+                    sm_m[wave][h] = m_run[h];
+                    sm_l[wave][h] = lsum;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float ov = sum_over_j(o[h][e]);
+                    if (j == 0) sm_o[wave][h][8 * c + e] = ov;
+                }
+            }
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int n = 0; n < 8; ++n) sm_o[wave][c][32 * j + 8 * r + n] = o[n][r];
 
         have_partial = have_partial || d.slot >= 0;
         if (hps == 1) {
@@ -526,6 +573,32 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     }
 }
 
+// The kernel instantiation for an output type and a tile engine.
+template <typename OutT>
+const void* kernel_for_group(uint32_t tile_group) {
+    switch (tile_group) {
+        case 0: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0>);
+        case 1: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 1>);
+        default: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 2>);
+    }
+}
+
+const void* decode_kernel(uint32_t out_dtype, uint32_t tile_group) {
+    switch (out_dtype) {
+        case QVP_DTYPE_F32: return kernel_for_group<float>(tile_group);
+        case QVP_DTYPE_BF16: return kernel_for_group<uint16_t>(tile_group);
+        default: return kernel_for_group<_Float16>(tile_group);
+    }
+}
+
+constexpr uint32_t kTileGroups[] = {0, 1, 2};
+
+// Static LDS of an instantiation (the vector tiles add their query and
+// weight arrays).
+constexpr uint32_t static_lds_bytes(uint32_t tile_group) {
+    return kStaticLdsBytes + vector_tile_lds_bytes(static_cast<int>(tile_group));
+}
+
 // Resident workgroups per device (one per CU), cached per device ordinal.
 std::mutex g_dev_mutex;
 std::vector<uint32_t> g_dev_wgs;
@@ -539,13 +612,12 @@ int device_max_wgs(uint32_t* wgs) {
         // The kernels may take all of the CU's LDS (deferred piece results
         // beside the static arrays); allowed once per device, before any
         // launch (and so before any graph capture).
-        const int dyn = static_cast<int>(kMaxLdsBytes - kStaticLdsBytes);
-        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_persistent<float>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
-        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_persistent<uint16_t>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
-        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_mfma_persistent<_Float16>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+        for (uint32_t dt : {QVP_DTYPE_F32, QVP_DTYPE_BF16, QVP_DTYPE_F16}) {
+            for (uint32_t tg : kTileGroups) {
+                const int dyn = static_cast<int>(kMaxLdsBytes - static_lds_bytes(tg));
+                QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, tg), hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+            }
+        }
         int cus = 0;
         QVP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         g_dev_wgs[dev] = static_cast<uint32_t>(std::max(1, cus) * kWgsPerCu);
@@ -669,7 +741,7 @@ bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_
 bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g) {
     const qvp_schedule& s = batch->sched;
     if (!s.valid || s.pack_generation != batch->generation || s.num_kv_heads != g.num_kv_heads ||
-        s.group != g.group) {
+        s.group != g.group || s.tile_group != g.tile_group) {
         return false;
     }
     uint32_t max_wgs = 0;
@@ -814,7 +886,7 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
         np_max = std::max<uint32_t>(np_max, static_cast<uint32_t>(wg_begin[w + 1] - wg_begin[w]));
     }
     const uint64_t def_bytes = static_cast<uint64_t>(np_max) * hps * g.group * (kD + 2) * sizeof(float);
-    s.defer = def_bytes + kStaticLdsBytes <= kMaxLdsBytes;
+    s.defer = def_bytes + static_lds_bytes(g.tile_group) <= kMaxLdsBytes;
     s.lds_bytes = s.defer ? static_cast<uint32_t>(def_bytes) : 0u;
 
     s.off_wg_begin = 0;
@@ -827,6 +899,7 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     s.pack_generation = in.generation;
     s.num_kv_heads = num_kv_heads;
     s.group = g.group;
+    s.tile_group = g.tile_group;
     s.max_wgs = max_wgs;
     s.weights = weights;
     s.num_wgs = Wn;
@@ -962,20 +1035,13 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     a.out = out;
     a.hps = static_cast<int>(s.hps);
     a.defer = s.defer ? 1 : 0;
-    const dim3 grid(s.num_wgs);
-    const size_t lds = s.lds_bytes;
-    switch (out_dtype) {
-        case QVP_DTYPE_F32:
-            hipLaunchKernelGGL(decode_mfma_persistent<float>, grid, dim3(kThreads), lds, stream, g, a);
-            break;
-        case QVP_DTYPE_BF16:
-            hipLaunchKernelGGL(decode_mfma_persistent<uint16_t>, grid, dim3(kThreads), lds, stream, g, a);
-            break;
-        default:
-            hipLaunchKernelGGL(decode_mfma_persistent<_Float16>, grid, dim3(kThreads), lds, stream, g, a);
-            break;
+    if (s.tile_group != g.tile_group) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "the batch's schedule was planned for another tile engine");
     }
-    QVP_HIP(hipGetLastError());
+    DecodeGeometry gk = g;
+    void* kargs[] = {&gk, &a};
+    QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs), dim3(kThreads), kargs,
+                            s.lds_bytes, stream));
     // The merge runs inside the kernel; the event still marks the split/merge
     // boundary for callers that time the two phases.
     if (split_event != nullptr) QVP_HIP(hipEventRecord(split_event, stream));

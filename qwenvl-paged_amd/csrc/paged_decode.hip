@@ -155,6 +155,18 @@ int decode_geometry(const qvp_decode_args* a, const qvp_packed_view& v, DecodeGe
     g.scale_log2 = a->scale * kLog2e;
     *supported_mfma = mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
                                      reinterpret_cast<uintptr_t>(a->kv_base));
+    if (a->tile_engine > QVP_TILE_VECTOR) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "unknown tile engine %u", a->tile_engine);
+    }
+    if (*supported_mfma) {
+        const bool vector = a->tile_engine == QVP_TILE_VECTOR ||
+                            (a->tile_engine == QVP_TILE_AUTO && g.group <= kVectorTilesUpToGroup);
+        if (vector && g.group > kVectorTileMaxGroup) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "vector tiles take query groups of at most %u (group %u)",
+                        kVectorTileMaxGroup, g.group);
+        }
+        g.tile_group = vector ? (g.group <= 1 ? 1u : 2u) : 0u;
+    }
     return QVP_OK;
 }
 
@@ -230,6 +242,7 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         plan.slots = sc.num_slots;
         plan.kv_heads_per_segment = sc.hps;
         plan.deferred_results = sc.defer ? 1u : 0u;
+        plan.tile_engine = g.tile_group != 0 ? QVP_TILE_VECTOR : QVP_TILE_MATRIX;
     } else {
         const bool f32 = qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens,
                                                     reinterpret_cast<uintptr_t>(a->query),

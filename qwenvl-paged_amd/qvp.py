@@ -79,6 +79,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", c_void_p),
         ("workspace_bytes", c_uint64),
         ("split_event", c_void_p),
+        ("tile_engine", c_uint32),
     ]
 
 
@@ -137,10 +138,16 @@ class DecodePlan(ctypes.Structure):
         ("split_tokens", c_uint32),
         ("deferred_results", c_uint32),
         ("query_group", c_uint32),
+        ("tile_engine", c_uint32),
     ]
 
 
 DECODE_KERNELS = {0: "none", 1: "mfma", 2: "f32_grouped", 3: "generic"}
+# qvp_tile_engine: arithmetic of the persistent bf16 kernel's tiles.
+TILE_AUTO = 0
+TILE_MATRIX = 1
+TILE_VECTOR = 2
+TILE_ENGINES = {0: "none", 1: "matrix", 2: "vector"}
 
 _u32p = POINTER(c_uint32)
 _u64p = POINTER(c_uint64)
@@ -515,6 +522,7 @@ class Batch:
         check(load().qvp_decode_plan_info(self.handle, byref(p)))
         d = {name: int(getattr(p, name)) for name, _ in DecodePlan._fields_}
         d["kernel"] = DECODE_KERNELS.get(d["kernel"], str(d["kernel"]))
+        d["tile_engine"] = TILE_ENGINES.get(d["tile_engine"], str(d["tile_engine"]))
         return d
 
     def workspace_bytes(self, num_query_heads: int, head_dim: int) -> int:
@@ -623,12 +631,13 @@ def layout_strides(tokens_per_block: int, num_layers: int, num_kv_heads: int, he
 def decode_args(*, query: int, out: int, kv_base: int, block_stride: int, batch: Batch, kv_dtype: int,
                 out_dtype: int, layer: int, num_layers: int, num_query_heads: int, num_kv_heads: int,
                 head_dim: int, tokens_per_block: int, scale: float, strides: dict | None = None,
-                workspace: int = 0, workspace_bytes: int = 0, split_event: "Event | None" = None) -> DecodeArgs:
+                workspace: int = 0, workspace_bytes: int = 0, split_event: "Event | None" = None,
+                tile_engine: int = TILE_AUTO) -> DecodeArgs:
     s = strides or layout_strides(tokens_per_block, num_layers, num_kv_heads, head_dim)
     return DecodeArgs(query, out, kv_base, block_stride, batch.handle, kv_dtype, out_dtype, layer, num_layers,
                       num_query_heads, num_kv_heads, head_dim, tokens_per_block, s["head_stride"],
                       s["token_stride"], s["stream_stride"], s["layer_stride"], scale, workspace or None,
-                      workspace_bytes, split_event.handle if split_event is not None else None)
+                      workspace_bytes, split_event.handle if split_event is not None else None, tile_engine)
 
 
 def paged_decode(args: DecodeArgs, stream=None) -> None:

@@ -60,7 +60,7 @@ class GpuRun:
         self.batch = qvp.Batch()
 
     def decode(self, out_dtype: int | None = None, split_tokens: int | None = None, workspace=None,
-               stream=None) -> np.ndarray:
+               stream=None, tile_engine: int = qvp.TILE_AUTO) -> np.ndarray:
         w = self.w
         od = w.kv_dtype if out_dtype is None else out_dtype
         self.batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks,
@@ -74,7 +74,7 @@ class GpuRun:
                                num_layers=w.num_layers, num_query_heads=w.num_query_heads,
                                num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
                                tokens_per_block=w.tokens_per_block, scale=w.scale, strides=w.strides,
-                               workspace=ws_ptr, workspace_bytes=ws_bytes)
+                               workspace=ws_ptr, workspace_bytes=ws_bytes, tile_engine=tile_engine)
         qvp.paged_decode(args, stream)
         np_dtype = np.float32 if od == qvp.DTYPE_F32 else np.uint16
         return out.download(np_dtype, (w.num_seqs, w.num_query_heads, w.head_dim), stream)
