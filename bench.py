@@ -323,7 +323,7 @@ def append_case(name: str, w: W.Workload, num_layers: int, first_layer: int, lay
 PEAK_BF16_TFLOPS = 2500.0
 
 
-def prefill_bench(steps: int, warmup: int) -> int:
+def prefill_bench(steps: int, warmup: int, with_torch: bool = True) -> int:
     """Causal prefill of B prompts (all positions new) at the Qwen2-VL-7B layer
     shape. Useful flops: 4 * Hq * D * sum over positions of (p + 1) (QK^T and
     PV, causal)."""
@@ -360,13 +360,15 @@ def prefill_bench(steps: int, warmup: int) -> int:
     tflops = flops / (ms * 1e-3) / 1e12
     # torch carries its own HIP runtime, which does not open the device next
     # to libqvp's in one process: the comparison runs in a child process.
-    child = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--torch-sdpa", "--steps", str(steps),
-                            "--warmup", str(warmup)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
-                           timeout=300)
-    results = [ln for ln in child.stdout.splitlines() if ln.startswith('{"ms"')]
-    sdpa_ms = json.loads(results[-1])["ms"] if child.returncode == 0 and results else None
-    if sdpa_ms is None:
-        print(f"torch sdpa child failed ({child.returncode}): {child.stderr[-400:]}", file=sys.stderr)
+    sdpa_ms = None
+    if with_torch:
+        child = subprocess.run([sys.executable, str(Path(__file__).resolve()), "--torch-sdpa", "--steps", str(steps),
+                                "--warmup", str(warmup)], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True,
+                               timeout=300)
+        results = [ln for ln in child.stdout.splitlines() if ln.startswith('{"ms"')]
+        sdpa_ms = json.loads(results[-1])["ms"] if child.returncode == 0 and results else None
+        if sdpa_ms is None:
+            print(f"torch sdpa child failed ({child.returncode}): {child.stderr[-400:]}", file=sys.stderr)
     print(json.dumps({"mode": "prefill", "kernel": "prefill_mfma", "workload": "4 x 2048-token prompts, Hq28/Hkv4/D128 "
                       "bf16, block 16, one layer", "steps": steps, "ms_per_prefill": round(ms, 4),
                       "useful_flops": flops, "tokens_per_s": round(total / (ms * 1e-3), 1),
@@ -648,6 +650,7 @@ def main() -> int:
     ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
     ap.add_argument("--append", action="store_true", help="time the K/V append of one config2 step")
     ap.add_argument("--prefill", action="store_true", help="time the causal prefill of 4 x 2048-token prompts")
+    ap.add_argument("--no-torch", action="store_true", help="--prefill without the torch SDPA comparison")
     ap.add_argument("--mrope", action="store_true", help="time M-RoPE position materialisation")
     ap.add_argument("--swap", action="store_true", help="time swap-out / swap-in of whole 7B frames")
     ap.add_argument("--copy", action="store_true", help="time copy_blocks of 128 frame pairs at 7B frame sizes")
@@ -672,7 +675,7 @@ def main() -> int:
     if args.append:
         return append_bench(args.steps, args.warmup)
     if args.prefill:
-        return prefill_bench(args.steps, args.warmup)
+        return prefill_bench(args.steps, args.warmup, not args.no_torch)
     if args.mrope:
         return mrope_bench(args.steps, args.warmup, not args.no_cpu)
     if args.swap:

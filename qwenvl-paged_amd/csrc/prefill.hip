@@ -206,73 +206,85 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     // VALU work of the other; tile t + 2 travels from registers to the LDS
     // buffer tile t used. Tiles from t_diag on reach the block's first
     // position and take the causal mask; the loop is split there so the
-    // others carry no mask code. Both query heads run in one block (a wave
-    // with one head computes it twice, writing once).
+    // others carry no mask code. A wave with two query heads runs both in one
+    // block; a wave with one (the last wave of an odd group) runs a
+    // one-head copy of the loop, leaving its SIMD's issue slots to the
+    // other workgroup's wave there.
     const int t_diag = (p0 + 1) / kTileTokens;
     const int last_tile = ntiles - 1;
-    u32x4 r0[4];
-    u32x4 kf[2][4], vf[8];
-    floatx4 sa[2], sb[2];
-    u32x4 ahi, alo, bhi, blo;
-    float alpha_a, alpha_b;
-    load_tile_regs(0, r0);
-    store_tile(0, r0, 0);
-    load_tile_regs(min(1, last_tile), r0);
-    __syncthreads();
-    read_k(0, kf);
-    read_v(0, vf);
-    qk_tile(kf, qa, sa);
-    qk_tile(kf, qb, sb);
-    if (t_diag == 0) mask2(sa, sb, 0);
-    softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
-    softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
-    store_tile(1, r0, min(1, last_tile));
-    __syncthreads();
-    // O is rescaled for tile t's maximum just before PV(t) accumulates into
-    // it, skipped when no column's maximum moved (the factor is then exactly
-    // 1); the branch sits at the top of the iteration, outside the block above.
-    auto rescale = [&]() {
-        if (__builtin_amdgcn_ballot_w64(alpha_a != 1.0f || alpha_b != 1.0f) != 0) {
-#pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                oa[n] *= alpha_a;
-                ob[n] *= alpha_b;
-            }
-        }
-    };
-    auto step = [&](int t, auto masked) {
-        const int nb = (t + 1) & 1;
-        rescale();
-        // Tile t + 2; near the end the last tile again, which lands in a
-        // buffer no later iteration reads.
-        load_tile_regs(min(t + 2, last_tile), r0);
-        read_k(nb, kf);
-        qk_tile(kf, qa, sa);
-        qk_tile(kf, qb, sb);
-        pv_tile(vf, ahi, alo, oa);
-        pv_tile(vf, bhi, blo, ob);
-        read_v(nb, vf);
-        if constexpr (decltype(masked)::value) mask2(sa, sb, t + 1);
-        softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
-        softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
-        // Schedule: the QK MFMAs first, then the PV MFMAs spread over the
-        // softmax's VALU work.
-#pragma unroll
-        for (int k = 0; k < 16; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-#pragma unroll
-        for (int k = 0; k < 32; ++k) {
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        }
-        store_tile(t & 1, r0, min(t + 2, last_tile));
+    auto run = [&](auto two_heads) {
+        constexpr bool kTwo = decltype(two_heads)::value;
+        u32x4 r0[4];
+        u32x4 kf[2][4], vf[8];
+        floatx4 sa[2], sb[2];
+        u32x4 ahi, alo, bhi, blo;
+        float alpha_a, alpha_b = 1.0f;
+        load_tile_regs(0, r0);
+        store_tile(0, r0, 0);
+        load_tile_regs(min(1, last_tile), r0);
         __syncthreads();
+        read_k(0, kf);
+        read_v(0, vf);
+        qk_tile(kf, qa, sa);
+        if constexpr (kTwo) qk_tile(kf, qb, sb);
+        if (t_diag == 0) mask2(sa, sb, 0);
+        softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
+        if constexpr (kTwo) softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
+        store_tile(1, r0, min(1, last_tile));
+        __syncthreads();
+        // O is rescaled for tile t's maximum just before PV(t) accumulates
+        // into it, skipped when no column's maximum moved (the factor is then
+        // exactly 1); the branch sits at the top of the iteration, outside
+        // the block above.
+        auto rescale = [&]() {
+            if (__builtin_amdgcn_ballot_w64(alpha_a != 1.0f || alpha_b != 1.0f) != 0) {
+#pragma unroll
+                for (int n = 0; n < 8; ++n) {
+                    oa[n] *= alpha_a;
+                    if constexpr (kTwo) ob[n] *= alpha_b;
+                }
+            }
+        };
+        auto step = [&](int t, auto masked) {
+            const int nb = (t + 1) & 1;
+            rescale();
+            // Tile t + 2; near the end the last tile again, which lands in a
+            // buffer no later iteration reads.
+            load_tile_regs(min(t + 2, last_tile), r0);
+            read_k(nb, kf);
+            qk_tile(kf, qa, sa);
+            if constexpr (kTwo) qk_tile(kf, qb, sb);
+            pv_tile(vf, ahi, alo, oa);
+            if constexpr (kTwo) pv_tile(vf, bhi, blo, ob);
+            read_v(nb, vf);
+            if constexpr (decltype(masked)::value) mask2(sa, sb, t + 1);
+            softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
+            if constexpr (kTwo) softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
+            // Schedule: the QK MFMAs first, then the PV MFMAs spread over the
+            // softmax's VALU work.
+            constexpr int kHeads = kTwo ? 2 : 1;
+#pragma unroll
+            for (int k = 0; k < 8 * kHeads; ++k) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+            for (int k = 0; k < 16 * kHeads; ++k) {
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            }
+            store_tile(t & 1, r0, min(t + 2, last_tile));
+            __syncthreads();
+        };
+        int t = 0;
+        for (; t + 1 < min(t_diag, ntiles); ++t) step(t, std::false_type{});
+        for (; t + 1 < ntiles; ++t) step(t, std::true_type{});
+        rescale();
+        pv_tile(vf, ahi, alo, oa);
+        if constexpr (kTwo) pv_tile(vf, bhi, blo, ob);
     };
-    int t = 0;
-    for (; t + 1 < min(t_diag, ntiles); ++t) step(t, std::false_type{});
-    for (; t + 1 < ntiles; ++t) step(t, std::true_type{});
-    rescale();
-    pv_tile(vf, ahi, alo, oa);
-    pv_tile(vf, bhi, blo, ob);
+    if (has_b) {
+        run(std::true_type{});
+    } else {
+        run(std::false_type{});
+    }
 
     OutT* out = static_cast<OutT*>(out_ptr);
     auto write = [&](int hq, const floatx4 (&o)[8], float l) {
