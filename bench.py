@@ -163,8 +163,8 @@ def write_traffic(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_writ
         int(((w.context_lens.astype(np.int64) + 15) // 16).sum()) * 4 + w.num_seqs * 4
     fetch = per_dispatch(fetch_csv, "FETCH_SIZE", "decode_mfma_persistent")
     write = per_dispatch(write_csv, "WRITE_SIZE", "decode_mfma_persistent")
-    cf = per_dispatch(copy_fetch_csv, "FETCH_SIZE", "copy_segments")
-    cw = per_dispatch(copy_write_csv, "WRITE_SIZE", "copy_segments")
+    cf = per_dispatch(copy_fetch_csv, "FETCH_SIZE", "copy_indexed")
+    cw = per_dispatch(copy_write_csv, "WRITE_SIZE", "copy_indexed")
     moved = 128 << 20
     ff, wf = moved / 1024 / cf, moved / 1024 / cw
     traffic = fetch * 1024 * ff + write * 1024 * wf
@@ -179,7 +179,7 @@ def write_traffic(fetch_csv: str, write_csv: str, copy_fetch_csv: str, copy_writ
         "write_factor": round(wf, 4),
         "bytes_per_launch": int(traffic),
         "traffic_over_algorithmic": round(traffic / kb, 4),
-        "calibration": {"kernel": "copy_segments", "bytes_read": moved, "bytes_written": moved,
+        "calibration": {"kernel": "copy_indexed", "bytes_read": moved, "bytes_written": moved,
                         "fetch_size_kib": round(cf, 3), "write_size_kib": round(cw, 3)},
         "commands": commands,
     }
@@ -241,9 +241,11 @@ def copy_bench(steps: int, warmup: int) -> int:
     """qvp_copy_blocks of 128 (source, destination) frame pairs in one launch
     (the copy-on-write step of config4: one shared tail per branch), at the
     7B frame sizes of one layer (32 KiB) and of all 28 layers (917,504 B),
-    and at 1 MiB; frames drawn at random from a 1 GiB pool. Kernel time from
-    two HIP events around `steps` launches on the copy stream; bytes moved =
-    2 x 128 x frame (read + write)."""
+    and at 1 MiB; frames drawn at random from a 1 GiB pool. Kernel time: two
+    HIP events around one launch of a graph holding `steps` copies (back to
+    back on the device, whatever the host's enqueue rate); beside it the same
+    launches enqueued one call at a time from Python. Bytes moved = 2 x 128 x
+    frame (read + write)."""
     pool_bytes = 1 << 30
     stream = qvp.Stream()
     lines = []
@@ -262,11 +264,23 @@ def copy_bench(steps: int, warmup: int) -> int:
             qvp.copy_blocks(pool.base, pool.stride, nblocks, src, dst, frame, stream)
         e1.record(stream)
         stream.synchronize()
+        eager_ms = e0.elapsed_ms(e1) / steps
+        with qvp.Graph.capture(stream) as graph:
+            for _ in range(steps):
+                qvp.copy_blocks(pool.base, pool.stride, nblocks, src, dst, frame, stream)
+        graph.launch(stream)
+        stream.synchronize()
+        e0.record(stream)
+        graph.launch(stream)
+        e1.record(stream)
+        stream.synchronize()
         ms = e0.elapsed_ms(e1) / steps
+        graph.destroy()
         moved = 2 * 128 * frame
         lines.append({"frame_bytes": frame, "pairs": 128, "avg_us": round(ms * 1e3, 3),
                       "read_plus_write_GBps": round(moved / (ms * 1e-3) / 1e9, 1),
-                      "frac_of_peak": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)})
+                      "frac_of_peak": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                      "eager_calls_avg_us": round(eager_ms * 1e3, 3)})
         pool.destroy()
     print(json.dumps({"mode": "copy_blocks", "unit": "GB/s read+write", "cases": lines}))
     return 0
@@ -520,7 +534,7 @@ def swap_bench(steps: int, warmup: int) -> int:
                       "roofline": {"bound": "host link", "out_frac_of_contiguous": round(d2h / g, 3),
                                    "in_frac_of_contiguous": round(h2d / sc, 3)}})
         arena.free()
-    print(json.dumps({"mode": "swap", "kernel": "copy_segments (swap gather/scatter)", "frame_bytes": frame,
+    print(json.dumps({"mode": "swap", "kernel": "copy_indexed (swap gather/scatter)", "frame_bytes": frame,
                       "data": "uninitialised HBM frames, shuffled frame ids", "steps": steps, "cases": cases}))
     return 0
 

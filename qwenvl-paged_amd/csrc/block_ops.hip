@@ -6,13 +6,18 @@
 // HostSwapBackend::store / load (src/SwapBackend.cpp:10-39): whole frames move
 // between HBM and a pinned host arena, the GPU itself driving the host link.
 //
-// All three share one kernel: a list of (source, destination) segments of equal
-// length travels in the kernel arguments (no staging buffer, no extra copy).
-// The segments are cut into 8 KiB chunks numbered across the whole list, and
-// a grid of at most two workgroups per CU walks the chunks with a stride of
-// the grid: short-lived workgroups (one chunk each) left the copy bound by how
+// All three share one copy loop: a list of (source, destination) segments of
+// equal length travels in the kernel arguments (no staging buffer, no extra
+// copy), as 32-bit indices into a base address per side (frame ids times the
+// frame stride; arena offsets in 16-byte units), 480 segments per launch; a
+// list of full pointers (128 per launch) covers arenas past 64 GiB. The
+// segments are cut into 8 KiB chunks numbered across the whole list, and a
+// grid of at most two workgroups per CU walks the chunks with a stride of the
+// grid: short-lived workgroups (one chunk each) left the copy bound by how
 // fast workgroups can be dispatched, about 5.5 TB/s of reads plus writes on
-// 128 whole 7B frames against 6.4 TB/s this way.
+// 128 whole 7B frames against 6.4 TB/s this way. Swaps of one-layer frames
+// (32 KiB) cross the host link in launches of up to 15 MiB instead of 4 MiB,
+// which halves the per-launch start-up and drain share of the time.
 #include "common.h"
 
 #include <algorithm>
@@ -29,40 +34,67 @@ constexpr int kCopyUnroll = 2;
 constexpr uint64_t kChunkBytes = static_cast<uint64_t>(kCopyThreads) * 16 * kCopyUnroll;
 constexpr uint32_t kWgsPerCu = 2;
 
+constexpr int kIndexedPerLaunch = 480;  // 3,840 bytes of indices in the kernel arguments
+
 struct SegmentList {
     const uint8_t* src[kSegmentsPerLaunch];
     uint8_t* dst[kSegmentsPerLaunch];
 };
 
+// Segment i: source src_base + src[i] * src_unit, destination dst_base +
+// dst[i] * dst_unit.
+struct IndexedList {
+    uint32_t src[kIndexedPerLaunch];
+    uint32_t dst[kIndexedPerLaunch];
+};
+
+// Chunk [chunk0, min(chunk0 + kChunkBytes, bytes)) of one segment.
+__device__ inline void copy_chunk(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint64_t chunk0,
+                                  uint64_t bytes) {
+    static_assert(kCopyUnroll == 2, "the full-chunk path moves two 16-byte words per thread");
+    const uint64_t chunk_end = min(chunk0 + kChunkBytes, bytes);
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0;
+    if (vec && chunk_end - chunk0 == kChunkBytes) {
+        // Both loads issue before either store (two words in flight per
+        // thread); plain registers, so nothing is staged through LDS.
+        const uint4* s4 = reinterpret_cast<const uint4*>(src + chunk0);
+        uint4* d4 = reinterpret_cast<uint4*>(dst + chunk0);
+        const uint4 r0 = s4[threadIdx.x];
+        const uint4 r1 = s4[threadIdx.x + kCopyThreads];
+        d4[threadIdx.x] = r0;
+        d4[threadIdx.x + kCopyThreads] = r1;
+    } else if (vec) {
+        const uint64_t vec_end = chunk0 + (chunk_end - chunk0) / 16 * 16;
+        for (uint64_t off = chunk0 + 16u * threadIdx.x; off < vec_end; off += 16u * kCopyThreads) {
+            *reinterpret_cast<uint4*>(dst + off) = *reinterpret_cast<const uint4*>(src + off);
+        }
+        for (uint64_t off = vec_end + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
+    } else {
+        for (uint64_t off = chunk0 + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
+    }
+}
+
 __global__ __launch_bounds__(kCopyThreads) void copy_segments(SegmentList list, uint64_t bytes,
                                                               uint32_t chunks_per_segment, uint32_t total_chunks) {
-    static_assert(kCopyUnroll == 2, "the full-chunk path moves two 16-byte words per thread");
     for (uint32_t c = blockIdx.x; c < total_chunks; c += gridDim.x) {
         const uint32_t seg = c / chunks_per_segment;
-        const uint8_t* __restrict__ src = list.src[seg];
-        uint8_t* __restrict__ dst = list.dst[seg];
+        const uint8_t* src = list.src[seg];
+        uint8_t* dst = list.dst[seg];
         if (src == dst) continue;
-        const uint64_t chunk0 = static_cast<uint64_t>(c - seg * chunks_per_segment) * kChunkBytes;
-        const uint64_t chunk_end = min(chunk0 + kChunkBytes, bytes);
-        const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0;
-        if (vec && chunk_end - chunk0 == kChunkBytes) {
-            // Both loads issue before either store (two words in flight per
-            // thread); plain registers, so nothing is staged through LDS.
-            const uint4* s4 = reinterpret_cast<const uint4*>(src + chunk0);
-            uint4* d4 = reinterpret_cast<uint4*>(dst + chunk0);
-            const uint4 r0 = s4[threadIdx.x];
-            const uint4 r1 = s4[threadIdx.x + kCopyThreads];
-            d4[threadIdx.x] = r0;
-            d4[threadIdx.x + kCopyThreads] = r1;
-        } else if (vec) {
-            const uint64_t vec_end = chunk0 + (chunk_end - chunk0) / 16 * 16;
-            for (uint64_t off = chunk0 + 16u * threadIdx.x; off < vec_end; off += 16u * kCopyThreads) {
-                *reinterpret_cast<uint4*>(dst + off) = *reinterpret_cast<const uint4*>(src + off);
-            }
-            for (uint64_t off = vec_end + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
-        } else {
-            for (uint64_t off = chunk0 + threadIdx.x; off < chunk_end; off += kCopyThreads) dst[off] = src[off];
-        }
+        copy_chunk(src, dst, static_cast<uint64_t>(c - seg * chunks_per_segment) * kChunkBytes, bytes);
+    }
+}
+
+__global__ __launch_bounds__(kCopyThreads) void copy_indexed(const uint8_t* src_base, uint64_t src_unit,
+                                                             uint8_t* dst_base, uint64_t dst_unit, IndexedList list,
+                                                             uint64_t bytes, uint32_t chunks_per_segment,
+                                                             uint32_t total_chunks) {
+    for (uint32_t c = blockIdx.x; c < total_chunks; c += gridDim.x) {
+        const uint32_t seg = c / chunks_per_segment;
+        const uint8_t* src = src_base + static_cast<uint64_t>(list.src[seg]) * src_unit;
+        uint8_t* dst = dst_base + static_cast<uint64_t>(list.dst[seg]) * dst_unit;
+        if (src == dst) continue;
+        copy_chunk(src, dst, static_cast<uint64_t>(c - seg * chunks_per_segment) * kChunkBytes, bytes);
     }
 }
 
@@ -107,6 +139,41 @@ int launch_segments(const std::vector<const uint8_t*>& src, const std::vector<ui
         QVP_HIP(hipGetLastError());
     }
     return QVP_OK;
+}
+
+// Enqueues segments [0, n) given as indices, in launches of kIndexedPerLaunch.
+int launch_indexed(const uint8_t* src_base, uint64_t src_unit, const std::vector<uint32_t>& src, uint8_t* dst_base,
+                   uint64_t dst_unit, const std::vector<uint32_t>& dst, uint64_t bytes, hipStream_t stream) {
+    const size_t n = src.size();
+    if (n == 0 || bytes == 0) return QVP_OK;
+    uint32_t cus = 0;
+    QVP_TRY(device_cus(&cus));
+    const uint64_t chunks = (bytes + kChunkBytes - 1) / kChunkBytes;
+    if (chunks * kIndexedPerLaunch > 0xffffffffull) return fail(QVP_ERR_INVALID_ARGUMENT, "segment too large");
+    for (size_t first = 0; first < n; first += kIndexedPerLaunch) {
+        const size_t count = std::min<size_t>(kIndexedPerLaunch, n - first);
+        IndexedList list{};
+        std::copy(src.begin() + first, src.begin() + first + count, list.src);
+        std::copy(dst.begin() + first, dst.begin() + first + count, list.dst);
+        const uint64_t total = chunks * count;
+        const uint64_t grid = std::min<uint64_t>(total, static_cast<uint64_t>(cus) * kWgsPerCu);
+        hipLaunchKernelGGL(copy_indexed, dim3(static_cast<unsigned>(grid)), dim3(kCopyThreads), 0, stream, src_base,
+                           src_unit, dst_base, dst_unit, list, bytes, static_cast<uint32_t>(chunks),
+                           static_cast<uint32_t>(total));
+        QVP_HIP(hipGetLastError());
+    }
+    return QVP_OK;
+}
+
+// Arena offsets in 16-byte units, when every one fits 32 bits (arenas up to
+// 64 GiB); false otherwise.
+bool arena_units(const uint64_t* offsets, uint32_t count, std::vector<uint32_t>& units) {
+    units.resize(count);
+    for (uint32_t i = 0; i < count; ++i) {
+        if (offsets[i] / 16 > 0xffffffffull) return false;
+        units[i] = static_cast<uint32_t>(offsets[i] / 16);
+    }
+    return true;
 }
 
 int check_frames(const uint32_t* ids, uint32_t count, uint32_t num_blocks, const char* what) {
@@ -189,13 +256,8 @@ int qvp_copy_blocks(void* kv_base, uint64_t block_stride, uint32_t num_blocks, c
         }
     }
     uint8_t* base = static_cast<uint8_t*>(kv_base);
-    std::vector<const uint8_t*> src(num_pairs);
-    std::vector<uint8_t*> dst(num_pairs);
-    for (uint32_t i = 0; i < num_pairs; ++i) {
-        src[i] = base + static_cast<uint64_t>(src_ids[i]) * block_stride;
-        dst[i] = base + static_cast<uint64_t>(dst_ids[i]) * block_stride;
-    }
-    return launch_segments(src, dst, copy_bytes, qvp::as_stream(stream));
+    return launch_indexed(base, block_stride, std::vector<uint32_t>(src_ids, src_ids + num_pairs), base, block_stride,
+                          std::vector<uint32_t>(dst_ids, dst_ids + num_pairs), copy_bytes, qvp::as_stream(stream));
 }
 
 int qvp_swap_gather(const void* kv_base, uint64_t block_stride, uint32_t num_blocks,
@@ -209,6 +271,11 @@ int qvp_swap_gather(const void* kv_base, uint64_t block_stride, uint32_t num_blo
     void* arena_dev = nullptr;
     QVP_HIP(hipHostGetDevicePointer(&arena_dev, arena, 0));
     const uint8_t* base = static_cast<const uint8_t*>(kv_base);
+    std::vector<uint32_t> units;
+    if (arena_units(arena_offsets, count, units)) {
+        return launch_indexed(base, block_stride, std::vector<uint32_t>(frame_ids, frame_ids + count),
+                              static_cast<uint8_t*>(arena_dev), 16, units, copy_bytes, qvp::as_stream(stream));
+    }
     std::vector<const uint8_t*> src(count);
     std::vector<uint8_t*> dst(count);
     for (uint32_t i = 0; i < count; ++i) {
@@ -230,6 +297,11 @@ int qvp_swap_scatter(void* kv_base, uint64_t block_stride, uint32_t num_blocks, 
     void* arena_dev = nullptr;
     QVP_HIP(hipHostGetDevicePointer(&arena_dev, const_cast<void*>(arena), 0));
     uint8_t* base = static_cast<uint8_t*>(kv_base);
+    std::vector<uint32_t> units;
+    if (arena_units(arena_offsets, count, units)) {
+        return launch_indexed(static_cast<const uint8_t*>(arena_dev), 16, units, base, block_stride,
+                              std::vector<uint32_t>(frame_ids, frame_ids + count), copy_bytes, qvp::as_stream(stream));
+    }
     std::vector<const uint8_t*> src(count);
     std::vector<uint8_t*> dst(count);
     for (uint32_t i = 0; i < count; ++i) {

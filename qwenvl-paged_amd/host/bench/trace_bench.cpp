@@ -15,10 +15,10 @@
 // causal prefill (PagedAttentionBatch::prefill) and get M-RoPE positions
 // (MRopePositionBatch); decoding requests append their new token's K/V before
 // the decode and get their position. K/V and queries are synthetic device
-// buffers; each phase is timed with events on the engine stream. The stream
-// idles while the host prepares a phase (validation, the copy-on-write walk,
-// staging uploads), so a phase's event time includes that host work; a
-// kernel trace gives the kernels' own time.
+// buffers; each phase is timed with events on the engine stream. When the
+// stream runs dry while the host prepares a phase (validation, the
+// copy-on-write walk, staging uploads), a phase's event time includes that
+// wait; a kernel trace gives the kernels' own time.
 //
 // Checks at the end: every request finished, the pool and the swap arena are
 // empty again. Output: one JSON line with decode tokens/s over the trace (wall
@@ -36,7 +36,14 @@
 // same requests, so equal logs mean equal decisions and equal frame and slot
 // ids.
 //
+// Steps are pipelined: the host prepares the next step (scheduler, cache
+// manager, packing, swap queueing) while the GPU runs the current one, with at
+// most --in-flight steps enqueued (default 2; 1 runs one step at a time). Swap
+// batches run on the allocator's side stream beside the engine stream's work;
+// their GPU time and bytes come from the allocator's per-batch events.
+//
 // Usage: trace_bench [--requests N] [--seed S] [--pool-percent P] [--watermark B] [--engine 0|1] [--log PATH]
+//                    [--in-flight N]
 #include "qvp.h"
 #include "qwenvl_paged/KVAppend.h"
 #include "qwenvl_paged/KVCacheManager.h"
@@ -91,6 +98,7 @@ int main(int argc, char** argv) {
     std::uint32_t requests = 200, pool_percent = 60, watermark = 64;
     std::uint64_t seed = 5;
     bool engine = false;
+    int in_flight = 2;
     std::string log_path;
     for (int i = 1; i + 1 < argc; i += 2) {
         const std::string k = argv[i];
@@ -104,6 +112,7 @@ int main(int argc, char** argv) {
         else if (k == "--pool-percent") pool_percent = static_cast<std::uint32_t>(v);
         else if (k == "--watermark") watermark = static_cast<std::uint32_t>(v);
         else if (k == "--engine") engine = v != 0;
+        else if (k == "--in-flight") in_flight = static_cast<int>(std::max<std::uint64_t>(1, v));
     }
     constexpr std::uint32_t kTpb = 16, kHkv = 4, kHq = 28, kD = 128;
     const BlockShape shape{kTpb, 1, kHkv, kD, 2};
@@ -153,10 +162,6 @@ int main(int argc, char** argv) {
     const std::size_t qbytes = static_cast<std::size_t>(sc.max_active_requests) * kHq * kD * 2;
     check(qvp_malloc(&dq, qbytes) == QVP_OK && qvp_malloc(&dout, qbytes) == QVP_OK, "q/out");
     check(qvp_fill_bytes(dq, 0x3c, qbytes, stream) == QVP_OK, "q fill");
-    void *ed0 = nullptr, *ed1 = nullptr, *es0 = nullptr, *es1 = nullptr;
-    check(qvp_event_create(&ed0) == QVP_OK && qvp_event_create(&ed1) == QVP_OK && qvp_event_create(&es0) == QVP_OK &&
-              qvp_event_create(&es1) == QVP_OK,
-          "events");
     PagedAttentionBatch attn;
     const float scale = 1.0f / std::sqrt(static_cast<float>(kD));
 
@@ -166,7 +171,6 @@ int main(int argc, char** argv) {
     MRopePositionBatch positions;
     const std::size_t max_rows = static_cast<std::size_t>(sc.max_batch_tokens) + sc.max_active_requests;
     void *dk = nullptr, *dv = nullptr, *dpq = nullptr, *dpo = nullptr, *dpos = nullptr;
-    void *ea0 = nullptr, *ea1 = nullptr, *ep0 = nullptr, *ep1 = nullptr, *em0 = nullptr, *em1 = nullptr;
     if (engine) {
         const std::size_t row = static_cast<std::size_t>(kHkv) * kD * 2;
         const std::size_t qrow = static_cast<std::size_t>(kHq) * kD * 2;
@@ -178,12 +182,37 @@ int main(int argc, char** argv) {
                   qvp_fill_bytes(dv, 0x3c, max_rows * row, stream) == QVP_OK &&
                   qvp_fill_bytes(dpq, 0x3c, max_rows * qrow, stream) == QVP_OK,
               "engine fill");
-        check(qvp_event_create(&ea0) == QVP_OK && qvp_event_create(&ea1) == QVP_OK &&
-                  qvp_event_create(&ep0) == QVP_OK && qvp_event_create(&ep1) == QVP_OK &&
-                  qvp_event_create(&em0) == QVP_OK && qvp_event_create(&em1) == QVP_OK,
-              "engine events");
     }
-    double append_gpu_ms = 0.0, prefill_gpu_ms = 0.0, mrope_gpu_ms = 0.0;
+    // Per-step GPU timing without stalling the host: each step records
+    // begin/end event pairs (append, prefill, decode, positions) and a final
+    // event into one of `in_flight` slots; a slot is read back (waiting for
+    // its step) only when it comes round again, so the host prepares up to
+    // in_flight - 1 steps ahead while the GPU runs (1: one step at a time).
+    enum Phase { kAppend = 0, kPrefill, kDecode, kPositions, kPhases };
+    struct StepEvents {
+        void* ev[2 * kPhases]{};
+        bool used[kPhases]{};
+        void* fin{nullptr};
+        bool pending{false};
+    };
+    std::vector<StepEvents> ring(static_cast<std::size_t>(in_flight));
+    for (StepEvents& r : ring) {
+        for (void*& e : r.ev) check(qvp_event_create(&e) == QVP_OK, "events");
+        check(qvp_event_create(&r.fin) == QVP_OK, "events");
+    }
+    double phase_ms[kPhases] = {0.0, 0.0, 0.0, 0.0};
+    auto retire = [&](StepEvents& r) {
+        if (!r.pending) return;
+        check(qvp_event_synchronize(r.fin) == QVP_OK, "step sync");
+        for (int k = 0; k < kPhases; ++k) {
+            if (!r.used[k]) continue;
+            float ms = 0.f;
+            check(qvp_event_elapsed_ms(&ms, r.ev[2 * k], r.ev[2 * k + 1]) == QVP_OK, "elapsed");
+            phase_ms[k] += ms;
+            r.used[k] = false;
+        }
+        r.pending = false;
+    };
     std::uint64_t prefill_tokens = 0;
     std::vector<SequenceId> app_seq, pos_seq;
     std::vector<TokenPosition> app_pos, pos_begin, pos_end;
@@ -202,8 +231,9 @@ int main(int argc, char** argv) {
     std::map<std::uint64_t, std::uint32_t> length, produced;
     std::deque<std::uint64_t> parked;
     std::uint64_t decode_tokens = 0, steps = 0, finished = 0, preemptions = 0, resumes = 0;
-    std::uint64_t swap_launch_before = alloc.swap_launches();
-    double decode_gpu_ms = 0.0, swap_gpu_ms = 0.0;
+    const std::uint64_t swap_launch_before = alloc.swap_launches();
+    const double swap_ms_before = alloc.swap_gpu_ms();
+    const std::uint64_t swap_bytes_before = alloc.swap_bytes_moved();
     std::uint64_t swapped_out_blocks = 0, swapped_in_blocks = 0;
     std::vector<CacheView> views;
     std::vector<std::uint32_t> lens;
@@ -212,6 +242,13 @@ int main(int argc, char** argv) {
     std::string log;
     std::string events;
     while (finished < requests && steps < 200000) {
+        StepEvents& slot = ring[steps % ring.size()];
+        retire(slot);
+        auto begin_phase = [&](Phase k) {
+            slot.used[k] = true;
+            check(qvp_event_record(slot.ev[2 * k], stream) == QVP_OK, "record");
+        };
+        auto end_phase = [&](Phase k) { check(qvp_event_record(slot.ev[2 * k + 1], stream) == QVP_OK, "record"); };
         ++steps;
         events.clear();
         bool pending = false;
@@ -293,65 +330,39 @@ int main(int argc, char** argv) {
             lens.push_back(pos + 1);
             ids.push_back(id);
         }
-        // Swap traffic and copy-on-write queued by this step run first, on
-        // the side stream; the events bracket them as seen from the engine
-        // stream.
-        const bool swaps = alloc.pending_operations() > 0;
-        if (swaps) {
-            check(qvp_event_record(es0, stream) == QVP_OK, "record");
-            check(alloc.flush(), "flush: " + alloc.last_error());
-            check(qvp_event_record(es1, stream) == QVP_OK, "record");
-        }
+        // Swap traffic queued by this step goes to the side stream now;
+        // engine work below waits only where it touches the frames moved.
+        check(alloc.flush(), "flush: " + alloc.last_error());
         if (engine && !app_seq.empty()) {
             // The step's K/V (prompt rows and decode tokens) through the
             // copy-on-write point: the blocks it shares are copied first, then
             // one store launch covers every row (offsets uploaded once when
             // there are more than 128).
             check(app_seq.size() <= max_rows, "append rows");
-            check(qvp_event_record(ea0, stream) == QVP_OK, "record");
+            begin_phase(kAppend);
             check(append.append(cache, alloc, app_seq, app_pos, 0, 1, dk, dv), "append: " + append.last_error());
-            check(qvp_event_record(ea1, stream) == QVP_OK, "record");
+            end_phase(kAppend);
         }
         if (engine && !pviews.empty()) {
-            check(qvp_event_record(ep0, stream) == QVP_OK, "record");
+            begin_phase(kPrefill);
             check(prefill_attn.prefill(pviews, plens, pfirst, 0, kHq, scale, dpq, dpo, ElementType::BF16),
                   "prefill: " + prefill_attn.last_error());
-            check(qvp_event_record(ep1, stream) == QVP_OK, "record");
+            end_phase(kPrefill);
         }
         if (!views.empty()) {
-            check(qvp_event_record(ed0, stream) == QVP_OK, "record");
+            begin_phase(kDecode);
             check(attn.decode(views, lens, 0, kHq, scale, dq, dout, ElementType::BF16), attn.last_error());
-            check(qvp_event_record(ed1, stream) == QVP_OK, "record");
-        }
-        if (engine && !pos_seq.empty()) {
-            check(qvp_event_record(em0, stream) == QVP_OK, "record");
-            check(positions.materialise(cache, pos_seq, pos_begin, pos_end, static_cast<std::int64_t*>(dpos), stream),
-                  "positions: " + positions.last_error());
-            check(qvp_event_record(em1, stream) == QVP_OK, "record");
-        }
-        check(qvp_stream_synchronize(stream) == QVP_OK, "sync");
-        float ms = 0.f;
-        if (engine && !app_seq.empty()) {
-            check(qvp_event_elapsed_ms(&ms, ea0, ea1) == QVP_OK, "elapsed");
-            append_gpu_ms += ms;
-        }
-        if (engine && !pviews.empty()) {
-            check(qvp_event_elapsed_ms(&ms, ep0, ep1) == QVP_OK, "elapsed");
-            prefill_gpu_ms += ms;
-        }
-        if (engine && !pos_seq.empty()) {
-            check(qvp_event_elapsed_ms(&ms, em0, em1) == QVP_OK, "elapsed");
-            mrope_gpu_ms += ms;
-        }
-        if (swaps) {
-            check(qvp_event_elapsed_ms(&ms, es0, es1) == QVP_OK, "elapsed");
-            swap_gpu_ms += ms;
-        }
-        if (!views.empty()) {
-            check(qvp_event_elapsed_ms(&ms, ed0, ed1) == QVP_OK, "elapsed");
-            decode_gpu_ms += ms;
+            end_phase(kDecode);
             decode_tokens += views.size();
         }
+        if (engine && !pos_seq.empty()) {
+            begin_phase(kPositions);
+            check(positions.materialise(cache, pos_seq, pos_begin, pos_end, static_cast<std::int64_t*>(dpos), stream),
+                  "positions: " + positions.last_error());
+            end_phase(kPositions);
+        }
+        check(qvp_event_record(slot.fin, stream) == QVP_OK, "record");
+        slot.pending = true;
         for (std::uint64_t id : ids) {
             sched.complete_step(id, 1);
             if (++produced[id] >= plans[id - 1].output) {
@@ -384,24 +395,28 @@ int main(int argc, char** argv) {
             log += std::to_string(steps - 1) + " P=" + pre + " D=" + dec + tail + events + "\n";
         }
     }
+    for (StepEvents& r : ring) retire(r);
+    check(alloc.synchronize(), "final sync");
     const double wall = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    const double append_gpu_ms = phase_ms[kAppend], prefill_gpu_ms = phase_ms[kPrefill];
+    const double decode_gpu_ms = phase_ms[kDecode], mrope_gpu_ms = phase_ms[kPositions];
+    const double swap_gpu_ms = alloc.swap_gpu_ms() - swap_ms_before;
     if (!log_path.empty()) {
         log += "finished=" + std::to_string(finished) + " of " + std::to_string(requests) + "\n";
         std::FILE* f = std::fopen(log_path.c_str(), "w");
         check(f != nullptr && std::fwrite(log.data(), 1, log.size(), f) == log.size() && std::fclose(f) == 0,
               "writing " + log_path);
     }
-    check(alloc.synchronize(), "final sync");
     const AllocatorStats st = alloc.stats();
     const bool drained = st.free_blocks == st.total_blocks && swap.resident_slots() == 0;
-    const double swap_bytes = static_cast<double>(swapped_out_blocks + swapped_in_blocks) * shape.byte_size();
+    const double swap_bytes = static_cast<double>(alloc.swap_bytes_moved() - swap_bytes_before);
     std::printf(
         "{\"mode\": \"config5_trace\", \"requests\": %u, \"finished\": %llu, \"steps\": %llu, \"pool_blocks\": %u, "
         "\"demand_blocks\": %llu, \"decode_tokens\": %llu, \"expected_decode_tokens\": %llu, \"wall_s\": %.4f, "
         "\"decode_tokens_per_s\": %.1f, \"decode_kernel_ms_total\": %.3f, \"decode_tokens_per_s_kernel_only\": "
         "%.1f, \"preemptions\": %llu, \"resumes\": %llu, \"swapped_out_blocks\": %llu, \"swapped_in_blocks\": %llu, "
         "\"swap_bytes\": %.0f, \"swap_ms_total\": %.3f, \"swap_GBps\": %.2f, \"swap_launches\": %llu, "
-        "\"drained\": %s, \"engine\": %s, \"prefill_tokens\": %llu, \"prefill_kernel_ms_total\": %.3f, "
+        "\"drained\": %s, \"engine\": %s, \"steps_in_flight\": %d, \"prefill_tokens\": %llu, \"prefill_kernel_ms_total\": %.3f, "
         "\"prefill_tokens_per_s_kernel_only\": %.1f, \"append_ms_total\": %.3f, \"mrope_ms_total\": %.3f}\n",
         requests, static_cast<unsigned long long>(finished), static_cast<unsigned long long>(steps), pool,
         static_cast<unsigned long long>(demand_blocks), static_cast<unsigned long long>(decode_tokens),
@@ -411,11 +426,14 @@ int main(int argc, char** argv) {
         static_cast<unsigned long long>(swapped_in_blocks), swap_bytes, swap_gpu_ms,
         swap_gpu_ms > 0 ? swap_bytes / (swap_gpu_ms * 1e-3) / 1e9 : 0.0,
         static_cast<unsigned long long>(alloc.swap_launches() - swap_launch_before), drained ? "true" : "false",
-        engine ? "true" : "false", static_cast<unsigned long long>(prefill_tokens), prefill_gpu_ms,
+        engine ? "true" : "false", in_flight, static_cast<unsigned long long>(prefill_tokens), prefill_gpu_ms,
         prefill_gpu_ms > 0 ? prefill_tokens / (prefill_gpu_ms * 1e-3) : 0.0, append_gpu_ms, mrope_gpu_ms);
     (void)qvp_free(dq);
     (void)qvp_free(dout);
     for (void* ptr : {dk, dv, dpq, dpo, dpos}) (void)qvp_free(ptr);
-    for (void* ev : {ea0, ea1, ep0, ep1, em0, em1}) (void)qvp_event_destroy(ev);
+    for (StepEvents& r : ring) {
+        for (void* e : r.ev) (void)qvp_event_destroy(e);
+        (void)qvp_event_destroy(r.fin);
+    }
     return (finished == requests && drained) ? 0 : 2;
 }

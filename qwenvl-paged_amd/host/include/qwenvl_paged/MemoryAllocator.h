@@ -116,6 +116,11 @@ public:
     // Launches issued by flush() so far, by kind (copy, gather, scatter).
     [[nodiscard]] std::uint64_t copy_launches() const noexcept;
     [[nodiscard]] std::uint64_t swap_launches() const noexcept;
+    // Swap batches known to have finished (every one after synchronize()):
+    // their GPU time on the side stream, start to end of each batch, and the
+    // bytes they moved.
+    [[nodiscard]] double swap_gpu_ms() const noexcept;
+    [[nodiscard]] std::uint64_t swap_bytes_moved() const noexcept;
     // Flush, then copy host bytes into / out of a frame and wait for the copy.
     bool write_block_bytes(PhysicalBlockId id, std::size_t offset, const void* src, std::size_t bytes);
     bool read_block_bytes(PhysicalBlockId id, std::size_t offset, void* dst, std::size_t bytes);
@@ -150,7 +155,9 @@ private:
     // recorded after it.
     struct SwapBatchEvent {
         std::uint64_t epoch;
-        void* event;
+        void* start;  // recorded on the side stream right before the launch
+        void* event;  // recorded right after it
+        std::uint64_t bytes;
     };
 
     bool fail(const std::string& what);
@@ -190,6 +197,8 @@ private:
     std::vector<DeviceOp> queue_;
     std::uint64_t copy_launches_{0};
     std::uint64_t swap_launches_{0};
+    double swap_gpu_ms_{0.0};
+    std::uint64_t swap_bytes_{0};
 };
 
 }  // namespace qwenvl_paged

@@ -66,7 +66,11 @@ MemoryAllocator::~MemoryAllocator() {
     // operations still queued are dropped with it.
     if (stream_ != nullptr) (void)qvp_stream_synchronize(stream_);
     if (side_stream_ != nullptr) (void)qvp_stream_synchronize(side_stream_);
-    for (SwapBatchEvent& b : swap_events_) (void)qvp_event_destroy(b.event);
+    for (SwapBatchEvent& b : swap_events_) {
+        (void)qvp_event_destroy(b.start);
+        (void)qvp_event_destroy(b.event);
+    }
+    for (void* e : spare_events_) (void)qvp_event_destroy(e);
     (void)qvp_event_destroy(main_event_);
     (void)qvp_stream_destroy(side_stream_);
     if (own_stream_) (void)qvp_stream_destroy(stream_);
@@ -212,6 +216,8 @@ std::size_t MemoryAllocator::block_stride() const noexcept { return pool_ ? qvp_
 std::size_t MemoryAllocator::pending_operations() const noexcept { return queue_.size(); }
 std::uint64_t MemoryAllocator::copy_launches() const noexcept { return copy_launches_; }
 std::uint64_t MemoryAllocator::swap_launches() const noexcept { return swap_launches_; }
+double MemoryAllocator::swap_gpu_ms() const noexcept { return swap_gpu_ms_; }
+std::uint64_t MemoryAllocator::swap_bytes_moved() const noexcept { return swap_bytes_; }
 
 void MemoryAllocator::enqueue_swap_gather(PhysicalBlockId frame, void* arena, std::size_t arena_bytes,
                                           std::size_t offset) {
@@ -252,25 +258,36 @@ bool MemoryAllocator::run_batch(OpKind kind, const std::vector<DeviceOp>& ops) {
     if (qvp_event_record(main_event_, stream_) != QVP_OK || qvp_stream_wait_event(side_stream_, main_event_) != QVP_OK) {
         return fail(std::string("swap ordering: ") + qvp_last_error());
     }
+    void* ev[2] = {nullptr, nullptr};
+    for (void*& e : ev) {
+        if (!spare_events_.empty()) {
+            e = spare_events_.back();
+            spare_events_.pop_back();
+        } else if (qvp_event_create(&e) != QVP_OK) {
+            for (void* made : ev) {
+                if (made != nullptr) spare_events_.push_back(made);
+            }
+            return fail(std::string("swap event: ") + qvp_last_error());
+        }
+    }
+    if (qvp_event_record(ev[0], side_stream_) != QVP_OK) {
+        spare_events_.insert(spare_events_.end(), ev, ev + 2);
+        return fail(std::string("swap ordering: ") + qvp_last_error());
+    }
     const int st = kind == OpKind::Gather
                        ? qvp_swap_gather(qvp_pool_base(pool_), stride, config_.max_blocks, a.data(), off.data(), n,
                                          ops[0].arena, ops[0].arena_bytes, stride, side_stream_)
                        : qvp_swap_scatter(qvp_pool_base(pool_), stride, config_.max_blocks, a.data(), off.data(), n,
                                           ops[0].arena, ops[0].arena_bytes, stride, side_stream_);
-    if (st != QVP_OK) return fail(std::string("swap launch: ") + qvp_last_error());
-    void* done = nullptr;
-    if (!spare_events_.empty()) {
-        done = spare_events_.back();
-        spare_events_.pop_back();
-    } else if (qvp_event_create(&done) != QVP_OK) {
-        return fail(std::string("swap event: ") + qvp_last_error());
-    }
-    if (qvp_event_record(done, side_stream_) != QVP_OK) {
-        (void)qvp_event_destroy(done);
-        return fail(std::string("swap ordering: ") + qvp_last_error());
+    if (st != QVP_OK || qvp_event_record(ev[1], side_stream_) != QVP_OK) {
+        // The start event may already be recorded on the side stream; the
+        // events are only reused once that stream has passed them.
+        (void)qvp_stream_synchronize(side_stream_);
+        spare_events_.insert(spare_events_.end(), ev, ev + 2);
+        return fail(std::string(st != QVP_OK ? "swap launch: " : "swap ordering: ") + qvp_last_error());
     }
     const std::uint64_t epoch = ++swap_epoch_;
-    swap_events_.push_back(SwapBatchEvent{epoch, done});
+    swap_events_.push_back(SwapBatchEvent{epoch, ev[0], ev[1], static_cast<std::uint64_t>(n) * stride});
     std::vector<std::uint64_t>& moved = kind == OpKind::Gather ? gather_epoch_ : scatter_epoch_;
     for (const DeviceOp& op : ops) moved[op.frame_a] = epoch;
     ++swap_launches_;
@@ -284,8 +301,13 @@ bool MemoryAllocator::retire_swap_batches() {
             return fail(std::string("swap event query: ") + qvp_last_error());
         }
         if (complete == 0) break;
-        completed_epoch_ = swap_events_.front().epoch;
-        spare_events_.push_back(swap_events_.front().event);
+        const SwapBatchEvent& b = swap_events_.front();
+        float ms = 0.f;
+        if (qvp_event_elapsed_ms(&ms, b.start, b.event) == QVP_OK) swap_gpu_ms_ += ms;
+        swap_bytes_ += b.bytes;
+        completed_epoch_ = b.epoch;
+        spare_events_.push_back(b.start);
+        spare_events_.push_back(b.event);
         swap_events_.pop_front();
     }
     return true;
