@@ -192,7 +192,10 @@ bool decode_host_frames(const CacheView& view, const T* query, const PagedAttent
     void* stream = scratch.stream;
     if (qvp_memcpy_htod(scratch.dev_slices, staging, total, stream) != QVP_OK ||
         qvp_memcpy_htod(scratch.dq, query, bytes, stream) != QVP_OK) {
-        return refuse(std::string("upload: ") + qvp_last_error());
+        // A first copy may be under way: the staging is reused by the next call.
+        const std::string why = std::string("upload: ") + qvp_last_error();
+        (void)qvp_stream_synchronize(stream);
+        return refuse(why);
     }
     std::vector<std::uint32_t> ids(needed);
     for (std::uint32_t j = 0; j < needed; ++j) ids[j] = j;
