@@ -16,7 +16,11 @@
 // decode); decode_us_median the decode kernel alone, relaunched on the packed
 // batch.
 //
-// Output: one JSON line. Usage: cow_bench [--prompts N] [--branches N] [--reps N]
+// --layers N stores all N layers of the model in each frame (N = 28: whole
+// Qwen2-VL-7B frames of 917,504 B, so each copy-on-write copy moves 28x the
+// bytes); the decode reads layer 0.
+//
+// Output: one JSON line. Usage: cow_bench [--prompts N] [--branches N] [--reps N] [--layers N]
 #include "qvp.h"
 #include "qwenvl_paged/KVCacheManager.h"
 #include "qwenvl_paged/MemoryAllocator.h"
@@ -76,16 +80,17 @@ float elapsed_ms(void* a, void* b) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    std::uint32_t prompts = 16, branches = 8, reps = 20;
+    std::uint32_t prompts = 16, branches = 8, reps = 20, layers = 1;
     for (int i = 1; i + 1 < argc; i += 2) {
         const std::string k = argv[i];
         const std::uint32_t v = static_cast<std::uint32_t>(std::atoi(argv[i + 1]));
         if (k == "--prompts") prompts = v;
         else if (k == "--branches") branches = v;
         else if (k == "--reps") reps = v;
+        else if (k == "--layers") layers = std::max<std::uint32_t>(1, v);
     }
     constexpr std::uint32_t kTpb = 16, kHkv = 4, kHq = 28, kD = 128, kPrompt = 2048;
-    const BlockShape shape{kTpb, 1, kHkv, kD, 2};
+    const BlockShape shape{kTpb, layers, kHkv, kD, 2};
     const std::uint32_t blocks_per_prompt = (kPrompt + 1 + kTpb - 1) / kTpb;  // 129
     const std::uint32_t pool = prompts * blocks_per_prompt + prompts * branches + 64;
 
@@ -114,12 +119,15 @@ int main(int argc, char** argv) {
         check(dev_cache.reserve_tokens(id, kPrompt + 1) && host_cache.reserve_tokens(id, kPrompt + 1),
               "reserve prompt");
         for (const BlockTableEntry& e : dev_cache.cache_view(id)->block_table->entries()) {
-            for (auto& x : frame) {
+            // Random layer 0 (what the decode reads); the other layers repeat it.
+            const std::size_t slice = frame.size() / layers;
+            for (std::size_t i = 0; i < slice; ++i) {
                 const float v = rng.gauss(0.5f);
                 std::uint32_t u;
                 std::memcpy(&u, &v, 4);
-                x = static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+                frame[i] = static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
             }
+            for (std::uint32_t l = 1; l < layers; ++l) std::copy_n(frame.begin(), slice, frame.begin() + l * slice);
             check(dev.write_block_bytes(e.physical_id, 0, frame.data(), frame_bytes), "write frame");
             check(host.write_block_bytes(e.physical_id, 0, frame.data(), frame_bytes), "write host frame");
         }
@@ -236,7 +244,7 @@ int main(int argc, char** argv) {
     args.batch = attn.packed();
     args.kv_dtype = QVP_DTYPE_BF16;
     args.out_dtype = QVP_DTYPE_BF16;
-    args.num_layers = 1;
+    args.num_layers = layers;
     args.num_query_heads = kHq;
     args.num_kv_heads = kHkv;
     args.head_dim = kD;
@@ -311,13 +319,13 @@ int main(int argc, char** argv) {
     const double unique = (static_cast<double>(prompts) * kPrompt + 2.0 * nb) * per_token;
     const double qo = static_cast<double>(nb) * kHq * kD * 2 * 2;
     std::printf(
-        "{\"mode\": \"config4_cow\", \"prompts\": %u, \"branches_per_prompt\": %u, \"cow_pairs\": %zu, "
+        "{\"mode\": \"config4_cow\", \"layers\": %u, \"prompts\": %u, \"branches_per_prompt\": %u, \"cow_pairs\": %zu, "
         "\"pending_before_flush\": %zu, \"copy_launches\": %llu, \"copy_us_median\": %.3f, \"copy_read_plus_write_GBps\": "
         "%.1f, \"frames_equal_host_allocator\": %s, \"copies_equal_source\": %s, \"decode_branches\": %u, "
         "\"decode_ctx\": %u, \"step_us_median\": %.3f, \"decode_us_median\": %.3f, \"decode_logical_GBps\": %.1f, \"decode_unique_GBps\": "
         "%.1f, \"decode_tokens_per_s\": %.1f, \"checked_elements\": %zu, \"worst_excess_over_tolerance\": %.3g, "
         "\"decode_within_tolerance\": %s}\n",
-        prompts, branches, copies.size(), pending, static_cast<unsigned long long>(copy_launches), copy_ms * 1e3,
+        layers, prompts, branches, copies.size(), pending, static_cast<unsigned long long>(copy_launches), copy_ms * 1e3,
         copy_bytes / (copy_ms * 1e-3) / 1e9, frames_equal ? "true" : "false", copies_equal ? "true" : "false", nb,
         ctx, step_ms * 1e3, decode_ms * 1e3, (logical + qo) / (decode_ms * 1e-3) / 1e9, (unique + qo) / (decode_ms * 1e-3) / 1e9,
         nb / (decode_ms * 1e-3), checked, worst, worst <= 0.0 ? "true" : "false");

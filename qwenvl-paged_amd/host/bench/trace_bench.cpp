@@ -43,7 +43,11 @@
 // their GPU time and bytes come from the allocator's per-batch events.
 //
 // Usage: trace_bench [--requests N] [--seed S] [--pool-percent P] [--watermark B] [--engine 0|1] [--log PATH]
-//                    [--in-flight N]
+//                    [--in-flight N] [--layers N]
+//
+// --layers N stores all N layers of the model in each frame (N = 28: whole
+// Qwen2-VL-7B frames of 917,504 B); every GPU phase works on layer 0, and swaps
+// move whole frames.
 #include "qvp.h"
 #include "qwenvl_paged/KVAppend.h"
 #include "qwenvl_paged/KVCacheManager.h"
@@ -99,6 +103,7 @@ int main(int argc, char** argv) {
     std::uint64_t seed = 5;
     bool engine = false;
     int in_flight = 2;
+    std::uint32_t layers = 1;
     std::string log_path;
     for (int i = 1; i + 1 < argc; i += 2) {
         const std::string k = argv[i];
@@ -113,9 +118,10 @@ int main(int argc, char** argv) {
         else if (k == "--watermark") watermark = static_cast<std::uint32_t>(v);
         else if (k == "--engine") engine = v != 0;
         else if (k == "--in-flight") in_flight = static_cast<int>(std::max<std::uint64_t>(1, v));
+        else if (k == "--layers") layers = static_cast<std::uint32_t>(std::max<std::uint64_t>(1, v));
     }
     constexpr std::uint32_t kTpb = 16, kHkv = 4, kHq = 28, kD = 128;
-    const BlockShape shape{kTpb, 1, kHkv, kD, 2};
+    const BlockShape shape{kTpb, layers, kHkv, kD, 2};
 
     struct Plan {
         std::uint32_t prompt, output;
@@ -411,14 +417,14 @@ int main(int argc, char** argv) {
     const bool drained = st.free_blocks == st.total_blocks && swap.resident_slots() == 0;
     const double swap_bytes = static_cast<double>(alloc.swap_bytes_moved() - swap_bytes_before);
     std::printf(
-        "{\"mode\": \"config5_trace\", \"requests\": %u, \"finished\": %llu, \"steps\": %llu, \"pool_blocks\": %u, "
+        "{\"mode\": \"config5_trace\", \"layers\": %u, \"requests\": %u, \"finished\": %llu, \"steps\": %llu, \"pool_blocks\": %u, "
         "\"demand_blocks\": %llu, \"decode_tokens\": %llu, \"expected_decode_tokens\": %llu, \"wall_s\": %.4f, "
         "\"decode_tokens_per_s\": %.1f, \"decode_kernel_ms_total\": %.3f, \"decode_tokens_per_s_kernel_only\": "
         "%.1f, \"preemptions\": %llu, \"resumes\": %llu, \"swapped_out_blocks\": %llu, \"swapped_in_blocks\": %llu, "
         "\"swap_bytes\": %.0f, \"swap_ms_total\": %.3f, \"swap_GBps\": %.2f, \"swap_launches\": %llu, "
         "\"drained\": %s, \"engine\": %s, \"steps_in_flight\": %d, \"prefill_tokens\": %llu, \"prefill_kernel_ms_total\": %.3f, "
         "\"prefill_tokens_per_s_kernel_only\": %.1f, \"append_ms_total\": %.3f, \"mrope_ms_total\": %.3f}\n",
-        requests, static_cast<unsigned long long>(finished), static_cast<unsigned long long>(steps), pool,
+        layers, requests, static_cast<unsigned long long>(finished), static_cast<unsigned long long>(steps), pool,
         static_cast<unsigned long long>(demand_blocks), static_cast<unsigned long long>(decode_tokens),
         static_cast<unsigned long long>(total_output), wall, decode_tokens / wall, decode_gpu_ms,
         decode_tokens / (decode_gpu_ms * 1e-3), static_cast<unsigned long long>(preemptions),

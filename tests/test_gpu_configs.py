@@ -39,11 +39,13 @@ def run(name: str, *args: str) -> dict:
 
 
 @pytest.mark.gpu
-def test_copy_on_write_configuration_full_size():
+@pytest.mark.parametrize("layers", [1, 28])
+def test_copy_on_write_configuration_full_size(layers):
     """config4 as specified: 16 prompts x 8 branches, 128 copy-on-write pairs
-    in one batched copy, decode over the 128 branches."""
-    r = run("cow_bench")
-    assert r["cow_pairs"] == 128
+    in one batched copy, decode over the 128 branches; with one layer per frame
+    and with whole 28-layer Qwen2-VL-7B frames (917,504 B copies)."""
+    r = run("cow_bench", "--layers", str(layers), "--reps", "5")
+    assert r["layers"] == layers and r["cow_pairs"] == 128
     assert r["pending_before_flush"] == 128
     assert r["copy_launches"] == 1
     assert r["frames_equal_host_allocator"] and r["copies_equal_source"]
@@ -75,6 +77,19 @@ def test_continuous_batching_trace_full_size_matches_the_reference(tmp_path, eng
     assert r["decode_tokens"] == r["expected_decode_tokens"]
     assert r["preemptions"] > 0 and r["resumes"] > 0
     assert r["swapped_out_blocks"] > 0 and r["swapped_in_blocks"] > 0
+    got, expected = log.read_text(), _reference_config5_log()
+    assert got == expected, _first_difference(got, expected)
+
+
+@pytest.mark.gpu
+def test_continuous_batching_trace_with_whole_28_layer_frames(tmp_path):
+    """The config5 trace with every frame holding all 28 layers (917,504 B):
+    the same decisions and ids as the reference's log (frame size changes no
+    decision), 39.5 GB swapped out and back in, and everything drains."""
+    log = tmp_path / "trace28.log"
+    r = run("trace_bench", "--requests", "200", "--seed", "5", "--layers", "28", "--log", str(log))
+    assert r["layers"] == 28 and r["finished"] == 200 and r["drained"]
+    assert r["swap_bytes"] == (r["swapped_out_blocks"] + r["swapped_in_blocks"]) * 917504
     got, expected = log.read_text(), _reference_config5_log()
     assert got == expected, _first_difference(got, expected)
 
