@@ -654,7 +654,9 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--split", type=int, default=512, help="split-K partition in tokens")
+    ap.add_argument("--split", type=int, default=None,
+                    help="split-K partition in tokens (default: the workload's, 0 for config2 -- cuts by cost "
+                         "alone -- and 512 for config3)")
     ap.add_argument("--pools", type=int, default=3, help="independent pool copies rotated between steps")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -712,6 +714,8 @@ def main() -> int:
         return 2
 
     w = W.config2() if args.workload == "config2" else W.config3()
+    if args.split is None:
+        args.split = w.split_tokens
     t_setup = time.perf_counter()
     # config3's pool (~3 GB) takes a repeated 64 MiB random chunk: contents do
     # not change the traffic, and the parity tests cover the values.
@@ -843,9 +847,11 @@ def main() -> int:
                 f"Hq64/Hkv8/D128, block 16, bf16 KV, pool +10% spare, {len(pools)} pool copies"),
             "batch": w.num_seqs,
             "cached_tokens": int(w.context_lens.sum()),
-            # The schedule the decode kernel ran (qvp_decode_plan_info): the
-            # bf16 MFMA kernel cuts cost-balanced tile ranges, one per
-            # workgroup, and has no split-size parameter.
+            # The pack's split_tokens (0: none given) and the schedule the
+            # decode kernel ran (qvp_decode_plan_info): the bf16 MFMA kernel
+            # cuts cost-balanced tile ranges, one per workgroup, held to
+            # split_tokens partition boundaries when one is given.
+            "split_tokens": args.split,
             "decode_plan": plan,
             "parallelism": "single GPU",
         },

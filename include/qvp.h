@@ -211,7 +211,13 @@ int qvp_batch_destroy(qvp_batch* batch);
  * so a refused call (QVP_ERR_INVALID_ARGUMENT for context_len == 0 or too few
  * mapped blocks, QVP_ERR_UNMAPPED for a missing frame) leaves the batch's
  * previous contents intact (PagedAttention.h:73-89).
- * split_tokens (0 selects 512) is rounded up to a multiple of 128.
+ * split_tokens (0 selects 512) is rounded up to a multiple of 128: the
+ * split-K partition (flash-decoding style) of the fp32 and generic decode
+ * kernels. The persistent bf16 kernel balances its work in ranges of 32-token
+ * tiles cut by cost; when split_tokens is given (non-zero) its ranges are
+ * cut only at multiples of split_tokens inside a sequence (or at sequence
+ * ends), so every cross-workgroup merge joins whole partitions; with 0 its
+ * cuts are free.
  * The arrays are staged in pinned memory and uploaded by one kernel on
  * `stream`. Packs alternate between two device buffers: the arrays of pack n
  * stay valid until pack n + 2, so pack n + 1 may be enqueued on another
@@ -337,8 +343,10 @@ typedef struct qvp_decode_plan {
                                    split kernels: token partitions */
     uint32_t slots;             /* partial results merged through the workspace */
     uint32_t kv_heads_per_segment; /* MFMA: kv heads one workgroup decodes side by side */
-    uint32_t split_tokens;      /* split kernels: tokens per partition; MFMA: 0 (its
-                                   ranges are cut by cost, not by a partition size) */
+    uint32_t split_tokens;      /* split kernels: tokens per partition; MFMA: the
+                                   partition its range cuts were held to (the pack's
+                                   split_tokens when the caller gave one), 0 when the
+                                   ranges were cut by cost alone */
     uint32_t deferred_results;  /* MFMA: 1 when piece results wait in LDS until a range ends */
     uint32_t query_group;       /* query heads per kv head of that decode */
     uint32_t tile_engine;       /* MFMA kernel: the qvp_tile_engine that ran (1 or 2) */

@@ -54,6 +54,7 @@ struct qvp_schedule {
     uint32_t max_partial_pieces_per_wg{0};
     uint32_t hps{1};  // kv heads per segment
     uint32_t tile_group{0};  // DecodeGeometry::tile_group the LDS budget was planned for
+    uint32_t partition_tiles{0};  // ranges cut only at multiples of this many tiles of a sequence (0: anywhere)
     std::vector<double> weights;  // streaming weight per kv-head group the ranges were cut for
     bool defer{false};            // piece results held in LDS until a range is done
     uint32_t lds_bytes{0};        // dynamic LDS per workgroup for them
@@ -102,6 +103,9 @@ struct qvp_batch {
     hipStream_t upload_stream[2]{nullptr, nullptr};  // stream of each slot's upload
     bool valid{false};
     uint64_t generation{0};            // bumped by every successful pack
+    // Partition of the split-K cuts the caller asked for, in 32-token tiles (0:
+    // none given -- the persistent kernel then cuts its ranges anywhere).
+    uint32_t partition_tiles{0};
     std::vector<int32_t> host_seq_lens;  // host copy of seq_lens for scheduling
     std::vector<uint32_t> host_ids;      // host copy of the needed block ids, CSR over host_cu_blocks
     std::vector<uint32_t> host_cu_blocks;

@@ -83,6 +83,9 @@ int decode_geometry(const qvp_decode_args* a, const qvp_packed_view& v, DecodeGe
 bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr,
                     uintptr_t kv_base_addr);
 
+// Tokens per tile of the persistent decode (its schedule counts tiles).
+constexpr uint32_t kScheduleTileTokens = 32;
+
 // The host-side batch a schedule is planned from (context lengths and the
 // needed block ids in CSR form).
 struct ScheduleInput {
@@ -92,6 +95,9 @@ struct ScheduleInput {
     const uint32_t* cu_blocks;
     uint32_t tpb;
     uint64_t generation;  // pack generation the schedule will belong to
+    // Split-K partition in 32-token tiles: ranges are cut only at multiples of
+    // it inside a sequence (or at sequence ends); 0 cuts anywhere.
+    uint32_t partition_tiles;
 };
 // True when the batch's schedule was built for this pack and this geometry.
 bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g);

@@ -674,15 +674,31 @@ std::vector<double> head_group_weights(const DecodeGeometry& g, uint32_t hps, ui
     return w;
 }
 
+// The allowed range ends of a split-K partition of `part` tiles: every
+// multiple of part positions from the start of a sequence (segment) and every
+// sequence end, increasing; the last one is T.
+std::vector<uint64_t> partition_ends(const std::vector<uint64_t>& pos_cum, uint32_t part) {
+    std::vector<uint64_t> ends;
+    for (size_t b = 0; b + 1 < pos_cum.size(); ++b) {
+        for (uint64_t e = pos_cum[b] + part; e < pos_cum[b + 1]; e += part) ends.push_back(e);
+        if (pos_cum[b + 1] > pos_cum[b]) ends.push_back(pos_cum[b + 1]);
+    }
+    return ends;
+}
+
 // Cuts T = pos_cum.back() tile positions into R contiguous ranges of equal
 // cost, a position costing 1 and every segment start inside a range (a
 // piece boundary: the waves' LDS merge and the piece's stores) costing cb
-// more.
-std::vector<uint64_t> cut_ranges(const std::vector<uint64_t>& pos_cum, uint32_t R, double cb) {
+// more. With part > 0 every cut is the partition end (partition_ends)
+// nearest the cost-balanced one that still leaves one partition to each
+// later range; R must then not exceed the number of partitions.
+std::vector<uint64_t> cut_ranges(const std::vector<uint64_t>& pos_cum, uint32_t R, double cb, uint32_t part) {
     const uint64_t T = pos_cum.back();
     const size_t S = pos_cum.size() - 1;
     std::vector<uint64_t> bd(R + 1, 0);
     bd[R] = T;
+    const std::vector<uint64_t> ends = part > 0 ? partition_ends(pos_cum, part) : std::vector<uint64_t>{};
+    size_t next_end = 0;  // first partition end the next cut may take
     uint64_t pos = 0;
     size_t seg = 0;
     for (uint32_t r = 0; r + 1 < R; ++r) {
@@ -710,6 +726,16 @@ std::vector<uint64_t> cut_ranges(const std::vector<uint64_t>& pos_cum, uint32_t 
             if (p < T) acc += cb;
         }
         cut = std::min(std::max(cut, lo), hi);
+        if (part > 0) {
+            // Partition ends next_end .. last (inclusive) are open to this
+            // cut: each later range keeps one of the ends after it.
+            const size_t last = ends.size() - 1 - (R - 1 - r);
+            size_t k = static_cast<size_t>(std::lower_bound(ends.begin(), ends.end(), cut) - ends.begin());
+            k = std::min(std::max(k, next_end), last);
+            if (k > next_end && ends[k] > cut && cut - ends[k - 1] < ends[k] - cut) --k;
+            cut = ends[k];
+            next_end = k + 1;
+        }
         bd[r + 1] = cut;
         pos = cut;
     }
@@ -741,7 +767,7 @@ bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_
 bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g) {
     const qvp_schedule& s = batch->sched;
     if (!s.valid || s.pack_generation != batch->generation || s.num_kv_heads != g.num_kv_heads ||
-        s.group != g.group || s.tile_group != g.tile_group) {
+        s.group != g.group || s.tile_group != g.tile_group || s.partition_tiles != batch->partition_tiles) {
         return false;
     }
     uint32_t max_wgs = 0;
@@ -780,8 +806,17 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     // per token's heads).
     const uint64_t tl = kWaves / hps;
     // At least one tile per tile lane, at least one range.
-    const uint32_t R = static_cast<uint32_t>(
-        std::min<uint64_t>(std::max<uint32_t>(1, max_wgs / nq), std::max<uint64_t>(1, (T + tl - 1) / tl)));
+    // With a split-K partition the cuts can only fall on partition
+    // boundaries: no more ranges than partitions.
+    uint64_t cut_room = T;
+    if (in.partition_tiles > 0) {
+        cut_room = 0;
+        for (uint32_t b = 0; b < nseq; ++b) {
+            cut_room += (pos_cum[b + 1] - pos_cum[b] + in.partition_tiles - 1) / in.partition_tiles;
+        }
+    }
+    const uint64_t max_ranges = std::max<uint64_t>(1, std::min<uint64_t>((T + tl - 1) / tl, cut_room));
+    const uint32_t R = static_cast<uint32_t>(std::min<uint64_t>(std::max<uint32_t>(1, max_wgs / nq), max_ranges));
     const uint32_t W = R * nq;
     std::vector<uint32_t> Rq(nq, R);
     if (R >= 2) {
@@ -795,7 +830,7 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
         // Rounding leftovers go to (or come from) the heaviest group.
         const uint32_t heavy = static_cast<uint32_t>(std::max_element(weights.begin(), weights.end()) - weights.begin());
         Rq[heavy] = static_cast<uint32_t>(std::max<int64_t>(1, static_cast<int64_t>(Rq[heavy]) + W - given));
-        for (uint32_t q = 0; q < nq; ++q) Rq[q] = static_cast<uint32_t>(std::min<uint64_t>(Rq[q], std::max<uint64_t>(1, (T + tl - 1) / tl)));
+        for (uint32_t q = 0; q < nq; ++q) Rq[q] = static_cast<uint32_t>(std::min<uint64_t>(Rq[q], max_ranges));
     }
 
     struct RangeRef {
@@ -808,7 +843,7 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     // kWaves waves) that is kPieceBoundaryTiles * kWaves / hps.
     const double cb = kPieceBoundaryTiles * kWaves / hps;
     for (uint32_t q = 0; q < nq; ++q) {
-        const std::vector<uint64_t> bd = cut_ranges(pos_cum, Rq[q], cb);
+        const std::vector<uint64_t> bd = cut_ranges(pos_cum, Rq[q], cb, in.partition_tiles);
         for (uint32_t r = 0; r < Rq[q]; ++r) ranges.push_back({bd[r], bd[r + 1], q});
     }
     std::stable_sort(ranges.begin(), ranges.end(), [](const RangeRef& x, const RangeRef& y) {
@@ -900,6 +935,7 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     s.num_kv_heads = num_kv_heads;
     s.group = g.group;
     s.tile_group = g.tile_group;
+    s.partition_tiles = in.partition_tiles;
     s.max_wgs = max_wgs;
     s.weights = weights;
     s.num_wgs = Wn;
@@ -959,6 +995,7 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     in.cu_blocks = batch->host_cu_blocks.data();
     in.tpb = batch->view.tokens_per_block;
     in.generation = batch->generation;
+    in.partition_tiles = batch->partition_tiles;
     if (!may_allocate) {
         // Plan into a copy, so that a refusal leaves the schedule as it was.
         qvp_schedule probe{};

@@ -18,6 +18,7 @@
 namespace qvp {
 
 constexpr int kTileTokens = 32;
+static_assert(kTileTokens == static_cast<int>(kScheduleTileTokens), "schedule and tiles count the same tokens");
 
 struct KvTile {
     u32x4 k[2][4];  // [half u][QK mfma i]

@@ -122,6 +122,9 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
     if (num_seqs > 0 && (cu_blocks == nullptr || context_lens == nullptr)) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "cu_blocks or context_lens is NULL");
     }
+    // A split size the caller gives is also where the persistent kernel may
+    // cut a sequence between workgroups; 0 leaves its cuts free.
+    const bool explicit_split = split_tokens != 0;
     if (split_tokens == 0) split_tokens = kDefaultSplit;
     if (split_tokens > kMaxSplit) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "split_tokens %u exceeds %u", split_tokens, kMaxSplit);
@@ -203,6 +206,7 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
             sin.cu_blocks = batch->cu_scratch.data();
             sin.tpb = tokens_per_block;
             sin.generation = generation;
+            sin.partition_tiles = explicit_split ? split_tokens / qvp::kScheduleTileTokens : 0u;
             batch->sched.valid = false;
             QVP_TRY(qvp::mfma_plan_schedule(batch->sched, sin, g));
         }
@@ -325,6 +329,7 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
         }
     }
     batch->generation = generation;
+    batch->partition_tiles = explicit_split ? split_tokens / qvp::kScheduleTileTokens : 0u;
     batch->last_plan = qvp_decode_plan{};
     batch->valid = true;
     return QVP_OK;

@@ -243,6 +243,7 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         plan.kv_heads_per_segment = sc.hps;
         plan.deferred_results = sc.defer ? 1u : 0u;
         plan.tile_engine = g.tile_group != 0 ? QVP_TILE_VECTOR : QVP_TILE_MATRIX;
+        plan.split_tokens = sc.partition_tiles * qvp::kScheduleTileTokens;
     } else {
         const bool f32 = qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens,
                                                     reinterpret_cast<uintptr_t>(a->query),

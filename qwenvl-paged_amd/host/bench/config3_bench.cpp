@@ -18,7 +18,9 @@
 // PagedAttentionBatch::decode -- block-table walk, pack and schedule upload,
 // decode -- and the decode kernel alone, and reports the schedule.
 //
-// Output: one JSON line. Usage: config3_bench [--seqs N] [--lo T] [--hi T] [--reps N]
+// Output: one JSON line. Usage: config3_bench [--seqs N] [--lo T] [--hi T] [--reps N] [--split T]
+// (--split: split-K partition in tokens, 512 by default; 0 lets the decode cut
+// its ranges anywhere)
 #include "qvp.h"
 #include "qwenvl_paged/KVCacheManager.h"
 #include "qwenvl_paged/MRope.h"
@@ -143,7 +145,7 @@ bool same_metadata(const SequenceMetadata& a, const SequenceMetadata& b) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    std::uint32_t seqs = 32, lo = 8192, hi = 32768, reps = 20;
+    std::uint32_t seqs = 32, lo = 8192, hi = 32768, reps = 20, split = 512;
     for (int i = 1; i + 1 < argc; i += 2) {
         const std::string k = argv[i];
         const std::uint32_t v = static_cast<std::uint32_t>(std::atoi(argv[i + 1]));
@@ -151,6 +153,7 @@ int main(int argc, char** argv) {
         else if (k == "--lo") lo = v;
         else if (k == "--hi") hi = v;
         else if (k == "--reps") reps = v;
+        else if (k == "--split") split = v;
     }
     check(seqs > 0 && lo > 0 && hi >= lo, "bad arguments");
     constexpr std::uint32_t kTpb = 16, kHkv = 8, kHq = 64, kD = 128;
@@ -254,6 +257,8 @@ int main(int argc, char** argv) {
     check(qvp_memcpy_htod(dq, q.data(), qn * 2, stream) == QVP_OK, "upload q");
     const float scale = 1.0f / std::sqrt(static_cast<float>(kD));
     PagedAttentionBatch attn, attn_plain;
+    attn.set_split_tokens(split);
+    attn_plain.set_split_tokens(split);
     check(attn.decode(tagged, ctx, 0, kHq, scale, dq, dout, ElementType::BF16), attn.last_error());
     check(attn_plain.decode(plain, ctx, 0, kHq, scale, dq, dout2, ElementType::BF16), attn_plain.last_error());
     check(qvp_stream_synchronize(stream) == QVP_OK, "sync");
@@ -364,13 +369,13 @@ int main(int argc, char** argv) {
         "\"tagged_equals_untagged_bitwise\": %s, \"step_us_median\": %.3f, \"step_tokens_per_s\": %.1f, "
         "\"decode_us_median\": %.3f, \"decode_GBps\": %.1f, "
         "\"decode_frac_of_8TBps\": %.4f, \"decode_tokens_per_s\": %.1f, \"plan\": {\"kernel\": %u, \"workgroups\": %u, "
-        "\"pieces\": %u, \"slots\": %u, \"kv_heads_per_segment\": %u, \"query_group\": %u}, \"checked_elements\": %zu, "
+        "\"pieces\": %u, \"slots\": %u, \"kv_heads_per_segment\": %u, \"split_tokens\": %u, \"query_group\": %u}, \"checked_elements\": %zu, "
         "\"worst_excess_over_tolerance\": %.3g, \"decode_within_tolerance\": %s}\n",
         seqs, static_cast<unsigned long long>(tokens), static_cast<unsigned long long>(image_tokens),
         metadata_roundtrip ? "true" : "false", static_cast<unsigned long long>(rows), positions_ok ? "true" : "false",
         tagged_equals_plain ? "true" : "false", step_ms * 1e3, seqs / (step_ms * 1e-3), decode_ms * 1e3, (kv_bytes + qo) / (decode_ms * 1e-3) / 1e9,
         (kv_bytes + qo) / (decode_ms * 1e-3) / 8e12, seqs / (decode_ms * 1e-3), plan.kernel, plan.workgroups,
-        plan.pieces, plan.slots, plan.kv_heads_per_segment, plan.query_group, checked, worst,
+        plan.pieces, plan.slots, plan.kv_heads_per_segment, plan.split_tokens, plan.query_group, checked, worst,
         worst <= 0.0 ? "true" : "false");
     (void)qvp_free(dq);
     (void)qvp_free(dout);

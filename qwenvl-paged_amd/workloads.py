@@ -119,7 +119,9 @@ class Workload:
     num_pool_blocks: int
     seed: int
     layer: int = 0
-    split_tokens: int = 512
+    # 0: the library default (512-token partitions for the split kernels,
+    # free cost-balanced cuts for the persistent kernel).
+    split_tokens: int = 0
     q_sigma: float = 1.0
     kv_sigma: float = 1.0
     notes: dict = field(default_factory=dict)
@@ -224,7 +226,7 @@ def config3(seed: int = 3, num_seqs: int = 32, ctx_lo: int = 8192, ctx_hi: int =
     order = shuffled_allocation_order(pool, seed)
     ids, cu = _tables_from_order(order, ctx, 16)
     w = Workload("config3", 16, 1, 64, 8, 128, DTYPE_BF16, 1.0 / math.sqrt(128.0), ctx, ids, cu, pool, seed,
-                 q_sigma=1.0, kv_sigma=0.5)
+                 q_sigma=1.0, kv_sigma=0.5, split_tokens=512)
     w.notes["image_spans"] = [(0, int(c) // 4) for c in ctx]
     return w
 
@@ -232,7 +234,7 @@ def config3(seed: int = 3, num_seqs: int = 32, ctx_lo: int = 8192, ctx_hi: int =
 def custom(context_lens, num_query_heads: int, num_kv_heads: int, head_dim: int, kv_dtype: int = DTYPE_BF16,
            tokens_per_block: int = 16, num_layers: int = 1, seed: int = 7, spare: float = 0.25,
            scale: float | None = None, layer: int = 0, q_sigma: float = 1.0, kv_sigma: float = 0.5,
-           split_tokens: int = 512) -> Workload:
+           split_tokens: int = 0) -> Workload:
     """Any shape, with a shuffled pool holding `spare` extra free frames."""
     ctx = np.asarray(context_lens, dtype=np.uint32)
     need = int(((ctx.astype(np.int64) + tokens_per_block - 1) // tokens_per_block).sum())

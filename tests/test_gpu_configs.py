@@ -102,13 +102,14 @@ def test_long_context_multimodal_configuration_full_size():
     patch grid, then a Text1D span). metadata() returns what was given, the
     M-RoPE positions of every token equal the closed form, the decode over the
     tagged sequences equals the decode over untagged forks bit for bit, and
-    sampled heads match float64 attention."""
+    sampled heads match float64 attention. The decode runs with config3's
+    split-K partitions of 512 tokens (the plan reports them)."""
     r = run("config3_bench")
     assert r["sequences"] == 32 and r["image_tokens"] > 0
     assert r["metadata_roundtrip"] and r["positions_match_closed_form"]
     assert r["tagged_equals_untagged_bitwise"]
     assert r["decode_within_tolerance"] and r["checked_elements"] == 4 * 8 * 128
-    assert r["plan"]["query_group"] == 8
+    assert r["plan"]["query_group"] == 8 and r["plan"]["split_tokens"] == 512
 
 
 @pytest.mark.gpu

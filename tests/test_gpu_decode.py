@@ -78,24 +78,37 @@ def test_split_kernels_follow_the_split_size(kv_dtype, split):
         assert_close_bf16(got, ref32, f"fp16 split={split}")
 
 
-def test_mfma_path_ignores_the_split_size():
-    """The bf16 MFMA kernel cuts the batch into cost-balanced tile ranges
-    instead of split_tokens partitions: every split size packs to the same
-    schedule and the same bits."""
-    w = W.config2(seed=11, num_seqs=8)
+def test_mfma_path_holds_its_cuts_to_the_split_partition():
+    """Without split_tokens the bf16 MFMA kernel cuts the batch into tile
+    ranges by cost alone; with one, every range starts and ends on a
+    split_tokens partition boundary of its sequence. Each range of one kv-head
+    group is then a run of whole partitions, so a group holds at most one
+    piece per partition -- far fewer than the cost cuts make on one long
+    sequence -- and the results stay within the bf16 bound of the oracle."""
+    w = W.custom([4096, 1500, 700, 129], 28, 4, 128, seed=11)
     run = GpuRun(w)
     _, ref32 = oracle_decode(w, run.image, run.query)
-    first = None
+    print("case: mfma path, cost cuts", flush=True)
+    free = run.decode(out_dtype=qvp.DTYPE_F32, split_tokens=0)
+    plan0 = run.batch.decode_plan()
+    assert plan0["kernel"] == "mfma" and plan0["split_tokens"] == 0, plan0
+    assert_close_bf16(free, ref32, "mfma cost cuts")
+    lens = w.context_lens
     for split in (128, 512, 4096):
         print(f"case: mfma path split={split}", flush=True)
         got = run.decode(out_dtype=qvp.DTYPE_F32, split_tokens=split)
         plan = run.batch.decode_plan()
-        assert plan["kernel"] == "mfma" and plan["split_tokens"] == 0, plan
-        if first is None:
-            first = got
-            assert_close_bf16(got, ref32, "mfma path")
-        else:
-            assert np.array_equal(first.view(np.uint32), got.view(np.uint32)), f"split {split} changed the bits"
+        assert plan["kernel"] == "mfma" and plan["split_tokens"] == split, plan
+        groups = 4 // plan["kv_heads_per_segment"]
+        partitions = sum(-(-int(n) // split) for n in lens)
+        assert plan["pieces"] <= groups * partitions, (plan, partitions)
+        assert_close_bf16(got, ref32, f"mfma split {split}")
+        again = run.decode(out_dtype=qvp.DTYPE_F32, split_tokens=split)
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), f"split {split} not deterministic"
+    # One partition per sequence: one piece per sequence and group, as many as
+    # the free cuts would make only if they never split a sequence.
+    assert plan["pieces"] == groups * len(lens), plan
+    assert plan0["pieces"] > groups * len(lens), plan0
 
 
 EDGE_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 511, 512, 513, 1000]
