@@ -111,6 +111,38 @@ def test_mfma_path_holds_its_cuts_to_the_split_partition():
     assert plan0["pieces"] > groups * len(lens), plan0
 
 
+def test_merge_state_carries_nothing_between_launches():
+    """Each launch leaves the in-kernel merge's state (segment counters, split
+    slots) ready for the next: decoding two queries in turn on one packed
+    batch -- with a differently shaped batch decoded on the same batch object
+    in between -- gives each query's output bit for bit as a fresh batch
+    decodes it."""
+    w = W.config2(seed=21, num_seqs=16)
+    qa = w.query()
+    qb = W.config2(seed=22, num_seqs=16).query()
+    image = w.pool_image()
+    fresh = {}
+    for key, q in (("a", qa), ("b", qb)):
+        print(f"case: fresh batch, query {key}", flush=True)
+        fresh[key] = GpuRun(w, image=image, query=q).decode(out_dtype=qvp.DTYPE_F32)
+    run = GpuRun(w, image=image, query=qa)
+    qbuf = {"a": run.q, "b": qvp.DeviceBuffer.from_array(qb)}
+    short = W.custom([100, 900, 3000, 4000], 28, 4, 128, seed=5)
+    run_s = GpuRun(short)
+    _, ref_s = oracle_decode(short, run_s.image, run_s.query)
+    for i, key in enumerate("ababba"):
+        print(f"case: launch {i} query {key}", flush=True)
+        run.q = qbuf[key]
+        got = run.decode(out_dtype=qvp.DTYPE_F32)
+        assert run.batch.decode_plan()["slots"] > 0
+        assert np.array_equal(got.view(np.uint32), fresh[key].view(np.uint32)), f"launch {i} (query {key}) differs"
+        if i == 2:
+            run_s.batch = run.batch
+            got_s = run_s.decode(out_dtype=qvp.DTYPE_F32)
+            assert run.batch.decode_plan()["kernel"] == "mfma"
+            assert_close_bf16(got_s, ref_s, "other batch on the same batch object")
+
+
 EDGE_LENGTHS = [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 255, 511, 512, 513, 1000]
 
 
