@@ -92,6 +92,8 @@ def reference() -> ctypes.CDLL:
         lib.ref_session_decode.restype = c_int
         lib.ref_session_decode.argtypes = [c_void_p, c_uint32, _u32p, _u32p, _u32p, c_int, c_void_p, c_uint32,
                                            c_uint32, c_float, c_void_p, POINTER(c_double)]
+        lib.ref_session_decode_threads.restype = c_int
+        lib.ref_session_decode_threads.argtypes = list(lib.ref_session_decode.argtypes) + [c_uint32]
         lib.ref_block_byte_size.restype = c_uint64
         lib.ref_block_byte_size.argtypes = [c_uint32] * 5
         lib.ref_block_size_bytes.restype = c_uint64
@@ -202,7 +204,7 @@ class RefSession:
                                                 d, bpe)
 
     def decode(self, ids, cu_blocks, context_lens, dtype: int, query: np.ndarray, layer: int, hq: int, d: int,
-               scale: float) -> tuple[int, np.ndarray, float]:
+               scale: float, threads: int = 1) -> tuple[int, np.ndarray, float]:
         ids_a, ids_p = _u32(ids)
         cu_a, cu_p = _u32(cu_blocks)
         ctx_a, ctx_p = _u32(context_lens)
@@ -211,8 +213,13 @@ class RefSession:
         out = np.zeros((B, hq, d), dtype=np_dtype)
         q = np.ascontiguousarray(query)
         secs = c_double(0.0)
-        refused = reference().ref_session_decode(self.h, B, ids_p, cu_p, ctx_p, dtype, q.ctypes.data, layer, hq,
-                                                 scale, out.ctypes.data, ctypes.byref(secs))
+        if threads > 1:
+            refused = reference().ref_session_decode_threads(self.h, B, ids_p, cu_p, ctx_p, dtype, q.ctypes.data,
+                                                             layer, hq, scale, out.ctypes.data, ctypes.byref(secs),
+                                                             threads)
+        else:
+            refused = reference().ref_session_decode(self.h, B, ids_p, cu_p, ctx_p, dtype, q.ctypes.data, layer,
+                                                     hq, scale, out.ctypes.data, ctypes.byref(secs))
         return refused, out, secs.value
 
     def close(self):

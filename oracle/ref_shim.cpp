@@ -21,7 +21,9 @@
 
 #include <immintrin.h>
 
+#include <atomic>
 #include <chrono>
+#include <thread>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -77,10 +79,14 @@ struct Session {
     std::unique_ptr<MemoryAllocator> allocator;
 };
 
+// Decodes every sequence with the reference's paged_attention_decode<T>,
+// one call per sequence; with threads > 1 the sequences are dealt
+// round-robin to that many threads (the calls only read the allocator and
+// their own tables).
 template <typename T>
 int decode_all(Session& s, std::uint32_t num_seqs, const std::uint32_t* ids, const std::uint32_t* cu_blocks,
                const std::uint32_t* ctx_lens, const void* query, std::uint32_t layer, std::uint32_t hq,
-               float scale, void* out, double* seconds) {
+               float scale, void* out, double* seconds, std::uint32_t threads = 1) {
     const std::size_t per_seq = static_cast<std::size_t>(hq) * s.shape.head_dim;
     std::vector<BlockTable> tables;
     tables.reserve(num_seqs);
@@ -97,9 +103,9 @@ int decode_all(Session& s, std::uint32_t num_seqs, const std::uint32_t* ids, con
         }
         tables.push_back(std::move(table));
     }
-    int refused = 0;
-    const auto t0 = std::chrono::steady_clock::now();
-    for (std::uint32_t b = 0; b < num_seqs; ++b) {
+    std::atomic<int> refused{0};
+    auto run = [&](std::uint32_t first, std::uint32_t step) {
+        for (std::uint32_t b = first; b < num_seqs; b += step) {
         CacheView view;
         view.sequence_id = b + 1;
         view.block_table = &tables[b];
@@ -113,10 +119,19 @@ int decode_all(Session& s, std::uint32_t num_seqs, const std::uint32_t* ids, con
         const T* q = static_cast<const T*>(query) + b * per_seq;
         T* o = static_cast<T*>(out) + b * per_seq;
         if (!paged_attention_decode<T>(view, q, params, o)) ++refused;
+        }
+    };
+    const auto t0 = std::chrono::steady_clock::now();
+    if (threads <= 1) {
+        run(0, 1);
+    } else {
+        std::vector<std::thread> pool;
+        for (std::uint32_t t = 0; t < threads; ++t) pool.emplace_back(run, t, threads);
+        for (std::thread& th : pool) th.join();
     }
     const auto t1 = std::chrono::steady_clock::now();
     if (seconds != nullptr) *seconds = std::chrono::duration<double>(t1 - t0).count();
-    return refused;
+    return refused.load();
 }
 
 }  // namespace
@@ -159,6 +174,24 @@ int ref_session_decode(void* session, std::uint32_t num_seqs, const std::uint32_
     if (dtype == 0) return decode_all<float>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds);
     if (dtype == 1) return decode_all<Bf16>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds);
     if (dtype == 2) return decode_all<Half>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds);
+    return -1;
+}
+
+// ref_session_decode with the sequences spread over `threads` threads.
+int ref_session_decode_threads(void* session, std::uint32_t num_seqs, const std::uint32_t* ids,
+                               const std::uint32_t* cu_blocks, const std::uint32_t* ctx_lens, int dtype,
+                               const void* query, std::uint32_t layer, std::uint32_t hq, float scale, void* out,
+                               double* seconds, std::uint32_t threads) {
+    Session& s = *static_cast<Session*>(session);
+    if (dtype == 0) {
+        return decode_all<float>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds, threads);
+    }
+    if (dtype == 1) {
+        return decode_all<Bf16>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds, threads);
+    }
+    if (dtype == 2) {
+        return decode_all<Half>(s, num_seqs, ids, cu_blocks, ctx_lens, query, layer, hq, scale, out, seconds, threads);
+    }
     return -1;
 }
 
