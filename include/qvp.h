@@ -307,6 +307,26 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
                         uint32_t num_pool_blocks, uint32_t split_tokens, const qvp_decode_args* decode,
                         void* stream);
 
+/* qvp_pack_for_decode with its upload left pending: the packed arrays and
+ * schedule wait in the batch's pinned staging, and the next qvp_paged_decode
+ * of ANOTHER batch enqueued on `stream` that runs the persistent bf16 kernel
+ * copies them in extra workgroups of its own launch, which get a CU only as
+ * that decode's workgroups finish (so the upload runs in the launch's tail
+ * instead of as a kernel of its own between two decodes). A decode or
+ * prefill of this batch itself, or qvp_batch_upload, enqueues the upload
+ * first if it is still pending; a later pack of this batch discards it. For
+ * an engine that packs step n + 1 on one batch object while step n decodes
+ * from another (two batches used in turn). Until the upload is enqueued the
+ * device arrays of qvp_batch_view hold the previous pack's contents. No
+ * reference counterpart (the reference resolves blocks per token,
+ * PagedAttention.h:73-89). */
+int qvp_pack_ahead(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids, const uint32_t* cu_blocks,
+                   const uint32_t* context_lens, uint32_t tokens_per_block, uint32_t num_pool_blocks,
+                   uint32_t split_tokens, const qvp_decode_args* decode, void* stream);
+/* Enqueues on `stream` the upload a qvp_pack_ahead of this batch left
+ * pending (nothing to do otherwise). */
+int qvp_batch_upload(qvp_batch* batch, void* stream);
+
 /* qvp_paged_decode for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid allocation). No
  * counterpart in the reference. It calls no hipMalloc, hipHostMalloc,

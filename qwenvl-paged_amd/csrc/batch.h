@@ -101,6 +101,12 @@ struct qvp_batch {
     size_t device_cap[2]{0, 0};    // in int32 elements
     qvp_reader readers[2];         // last decode / prefill that read each slot
     hipStream_t upload_stream[2]{nullptr, nullptr};  // stream of each slot's upload
+    // A pack made with qvp_pack_ahead whose upload has not been enqueued yet:
+    // its bytes wait in staging[slot] until a decode on upload_stream[slot]
+    // carries them, or the batch's own decode / prefill / qvp_batch_upload
+    // enqueues them.
+    bool upload_pending[2]{false, false};
+    size_t upload_bytes[2]{0, 0};
     bool valid{false};
     uint64_t generation{0};            // bumped by every successful pack
     // Partition of the split-K cuts the caller asked for, in 32-token tiles (0:
@@ -120,6 +126,24 @@ struct qvp_batch {
 };
 
 namespace qvp {
+// A pack's upload taken over by a decode launch: 16-byte words src -> dst
+// (src is the device mapping of the pinned staging), then `tail` 4-byte
+// words after them.
+struct PendingUpload {
+    qvp_batch* batch{nullptr};
+    int slot{0};
+    const void* src{nullptr};
+    void* dst{nullptr};
+    size_t n16{0};
+    uint32_t tail{0};
+};
+// Enqueues the batch's own pending upload (its current pack) on `stream`.
+int flush_own_upload(qvp_batch* batch, hipStream_t stream);
+// Takes one pending upload registered on `stream` by a batch other than
+// `exclude`; returns false when there is none. The caller enqueues the copy
+// and then calls finish_taken_upload on the same stream.
+bool take_pending_upload(hipStream_t stream, const qvp_batch* exclude, PendingUpload* out);
+int finish_taken_upload(const PendingUpload& u, hipStream_t stream);
 // Makes `stream` wait on the device for a buffer's last reader when that
 // reader was enqueued on another stream.
 int wait_for_reader(qvp_reader& r, hipStream_t stream);

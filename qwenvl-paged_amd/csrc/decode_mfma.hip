@@ -103,6 +103,13 @@ struct MfmaArgs {
     void* out;      // [num_seqs][Hq][128]
     int hps;        // kv heads per segment (4, 2 or 1)
     int defer;      // hold piece results in LDS and write them after the range
+    // Workgroups past num_decode_wgs copy another pack's pending upload:
+    // up_n16 16-byte words up_src -> up_dst, then up_tail 4-byte words.
+    int num_decode_wgs;
+    const uint4* up_src;
+    uint4* up_dst;
+    uint64_t up_n16;
+    uint32_t up_tail;
 };
 
 
@@ -211,6 +218,20 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     // Piece results held until the range is done (a.defer): [piece][hps *
     // G][kD] accumulators, then [piece][hps * G][2] (m, l).
     extern __shared__ float sm_def[];
+
+    // A copy workgroup: launched after the decode workgroups, it only gets a
+    // CU once one of them has finished (one decode workgroup fills a CU), so
+    // the next step's upload runs in this launch's tail. One 16-byte read of
+    // pinned host memory per thread.
+    if (static_cast<int>(blockIdx.x) >= a.num_decode_wgs) {
+        const uint64_t i = static_cast<uint64_t>(blockIdx.x - a.num_decode_wgs) * kThreads + threadIdx.x;
+        if (i < a.up_n16) a.up_dst[i] = a.up_src[i];
+        if (static_cast<int>(blockIdx.x) == a.num_decode_wgs && threadIdx.x < a.up_tail) {
+            reinterpret_cast<uint32_t*>(a.up_dst + a.up_n16)[threadIdx.x] =
+                reinterpret_cast<const uint32_t*>(a.up_src + a.up_n16)[threadIdx.x];
+        }
+        return;
+    }
 
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
@@ -1059,7 +1080,7 @@ uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t h
 }
 
 int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t out_dtype, void* out,
-                       void* workspace, hipEvent_t split_event, hipStream_t stream) {
+                       void* workspace, hipEvent_t split_event, hipStream_t stream, const PendingUpload* upload) {
     const qvp_schedule& s = batch->sched;
     MfmaArgs a{};
     a.wg_begin = s.words + s.off_wg_begin;
@@ -1072,12 +1093,21 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     a.out = out;
     a.hps = static_cast<int>(s.hps);
     a.defer = s.defer ? 1 : 0;
+    a.num_decode_wgs = static_cast<int>(s.num_wgs);
+    uint32_t copy_wgs = 0;
+    if (upload != nullptr) {
+        a.up_src = static_cast<const uint4*>(upload->src);
+        a.up_dst = static_cast<uint4*>(upload->dst);
+        a.up_n16 = upload->n16;
+        a.up_tail = upload->tail;
+        copy_wgs = static_cast<uint32_t>(std::max<uint64_t>(1, (upload->n16 + kThreads - 1) / kThreads));
+    }
     if (s.tile_group != g.tile_group) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "the batch's schedule was planned for another tile engine");
     }
     DecodeGeometry gk = g;
     void* kargs[] = {&gk, &a};
-    QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs), dim3(kThreads), kargs,
+    QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs + copy_wgs), dim3(kThreads), kargs,
                             s.lds_bytes, stream));
     // The merge runs inside the kernel; the event still marks the split/merge
     // boundary for callers that time the two phases.

@@ -18,7 +18,9 @@
 #include "decode_common.h"
 
 #include <algorithm>
+#include <mutex>
 #include <new>
+#include <vector>
 
 namespace {
 
@@ -52,7 +54,67 @@ Layout make_layout(uint32_t num_seqs, uint32_t max_nb, uint32_t num_splits) {
     return l;
 }
 
+// Batches whose last pack (qvp_pack_ahead) still waits in staging, in the
+// order they were packed.
+std::mutex g_pending_mutex;
+std::vector<qvp_batch*> g_pending;
+
+void unregister_pending(qvp_batch* batch) {
+    std::lock_guard<std::mutex> lock(g_pending_mutex);
+    g_pending.erase(std::remove(g_pending.begin(), g_pending.end(), batch), g_pending.end());
+}
+
+// The upload of `slot` as a PendingUpload (device mapping of its staging).
+int describe_upload(qvp_batch* batch, int slot, qvp::PendingUpload* u) {
+    void* src = nullptr;
+    QVP_HIP(hipHostGetDevicePointer(&src, batch->staging[slot], 0));
+    const size_t bytes = batch->upload_bytes[slot];
+    u->batch = batch;
+    u->slot = slot;
+    u->src = src;
+    u->dst = batch->device[slot];
+    u->n16 = bytes / 16;
+    u->tail = static_cast<uint32_t>((bytes % 16) / 4);
+    return QVP_OK;
+}
+
 }  // namespace
+
+namespace qvp {
+
+int finish_taken_upload(const PendingUpload& u, hipStream_t stream) {
+    qvp_batch* b = u.batch;
+    QVP_HIP(hipEventRecord(b->staging_done[u.slot], stream));
+    b->staging_pending[u.slot] = true;
+    b->upload_stream[u.slot] = stream;
+    b->upload_pending[u.slot] = false;
+    return QVP_OK;
+}
+
+int flush_own_upload(qvp_batch* batch, hipStream_t stream) {
+    const int slot = batch->current;
+    if (!batch->upload_pending[slot]) return QVP_OK;
+    unregister_pending(batch);
+    QVP_TRY(pull_from_pinned(batch->device[slot], batch->staging[slot], batch->upload_bytes[slot], stream));
+    PendingUpload u{};
+    u.batch = batch;
+    u.slot = slot;
+    return finish_taken_upload(u, stream);
+}
+
+bool take_pending_upload(hipStream_t stream, const qvp_batch* exclude, PendingUpload* out) {
+    std::lock_guard<std::mutex> lock(g_pending_mutex);
+    for (size_t i = 0; i < g_pending.size(); ++i) {
+        qvp_batch* b = g_pending[i];
+        if (b == exclude || b->upload_stream[b->current] != stream || !b->upload_pending[b->current]) continue;
+        if (describe_upload(b, b->current, out) != QVP_OK) return false;
+        g_pending.erase(g_pending.begin() + static_cast<std::ptrdiff_t>(i));
+        return true;
+    }
+    return false;
+}
+
+}  // namespace qvp
 
 using qvp::fail;
 
@@ -77,6 +139,7 @@ int qvp_batch_create(qvp_batch** batch) {
 
 int qvp_batch_destroy(qvp_batch* batch) {
     if (batch == nullptr) return QVP_OK;
+    unregister_pending(batch);
     int status = QVP_OK;
     // Decodes may still read the buffers.
     if (batch->readers[0].pending || batch->readers[1].pending || batch->sched.reader.pending) {
@@ -113,10 +176,15 @@ int qvp_pack(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
                                num_pool_blocks, split_tokens, nullptr, stream);
 }
 
-int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
-                        const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
-                        uint32_t num_pool_blocks, uint32_t split_tokens, const qvp_decode_args* decode,
-                        void* stream) {
+}  // extern "C"
+
+namespace {
+
+// qvp_pack_for_decode; with defer_upload the upload is left pending (see
+// qvp_pack_ahead).
+int pack_impl(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids, const uint32_t* cu_blocks,
+              const uint32_t* context_lens, uint32_t tokens_per_block, uint32_t num_pool_blocks,
+              uint32_t split_tokens, const qvp_decode_args* decode, void* stream, bool defer_upload) {
     if (batch == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "batch is NULL");
     if (tokens_per_block == 0) return fail(QVP_ERR_INVALID_ARGUMENT, "tokens_per_block is 0");
     if (num_seqs > 0 && (cu_blocks == nullptr || context_lens == nullptr)) {
@@ -213,6 +281,11 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
     }
     const size_t total = lay.total + (with_schedule ? batch->sched.total : 0);
 
+    // A pack still waiting for its upload (qvp_pack_ahead) is superseded.
+    if (batch->upload_pending[0] || batch->upload_pending[1]) {
+        unregister_pending(batch);
+        batch->upload_pending[0] = batch->upload_pending[1] = false;
+    }
     // The staging buffer about to be reused may still be read by the upload
     // of the call before last.
     if (batch->staging_pending[slot]) {
@@ -273,21 +346,27 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
     if (with_schedule) qvp::mfma_write_schedule(batch->sched, sin, h + lay.total);
 
     // The pack before last (same slot) may still be read by a decode on
-    // another stream; one upload then carries the arrays and the schedule.
+    // another stream; one upload then carries the arrays and the schedule
+    // (now, or left pending for a later decode on `s`).
     int st = qvp::wait_for_reader(batch->readers[slot], s);
-    if (st == QVP_OK) st = qvp::pull_from_pinned(batch->device[slot], h, total * sizeof(int32_t), s);
+    if (st == QVP_OK && !defer_upload) st = qvp::pull_from_pinned(batch->device[slot], h, total * sizeof(int32_t), s);
     if (st != QVP_OK) {
         batch->valid = false;
         batch->sched.valid = false;
         return st;
     }
-    hipError_t err = hipEventRecord(batch->staging_done[slot], s);
-    if (err != hipSuccess) {
-        batch->valid = false;
-        batch->sched.valid = false;
-        return qvp::hip_fail(err, "hipEventRecord(pack)");
+    if (defer_upload) {
+        batch->upload_pending[slot] = true;
+        batch->upload_bytes[slot] = total * sizeof(int32_t);
+    } else {
+        hipError_t err = hipEventRecord(batch->staging_done[slot], s);
+        if (err != hipSuccess) {
+            batch->valid = false;
+            batch->sched.valid = false;
+            return qvp::hip_fail(err, "hipEventRecord(pack)");
+        }
+        batch->staging_pending[slot] = true;
     }
-    batch->staging_pending[slot] = true;
     batch->upload_stream[slot] = s;
     batch->parity ^= 1;
     batch->current = slot;
@@ -332,7 +411,36 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
     batch->partition_tiles = explicit_split ? split_tokens / qvp::kScheduleTileTokens : 0u;
     batch->last_plan = qvp_decode_plan{};
     batch->valid = true;
+    if (defer_upload) {
+        std::lock_guard<std::mutex> lock(g_pending_mutex);
+        g_pending.push_back(batch);
+    }
     return QVP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids,
+                        const uint32_t* cu_blocks, const uint32_t* context_lens, uint32_t tokens_per_block,
+                        uint32_t num_pool_blocks, uint32_t split_tokens, const qvp_decode_args* decode,
+                        void* stream) {
+    return pack_impl(batch, num_seqs, block_ids, cu_blocks, context_lens, tokens_per_block, num_pool_blocks,
+                     split_tokens, decode, stream, false);
+}
+
+int qvp_pack_ahead(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids, const uint32_t* cu_blocks,
+                   const uint32_t* context_lens, uint32_t tokens_per_block, uint32_t num_pool_blocks,
+                   uint32_t split_tokens, const qvp_decode_args* decode, void* stream) {
+    return pack_impl(batch, num_seqs, block_ids, cu_blocks, context_lens, tokens_per_block, num_pool_blocks,
+                     split_tokens, decode, stream, true);
+}
+
+int qvp_batch_upload(qvp_batch* batch, void* stream) {
+    if (batch == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "batch is NULL");
+    if (!batch->valid) return QVP_OK;
+    return qvp::flush_own_upload(batch, qvp::as_stream(stream));
 }
 
 }  // extern "C"

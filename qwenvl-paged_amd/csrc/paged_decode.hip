@@ -230,11 +230,18 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
     } else if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     }
+    // A pack left pending by qvp_pack_ahead is uploaded before its decode.
+    QVP_TRY(qvp::flush_own_upload(batch, s));
     qvp_decode_plan plan{};
     plan.query_group = g.group;
     int status = QVP_OK;
     if (mfma) {
-        status = qvp::launch_mfma_decode(g, batch, a->out_dtype, a->out, ws, ev, s);
+        // Another batch's pending upload on this stream (the next step,
+        // packed ahead) rides in this launch's tail.
+        qvp::PendingUpload up{};
+        const bool carry = qvp::take_pending_upload(s, batch, &up);
+        status = qvp::launch_mfma_decode(g, batch, a->out_dtype, a->out, ws, ev, s, carry ? &up : nullptr);
+        if (carry && status == QVP_OK) status = qvp::finish_taken_upload(up, s);
         const qvp_schedule& sc = batch->sched;
         plan.kernel = QVP_DECODE_MFMA;
         plan.workgroups = sc.num_wgs;

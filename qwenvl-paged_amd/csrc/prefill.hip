@@ -397,6 +397,8 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
     g.scale_log2 = a->scale * qvp::kLog2e;
     hipStream_t s = qvp::as_stream(stream);
     qvp_prefill_plan& plan = batch->prefill;
+    // A pack left pending by qvp_pack_ahead is uploaded before its prefill.
+    QVP_TRY(qvp::flush_own_upload(batch, s));
 
     // The MFMA kernel takes its running maximum on raw scores: scale > 0.
     if (!(a->scale > 0.0f) || !qvp::prefill_mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),

@@ -198,6 +198,9 @@ SIGNATURES = {
     "qvp_paged_decode_noalloc": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "qvp_pack_for_decode": (c_int, [c_void_p, c_uint32, _u32p, _u32p, _u32p, c_uint32, c_uint32, c_uint32,
                                     c_void_p, c_void_p]),
+    "qvp_pack_ahead": (c_int, [c_void_p, c_uint32, _u32p, _u32p, _u32p, c_uint32, c_uint32, c_uint32,
+                                    c_void_p, c_void_p]),
+    "qvp_batch_upload": (c_int, [c_void_p, c_void_p]),
     "qvp_copy_blocks": (c_int, [c_void_p, c_uint64, c_uint32, _u32p, _u32p, c_uint32, c_uint64, c_void_p]),
     "qvp_swap_gather": (
         c_int,
@@ -480,13 +483,20 @@ class Batch:
         self.handle = p.value
 
     def pack(self, ids, cu_blocks, context_lens, tokens_per_block: int, num_pool_blocks: int,
-             split_tokens: int = 0, stream=None, decode: "DecodeArgs | None" = None) -> PackedView:
-        """qvp_pack, or qvp_pack_for_decode when the decode the pack is for is given."""
+             split_tokens: int = 0, stream=None, decode: "DecodeArgs | None" = None,
+             ahead: bool = False) -> PackedView:
+        """qvp_pack, or qvp_pack_for_decode when the decode the pack is for is
+        given; with ahead=True qvp_pack_ahead (the upload left pending for the
+        next decode of another batch on the stream)."""
         ids_a, ids_p = _u32(ids if len(ids) else np.zeros(1, np.uint32))
         cu_a, cu_p = _u32(cu_blocks)
         ctx_a, ctx_p = _u32(context_lens)
         num_seqs = len(ctx_a)
-        if decode is None:
+        if ahead:
+            check(load().qvp_pack_ahead(self.handle, num_seqs, ids_p, cu_p, ctx_p, tokens_per_block,
+                                        num_pool_blocks, split_tokens, byref(decode) if decode is not None else None,
+                                        _sp(stream)))
+        elif decode is None:
             check(load().qvp_pack(self.handle, num_seqs, ids_p, cu_p, ctx_p, tokens_per_block, num_pool_blocks,
                                   split_tokens, _sp(stream)))
         else:
@@ -494,6 +504,10 @@ class Batch:
                                              num_pool_blocks, split_tokens, byref(decode), _sp(stream)))
         # The library copies from pinned staging, so the numpy inputs may go now.
         return self.view()
+
+    def upload(self, stream=None) -> None:
+        """qvp_batch_upload: enqueue a pending pack-ahead upload now."""
+        check(load().qvp_batch_upload(self.handle, _sp(stream)))
 
     def view(self) -> PackedView:
         v = PackedView()

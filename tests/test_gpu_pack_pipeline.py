@@ -5,6 +5,8 @@ device buffers). Every decode is compared with the oracle."""
 
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -125,3 +127,101 @@ def test_packs_on_a_second_stream_overlap_running_decodes(hinted):
         print(f"case: pipelined step {i} hinted={hinted}", flush=True)
         got = outs[i].download(np.float32, (w.num_seqs, 28, 128))
         assert_close_bf16(got, refs[i % 2], f"pipelined step {i}")
+
+
+def _plain_decode(run: GpuRun, w: W.Workload, lens: np.ndarray) -> np.ndarray:
+    """A fresh batch, packed with its upload and decoded: the reference bits."""
+    batch = qvp.Batch()
+    out = qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4)
+    a = _args(run, w, run.q, out, batch)
+    batch.pack(w.ids, w.cu_blocks, lens, 16, w.num_pool_blocks, decode=a)
+    qvp.paged_decode(a)
+    return out.download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim))
+
+
+def test_pack_ahead_upload_rides_in_the_other_batchs_decode():
+    """Two batch objects in turn, the pattern qvp_pack_ahead is for: step i + 1
+    is packed ahead on one while step i decodes from the other. The decode of
+    step i carries step i + 1's upload in the tail of its launch -- once it has
+    run, the other batch's device arrays hold step i + 1's lengths, before any
+    decode of that batch -- and every step's output equals, bit for bit, a
+    plain pack-then-decode of the same step (and the oracle for one step)."""
+    w = W.config2(seed=41, num_seqs=16)
+    run = GpuRun(w)
+    batches = [qvp.Batch(), qvp.Batch()]
+    steps = 6
+    lens = [np.maximum(w.context_lens.astype(np.int64) - 40 * i, 1).astype(np.uint32) for i in range(steps)]
+    outs = [qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4) for _ in range(steps)]
+    args = [_args(run, w, run.q, outs[i], batches[i % 2]) for i in range(steps)]
+    s = qvp.Stream()
+    batches[0].pack(w.ids, w.cu_blocks, lens[0], 16, w.num_pool_blocks, stream=s, decode=args[0])
+    for i in range(steps):
+        print(f"case: pack-ahead step {i}", flush=True)
+        if i + 1 < steps:
+            batches[(i + 1) % 2].pack(w.ids, w.cu_blocks, lens[i + 1], 16, w.num_pool_blocks, stream=s,
+                                      decode=args[i + 1], ahead=True)
+        qvp.paged_decode(args[i], s)
+        assert batches[i % 2].decode_plan()["kernel"] == "mfma"
+        if i + 1 < steps:
+            s.synchronize()
+            assert batches[(i + 1) % 2].download()["seq_lens"].tolist() == lens[i + 1].astype(np.int64).tolist()
+    s.synchronize()
+    for i in range(steps):
+        got = outs[i].download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim))
+        ref = _plain_decode(run, w, lens[i])
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"step {i} differs from a plain pack"
+    w_last = dataclasses.replace(w, context_lens=lens[-1])
+    _, ref32 = oracle_decode(w_last, run.image, run.query)
+    got = outs[-1].download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim))
+    assert_close_bf16(got, ref32, "last pack-ahead step")
+
+
+def test_pack_ahead_without_a_carrier():
+    """A pending upload that no other decode carries: the batch's own decode
+    enqueues it first; qvp_batch_upload enqueues it on request; a later pack
+    of the batch discards it; a split-kernel decode of another batch leaves
+    it pending; destroying the batch with it pending is safe."""
+    w = W.config2(seed=43, num_seqs=12)
+    run = GpuRun(w)
+    s = qvp.Stream()
+    lens1 = np.maximum(w.context_lens.astype(np.int64) - 100, 1).astype(np.uint32)
+    lens2 = np.maximum(w.context_lens.astype(np.int64) - 300, 1).astype(np.uint32)
+    b = qvp.Batch()
+    out = qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4)
+    a = _args(run, w, run.q, out, b)
+
+    print("case: own decode after pack-ahead", flush=True)
+    b.pack(w.ids, w.cu_blocks, lens1, 16, w.num_pool_blocks, stream=s, decode=a, ahead=True)
+    qvp.paged_decode(a, s)
+    got = out.download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim), s)
+    assert np.array_equal(got.view(np.uint32), _plain_decode(run, w, lens1).view(np.uint32))
+
+    print("case: upload on request", flush=True)
+    b.pack(w.ids, w.cu_blocks, lens2, 16, w.num_pool_blocks, stream=s, decode=a, ahead=True)
+    b.upload(s)
+    s.synchronize()
+    assert b.download()["seq_lens"].tolist() == lens2.astype(np.int64).tolist()
+
+    print("case: pack-ahead superseded by a plain pack", flush=True)
+    b.pack(w.ids, w.cu_blocks, lens1, 16, w.num_pool_blocks, stream=s, decode=a, ahead=True)
+    b.pack(w.ids, w.cu_blocks, lens2, 16, w.num_pool_blocks, stream=s, decode=a)
+    qvp.paged_decode(a, s)
+    got = out.download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim), s)
+    assert np.array_equal(got.view(np.uint32), _plain_decode(run, w, lens2).view(np.uint32))
+
+    print("case: a split-kernel decode of another batch leaves it pending", flush=True)
+    w64 = W.custom([300, 700, 1200], 28, 4, 64, seed=8)
+    run64 = GpuRun(w64)
+    b.pack(w.ids, w.cu_blocks, lens1, 16, w.num_pool_blocks, stream=s, decode=a, ahead=True)
+    run64.decode(out_dtype=qvp.DTYPE_F32, stream=s)
+    assert run64.batch.decode_plan()["kernel"] == "generic"
+    qvp.paged_decode(a, s)
+    got = out.download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim), s)
+    assert np.array_equal(got.view(np.uint32), _plain_decode(run, w, lens1).view(np.uint32))
+
+    print("case: destroy with a pending upload", flush=True)
+    c = qvp.Batch()
+    c.pack(w.ids, w.cu_blocks, lens1, 16, w.num_pool_blocks, stream=s, decode=a, ahead=True)
+    c.destroy()
+    qvp.paged_decode(a, s)  # no pending upload of a destroyed batch is carried
+    s.synchronize()
