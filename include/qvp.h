@@ -317,8 +317,9 @@ int qvp_pack_for_decode(qvp_batch* batch, uint32_t num_seqs, const uint32_t* blo
  * first if it is still pending; a later pack of this batch discards it. For
  * an engine that packs step n + 1 on one batch object while step n decodes
  * from another (two batches used in turn). Until the upload is enqueued the
- * device arrays of qvp_batch_view hold the previous pack's contents. No
- * reference counterpart (the reference resolves blocks per token,
+ * device arrays of qvp_batch_view hold the previous pack's contents. A
+ * decode under graph capture carries no pending upload and refuses a batch
+ * whose own upload is pending. No reference counterpart (the reference resolves blocks per token,
  * PagedAttention.h:73-89). */
 int qvp_pack_ahead(qvp_batch* batch, uint32_t num_seqs, const uint32_t* block_ids, const uint32_t* cu_blocks,
                    const uint32_t* context_lens, uint32_t tokens_per_block, uint32_t num_pool_blocks,

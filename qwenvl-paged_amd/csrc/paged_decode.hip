@@ -230,7 +230,16 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
     } else if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     }
-    // A pack left pending by qvp_pack_ahead is uploaded before its decode.
+    // A pack left pending by qvp_pack_ahead is uploaded before its decode;
+    // under graph capture the copy would replay from staging a later pack
+    // rewrites, so a capture neither uploads nor carries one.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    QVP_HIP(hipStreamIsCapturing(s, &capture));
+    const bool capturing = capture != hipStreamCaptureStatusNone;
+    if (capturing && batch->upload_pending[batch->current]) {
+        return fail(QVP_ERR_INVALID_ARGUMENT,
+                    "the batch's qvp_pack_ahead upload is still pending: enqueue it (qvp_batch_upload) before capture");
+    }
     QVP_TRY(qvp::flush_own_upload(batch, s));
     qvp_decode_plan plan{};
     plan.query_group = g.group;
@@ -239,7 +248,7 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         // Another batch's pending upload on this stream (the next step,
         // packed ahead) rides in this launch's tail.
         qvp::PendingUpload up{};
-        const bool carry = qvp::take_pending_upload(s, batch, &up);
+        const bool carry = !capturing && qvp::take_pending_upload(s, batch, &up);
         status = qvp::launch_mfma_decode(g, batch, a->out_dtype, a->out, ws, ev, s, carry ? &up : nullptr);
         if (carry && status == QVP_OK) status = qvp::finish_taken_upload(up, s);
         const qvp_schedule& sc = batch->sched;

@@ -596,6 +596,9 @@ class _Capture:
         if exc_type is None:
             check(rc)
             self.graph.handle = h.value
+        elif rc == 0 and h.value:
+            # The capture ended because its body raised: nothing to replay.
+            load().qvp_graph_destroy(h.value)
         return False
 
 

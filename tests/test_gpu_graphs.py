@@ -135,3 +135,63 @@ def test_capture_needs_a_created_stream():
     with pytest.raises(qvp.QvpError):
         with qvp.Graph.capture(None):
             pass
+
+
+def test_capture_neither_carries_nor_replays_a_pending_pack_ahead_upload():
+    """A decode captured while another batch's qvp_pack_ahead upload is
+    pending on the stream does not take it into the graph (replays would copy
+    whatever the staging holds then): the upload stays pending and the other
+    batch's own decode enqueues it. A decode of a batch whose own upload is
+    pending is refused under capture."""
+    w = W.custom([300, 2000, 513, 77, 1], 28, 4, 128, seed=31)
+    stream = qvp.Stream()
+    run = GpuRun(w)
+    run.batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, 0, stream)
+    ws = qvp.DeviceBuffer(max(run.batch.workspace_bytes(w.num_query_heads, w.head_dim), 256))
+    n = w.num_seqs * w.num_query_heads * w.head_dim
+    out = qvp.DeviceBuffer(n * 2)
+    args = _decode_args(run, out, ws, qvp.DTYPE_BF16)
+    qvp.paged_decode(args, stream)
+    eager = out.download(np.uint16, (n,), stream)
+
+    other = qvp.Batch()
+    lens = np.maximum(w.context_lens.astype(np.int64) - 50, 1).astype(np.uint32)
+    out2 = qvp.DeviceBuffer(n * 2)
+    args2 = qvp.decode_args(query=run.q.ptr, out=out2.ptr, kv_base=run.pool.base, block_stride=run.pool.stride,
+                            batch=other, kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_BF16, layer=w.layer,
+                            num_layers=w.num_layers, num_query_heads=w.num_query_heads,
+                            num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, tokens_per_block=w.tokens_per_block,
+                            scale=w.scale, strides=w.strides)
+    other.pack(w.ids, w.cu_blocks, lens, w.tokens_per_block, w.num_pool_blocks, 0, stream, decode=args2, ahead=True)
+    print("case: capture beside a pending upload", flush=True)
+    with qvp.Graph.capture(stream) as graph:
+        qvp.paged_decode(args, stream)
+    for replay in range(3):
+        out.fill(0xFF, stream)
+        graph.launch(stream)
+        stream.synchronize()
+        assert np.array_equal(out.download(np.uint16, (n,), stream), eager), f"replay {replay}"
+    graph.destroy()
+    # Still pending: the other batch's own decode uploads it first.
+    qvp.paged_decode(args2, stream)
+    got2 = out2.download(np.uint16, (n,), stream)
+    fresh = qvp.Batch()
+    out3 = qvp.DeviceBuffer(n * 2)
+    args3 = qvp.decode_args(query=run.q.ptr, out=out3.ptr, kv_base=run.pool.base, block_stride=run.pool.stride,
+                            batch=fresh, kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_BF16, layer=w.layer,
+                            num_layers=w.num_layers, num_query_heads=w.num_query_heads,
+                            num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, tokens_per_block=w.tokens_per_block,
+                            scale=w.scale, strides=w.strides)
+    fresh.pack(w.ids, w.cu_blocks, lens, w.tokens_per_block, w.num_pool_blocks, 0, stream, decode=args3)
+    qvp.paged_decode(args3, stream)
+    assert np.array_equal(got2, out3.download(np.uint16, (n,), stream))
+
+    print("case: capture of a batch with its own upload pending is refused", flush=True)
+    other.pack(w.ids, w.cu_blocks, lens, w.tokens_per_block, w.num_pool_blocks, 0, stream, decode=args2, ahead=True)
+    with pytest.raises(qvp.QvpError) as e:
+        with qvp.Graph.capture(stream):
+            qvp.paged_decode(args2, stream)
+    assert e.value.status == qvp.ERR_INVALID_ARGUMENT
+    other.upload(stream)
+    qvp.paged_decode(args2, stream)
+    assert np.array_equal(out2.download(np.uint16, (n,), stream), got2)
