@@ -776,13 +776,15 @@ void destroy_schedule(qvp_schedule& s) {
     s = qvp_schedule{};
 }
 
+// The tile math takes its running maximum on raw scores (scale > 0); other
+// scales go to the generic kernel.
 bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr, uintptr_t kv_base_addr) {
     const bool pow2 = g.tpb != 0 && (g.tpb & (g.tpb - 1)) == 0;
     const bool aligned = (g.block_stride % 16 == 0) && (g.k_off % 16 == 0) && (g.v_off % 16 == 0) &&
                          (g.token_stride % 16 == 0) && (g.head_stride % 16 == 0) && (kv_base_addr % 16 == 0) &&
                          (query_addr % 16 == 0);
     return kv_dtype == QVP_DTYPE_BF16 && g.head_dim == kD && g.group >= 1 && g.group <= 16 && pow2 && g.tpb >= 16 &&
-           aligned;
+           aligned && g.scale_log2 > 0.0f;
 }
 
 bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g) {

@@ -52,88 +52,6 @@ __device__ inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// One tile of online softmax + PV for the wave. Column c (this lane's c)
-// sees tokens t <= col_last; values of tokens at or past v_end are zeroed in
-// place (their weights are 0, but the bytes read for them are not data and
-// 0 * NaN would poison O).
-__device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0, int col_last, int v_end,
-                                    float scale_log2, int j, float& m_run, float& l_run, floatx4 (&o)[8]) {
-    float s[2][4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, cur.k[u][i]),
-                                                          __builtin_bit_cast(bf16x8_t, qop[i]), acc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tok = tok0 + j + 16 * u + 4 * r;
-            s[u][r] = (tok <= col_last) ? acc[r] * scale_log2 : -INFINITY;
-        }
-    }
-
-    // The four lanes (c, 0..3) of query head c share one running max.
-    float mt = s[0][0];
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mt = fmaxf(mt, s[u][r]);
-    mt = max_over_j(mt);
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-
-    float psum = 0.f;
-    uint32_t phi[4], plo[4];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int r = 0; r < 4; r += 2) {
-            const float p0 = fast_exp2(s[u][r] - m_new);
-            const float p1 = fast_exp2(s[u][r + 1] - m_new);
-            psum += p0 + p1;
-            const uint32_t h0 = __float_as_uint(p0) >> 16;
-            const uint32_t h1 = __float_as_uint(p1) >> 16;
-            const uint32_t l0 = float_to_bf16_bits(p0 - __uint_as_float(h0 << 16));
-            const uint32_t l1 = float_to_bf16_bits(p1 - __uint_as_float(h1 << 16));
-            phi[2 * u + r / 2] = h0 | (h1 << 16);
-            plo[2 * u + r / 2] = l0 | (l1 << 16);
-        }
-    }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) o[n] *= alpha;
-
-    const u32x4 bhi = {phi[0], phi[1], phi[2], phi[3]};
-    const u32x4 blo = {plo[0], plo[1], plo[2], plo[3]};
-    // Values of tokens past the context are zeroed in place (their weights are
-    // 0, but the bytes read for them are not data and 0 * NaN would poison O).
-    // Only the last tile of a sequence has such tokens.
-    if (tok0 + kTileTokens > v_end) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            if (tok0 + 4 * q + j >= v_end) cur.v[q] = u32x4{0u, 0u, 0u, 0u};
-        }
-    }
-    const u32x4 (&v)[8] = cur.v;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-        const int w = n >> 1;
-        u32x4 a;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t x = v[2 * k][w];
-            const uint32_t y = v[2 * k + 1][w];
-            a[k] = (n & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-        }
-        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bhi), o[n], 0, 0, 0);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, blo), o[n], 0, 0, 0);
-    }
-}
-
 // Pieces of the tile step for callers that stage K and V themselves (the
 // prefill reads V already transposed from LDS and runs several query tiles
 // per K/V tile).
@@ -198,6 +116,56 @@ __device__ inline void pv_tile(const u32x4 (&a)[8], const u32x4& bhi, const u32x
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
         const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a[n]);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bhi), o[n], 0, 0, 0);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, blo), o[n], 0, 0, 0);
+    }
+}
+
+// One tile of online softmax + PV for the wave (scale > 0: the running
+// maximum is taken on the raw scores, see softmax_p). Column c (this lane's
+// c) sees tokens t <= col_last; only a tile that reaches past col_last takes
+// the mask. Values of tokens at or past v_end are zeroed in place (their
+// weights are 0, but the bytes read for them are not data and 0 * NaN would
+// poison O); only the last tile of a sequence has such tokens. O is rescaled
+// only when some column's maximum moved. V's A operands come from the loaded
+// rows by byte permutes: lane (c, j) holds dims 8c .. 8c + 7 of tokens
+// 4q + j, and PV MFMA n takes element n of each, two tokens per dword.
+__device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0, int col_last, int v_end,
+                                    float scale_log2, int j, float& m_run, float& l_run, floatx4 (&o)[8]) {
+    floatx4 s[2];
+    qk_tile(cur.k, qop, s);
+    if (tok0 + kTileTokens - 1 > col_last) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (tok0 + j + 16 * u + 4 * r > col_last) s[u][r] = -INFINITY;
+            }
+    }
+    u32x4 bhi, blo;
+    float alpha;
+    softmax_p(s, scale_log2, m_run, l_run, bhi, blo, alpha);
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[n] *= alpha;
+    }
+    if (tok0 + kTileTokens > v_end) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if (tok0 + 4 * q + j >= v_end) cur.v[q] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const int w = n >> 1;
+        u32x4 a;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // Element n of tokens 2k and 2k + 1 of this lane's loads: their
+            // low halves (n even) or high halves (n odd), token 2k low.
+            a[k] = __builtin_amdgcn_perm(cur.v[2 * k + 1][w], cur.v[2 * k][w], (n & 1) ? 0x07060302u : 0x05040100u);
+        }
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, a);
         o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bhi), o[n], 0, 0, 0);
         o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, blo), o[n], 0, 0, 0);
     }

@@ -153,6 +153,20 @@ def test_ragged_lengths_across_block_and_split_edges(kv_dtype):
     _parity(w, out_dtypes=(qvp.DTYPE_F32,))
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.05, 0.004], ids=["zero", "negative", "small-positive"])
+def test_any_softmax_scale(scale):
+    """The persistent kernel takes its running maximum on raw scores, which
+    holds for scale > 0; a zero or negative scale (uniform weights, reversed
+    order of the scores) runs on the generic kernel. Both match the oracle."""
+    print(f"case: scale {scale}", flush=True)
+    w = W.custom([70, 300, 513, 2000], 28, 4, 128, seed=19, scale=scale)
+    run = GpuRun(w)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    assert run.batch.decode_plan()["kernel"] == ("mfma" if scale > 0 else "generic")
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    assert_close_bf16(got, ref32, f"scale {scale}")
+
+
 @pytest.mark.parametrize("hq,hkv", [(4, 4), (8, 4), (28, 4), (32, 4), (64, 4), (16, 1), (12, 2)])
 def test_grouped_query_head_shapes(hq, hkv):
     print(f"case: gqa hq={hq} hkv={hkv}", flush=True)
