@@ -79,10 +79,11 @@ constexpr int kMergeBatch = 2;
 
 // Cost of a piece boundary inside a range, in one wave's tile times: the
 // waves' LDS merge (a workgroup barrier) and the piece's stores, which the
-// next tile's wait then covers. Per-workgroup timestamps on the Qwen2-VL-7B
-// batch put it at ~2.3 us against ~5.3 us per tile; cutting ranges with it
-// shortened that kernel by ~2 us (0.3 to 0.6 measured, smooth).
-constexpr double kPieceBoundaryTiles = 0.5;
+// next tile's wait then covers. Per-wave timestamps of the Qwen2-VL-7B batch
+// (15 launches): with 0.5 a range's loop still ended ~0.9 us later per extra
+// piece (a wave-tile takes ~4.0 us in the steady state), so a boundary costs
+// ~0.7 tile times; with 0.7 the residue is ~0.5 us per piece.
+constexpr double kPieceBoundaryTiles = 0.7;
 
 // LDS of one workgroup: the CU's 160 KiB (one workgroup per CU), of which the
 // kernel's static arrays take kStaticLdsBytes; the rest can hold deferred
@@ -664,17 +665,23 @@ uint32_t head_group_size(uint32_t num_kv_heads, uint64_t tiles_per_head, uint32_
 // Relative streaming cost of kv head group q (hps heads from q * hps). On
 // MI355X the bytes at offsets 256 .. 511 of every 1 KiB of device address
 // space stream slower than the rest when the 256-byte slices of a 1 KiB row
-// are read by different workgroups (Qwen2-VL-7B layout, one kv head per
-// workgroup: the head-1 workgroups ran 15-18% longer than the others in
-// per-workgroup timestamps, on every box measured; with the frame stride
-// padded by 256 bytes the slowness moved with the address, not with the
-// head). A head's weight is 1 + kSlowSliceCost x the fraction of its bytes in
-// that slice, over the four token rows that repeat the pattern; the
-// classes are fixed only when the pool base, the frame stride and the K/V
-// offsets are multiples of 1 KiB and the token and head strides multiples
-// of 256 bytes, otherwise every group weighs the same. Groups that cover
-// whole kilobytes (four heads of 256 bytes) weigh the same as each other.
-constexpr double kSlowSliceCost = 0.25;
+// are read by different workgroups, and bytes 768 .. 1023 slightly slower
+// (Qwen2-VL-7B layout, one kv head per workgroup, per-wave timestamps of 15
+// launches: a head-1 wave-tile took 4.9 us in the steady state against 4.0
+// us for heads 0 and 2 and 4.1 us for head 3, and its first tile landed ~4 us
+// later; with the frame stride padded by 256 bytes the slowness moved with the
+// address, not with the head, and laying the head groups' sequences out in
+// different orders, so that the four heads of a token are not read at the
+// same time, changed nothing). A head's weight is 1 + kSlowSliceCost x the
+// fraction of its bytes in slice 1 + kSlice3Cost x the fraction in slice 3,
+// over the four token rows that repeat the pattern; with these values the
+// four heads' ranges end within 0.7 us of each other on average. The classes
+// are fixed only when the pool base, the frame stride and the K/V offsets are
+// multiples of 1 KiB and the token and head strides multiples of 256 bytes,
+// otherwise every group weighs the same. Groups that cover whole kilobytes
+// (four heads of 256 bytes) weigh the same as each other.
+constexpr double kSlowSliceCost = 0.36;
+constexpr double kSlice3Cost = 0.05;
 std::vector<double> head_group_weights(const DecodeGeometry& g, uint32_t hps, uint32_t nq) {
     std::vector<double> w(nq, 1.0);
     const uint64_t base = reinterpret_cast<uintptr_t>(g.kv_base);
@@ -684,13 +691,15 @@ std::vector<double> head_group_weights(const DecodeGeometry& g, uint32_t hps, ui
     }
     for (uint32_t q = 0; q < nq; ++q) {
         double slow = 0.0;
+        double slow3 = 0.0;
         for (uint32_t h = q * hps; h < (q + 1) * hps; ++h) {
             for (uint64_t t = 0; t < 4; ++t) {
                 const uint64_t off = (h * g.head_stride + t * g.token_stride) % 1024;
                 if (off >= 256 && off < 512) slow += 1.0;
+                if (off >= 768) slow3 += 1.0;
             }
         }
-        w[q] = 1.0 + kSlowSliceCost * slow / (4.0 * hps);
+        w[q] = 1.0 + (kSlowSliceCost * slow + kSlice3Cost * slow3) / (4.0 * hps);
     }
     return w;
 }
