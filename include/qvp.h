@@ -371,6 +371,9 @@ typedef struct qvp_decode_plan {
     uint32_t deferred_results;  /* MFMA: 1 when piece results wait in LDS until a range ends */
     uint32_t query_group;       /* query heads per kv head of that decode */
     uint32_t tile_engine;       /* MFMA kernel: the qvp_tile_engine that ran (1 or 2) */
+    uint32_t shared_prefix_groups; /* MFMA kernel: groups of sequences whose common leading
+                                      frames were decoded once for the whole group */
+    uint32_t shared_prefix_items;  /* MFMA kernel: work items of that shared-prefix launch */
 } qvp_decode_plan;
 
 int qvp_decode_plan_info(const qvp_batch* batch, qvp_decode_plan* plan);

@@ -15,6 +15,21 @@ struct qvp_piece {
     int32_t b, g, t0, t1, ctx, slot, seg_slot0, seg_nslots;
 };
 
+// A shared-prefix work item of the persistent decode: tiles [t0, t1) of kv
+// head g for nmem sequences whose block tables hold the same frames over
+// those tiles (member b[0]'s table supplies them), decoded once for all of
+// them. Member m's partial result goes to workspace slot slot[m] of its
+// (sequence, kv head) segment, whose completion counter is
+// counters[seg_slot0[m]]; the segment's other pieces (its private suffix)
+// are ordinary pieces of the main decode launch.
+constexpr int kPrefixMaxMembers = 8;
+struct qvp_prefix_item {
+    int32_t g, t0, t1, nmem;
+    int32_t b[kPrefixMaxMembers];
+    int32_t slot[kPrefixMaxMembers];
+    int32_t seg_slot0[kPrefixMaxMembers];
+};
+
 // The last enqueued consumer of a device buffer: its stream, and an event
 // recorded right after the read when it ran beside the buffer's writer. A
 // writer on another stream waits for that event on the device (recording one
@@ -35,6 +50,7 @@ struct qvp_reader {
 //   first[num_wgs][8][8]   per wave: its first tile (piece, tile, kv head, the
 //                          two block ids; piece -1 when it has none) and the
 //                          workgroup's piece range (begin, end)
+//   prefix[num_prefix_items] qvp_prefix_item (shared-prefix launch)
 struct qvp_schedule {
     bool valid{false};
     // Device words of the schedule in use: either the batch's packed buffer
@@ -44,6 +60,7 @@ struct qvp_schedule {
     // Host plan between planning and writing: per-workgroup piece CSR and pieces.
     std::vector<int32_t> plan_wg_begin;
     std::vector<qvp_piece> plan_pieces;
+    std::vector<qvp_prefix_item> plan_prefix;
     uint64_t pack_generation{0};
     uint32_t num_kv_heads{0};
     uint32_t group{0};  // query heads per kv head (sizes the deferred LDS and the slots)
@@ -58,7 +75,11 @@ struct qvp_schedule {
     std::vector<double> weights;  // streaming weight per kv-head group the ranges were cut for
     bool defer{false};            // piece results held in LDS until a range is done
     uint32_t lds_bytes{0};        // dynamic LDS per workgroup for them
-    size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, off_first{0}, total{0};  // int32 units
+    // Shared prefixes decoded once for their sequences (a launch before the
+    // main one): work items and the sequence groups they came from.
+    uint32_t num_prefix_items{0};
+    uint32_t prefix_groups{0};
+    size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, off_first{0}, off_prefix{0}, total{0};  // int32 units
     // Two pinned staging buffers, used in turn: rebuilding the schedule for
     // step n + 1 waits only for the upload of the rebuild before last, which
     // the stream reaches once step n - 1's decode is done, so the host can

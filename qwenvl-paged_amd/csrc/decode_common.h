@@ -110,6 +110,9 @@ void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t
 // objects) is refused with QVP_ERR_CAPACITY before anything changes.
 int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t stream, bool may_allocate = true);
 uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim);
+// Slots per query head that shared prefixes can add to a decode of the batch
+// (an upper bound: members x the largest number of prefix chunks).
+uint64_t mfma_prefix_slot_bound(const qvp_batch* batch);
 // Enqueues the persistent kernel; with `upload`, extra workgroups of the same
 // launch copy that pending pack upload in the launch's tail.
 int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t out_dtype, void* out,

@@ -70,8 +70,10 @@ constexpr int kWgsPerCu = 1;
 // decoded four side by side.
 constexpr uint64_t kMinTilesPerWaveForHeadGroups = 32;
 // A workgroup's range is contiguous, so only its first and last pieces can be
-// partial segments.
-constexpr int kMaxPartialPerWg = 2;
+// partial segments -- unless shared prefixes split its sequences' segments,
+// each of which then ends in one piece of the range. Partial pieces one
+// workgroup may hold (the planner keeps schedules within it).
+constexpr int kMaxMergesPerWg = 64;
 // Slots combined per round of loads in the end-of-range merge, and work items
 // (four dims of a row) per thread per round.
 constexpr int kMergeChunk = 8;
@@ -89,7 +91,7 @@ constexpr double kPieceBoundaryTiles = 0.7;
 // kernel's static arrays take kStaticLdsBytes; the rest can hold deferred
 // piece results.
 constexpr uint32_t kMaxLdsBytes = 160u * 1024u;
-constexpr uint32_t kStaticLdsBytes = (2 * kWaves * 16 + kWaves * 16 * kRowPad) * 4 + 64;
+constexpr uint32_t kStaticLdsBytes = (2 * kWaves * 16 + kWaves * 16 * kRowPad + kMaxMergesPerWg + 1) * 4 + 64;
 
 // Words per wave of the schedule's first-tile table.
 constexpr int kFirstWords = 8;
@@ -215,7 +217,8 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     __shared__ float sm_m[kWaves][16];
     __shared__ float sm_l[kWaves][16];
     __shared__ float sm_o[kWaves][16][kRowPad];
-    __shared__ int sm_merge[kMaxPartialPerWg];
+    __shared__ int sm_merge[kMaxMergesPerWg];
+    __shared__ int sm_nmerge;
     // Piece results held until the range is done (a.defer): [piece][hps *
     // G][kD] accumulators, then [piece][hps * G][2] (m, l).
     extern __shared__ float sm_def[];
@@ -472,28 +475,38 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     // once written through to the point of coherence), and the barrier then
     // orders all the waves' stores before any counter moves. The asm's
     // memory clobber keeps the compiler from moving memory accesses across
-    // the wait.
-    // Only the first and the last piece of a contiguous range can be partial
-    // segments; their descriptors are uniform (scalar loads).
-    const qvp_piece first_piece = piece_at(a.pieces, pb);
-    const qvp_piece last_piece = piece_at(a.pieces, pe - 1);
+    // the wait. A contiguous range holds at most two partial pieces (its
+    // first and last) unless shared prefixes split the segments of its
+    // sequences (each then ends in one private piece of the range, counted in
+    // after the prefix launch counted its chunks): thread k counts piece
+    // pb + k in, all in parallel, and the completed segments go to a list.
+    // The descriptors of the pieces to count in are read before the wait, so
+    // their loads overlap it.
+    int my_slot = -1;
+    int my_seg = 0;
+    int my_n = 0;
+    if (static_cast<int>(threadIdx.x) < pe - pb) {
+        const qvp_piece d = piece_at(a.pieces, pb + static_cast<int>(threadIdx.x));
+        my_slot = d.slot;
+        my_seg = d.seg_slot0;
+        my_n = d.seg_nslots;
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (threadIdx.x == 0) sm_nmerge = 0;
     __syncthreads();
-    // Thread 0 counts the first piece in, thread 1 the last one (when it is
-    // another piece); the two increments run in parallel.
-    if (threadIdx.x < kMaxPartialPerWg) {
-        const bool is_first = threadIdx.x == 0;
-        const bool exists = is_first || pe - 1 > pb;
-        const int slot = is_first ? first_piece.slot : last_piece.slot;
-        const int seg_slot0 = is_first ? first_piece.seg_slot0 : last_piece.seg_slot0;
-        const int seg_nslots = is_first ? first_piece.seg_nslots : last_piece.seg_nslots;
-        int mine = -1;
-        if (exists && slot >= 0) {
-            const int done = __hip_atomic_fetch_add(&a.counters[seg_slot0], 1, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-            if (done == seg_nslots - 1) mine = is_first ? pb : pe - 1;
+    for (int k = threadIdx.x; k < pe - pb; k += kThreads) {
+        if (k != static_cast<int>(threadIdx.x)) {
+            const qvp_piece d = piece_at(a.pieces, pb + k);
+            my_slot = d.slot;
+            my_seg = d.seg_slot0;
+            my_n = d.seg_nslots;
         }
-        sm_merge[threadIdx.x] = mine;
+        if (my_slot < 0) continue;
+        const int done = __hip_atomic_fetch_add(&a.counters[my_seg], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == my_n - 1) {
+            const int at = __hip_atomic_fetch_add(&sm_nmerge, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            sm_merge[at] = pb + k;
+        }
     }
     __syncthreads();
     // Merge the segments this workgroup completed. All their elements are
@@ -501,22 +514,14 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     // and each round issues every slot load of its elements before combining
     // (agent-scope loads read the slots of other workgroups, on other XCDs,
     // from the point of coherence): the merge costs about one round trip.
-    // The segments to merge (at most two) are uniform across the workgroup:
-    // their slot ranges and output rows are fetched once, with scalar loads,
-    // so the loops below issue no loads but the slot reads.
-    const int pm0 = __builtin_amdgcn_readfirstlane(sm_merge[0]);
-    const int pm1 = __builtin_amdgcn_readfirstlane(sm_merge[kMaxPartialPerWg - 1]);
-    if (pm0 < 0 && pm1 < 0) return;
-    const int nm = (pm0 >= 0) + (pm1 >= 0);
-    const qvp_piece m0 = piece_at(a.pieces, pm0 >= 0 ? pm0 : pm1);
-    const qvp_piece m1 = piece_at(a.pieces, pm1 >= 0 ? pm1 : pm0);
-    const int max_ns = max(m0.seg_nslots, m1.seg_nslots);
-    const uint64_t orow0 = (static_cast<uint64_t>(m0.b) * p.num_q_heads + m0.g * hpsG) * kD;
-    const uint64_t orow1 = (static_cast<uint64_t>(m1.b) * p.num_q_heads + m1.g * hpsG) * kD;
+    const int nm = __builtin_amdgcn_readfirstlane(sm_nmerge);
+    if (nm == 0) return;
     // Work items are four consecutive dims of one row: per slot one 8-byte
     // agent-scope load of the row's (m, l) and two of its four accumulators.
     const int per_seg = hpsG * (kD / 4);
     const int total = nm * per_seg;
+    int max_ns = 0;
+    for (int i = 0; i < nm; ++i) max_ns = max(max_ns, piece_at(a.pieces, __builtin_amdgcn_readfirstlane(sm_merge[i])).seg_nslots);
     for (int f0 = threadIdx.x; f0 < total; f0 += kThreads * kMergeBatch) {
         int ri[kMergeBatch], dq[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch];
         uint64_t orow[kMergeBatch];
@@ -524,13 +529,14 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
 #pragma unroll
         for (int i = 0; i < kMergeBatch; ++i) {
             const int f = f0 + i * kThreads;
-            const bool second = f >= per_seg;
-            const int e = f < total ? f - (second ? per_seg : 0) : 0;
+            const int si = f < total ? f / per_seg : 0;
+            const int e = f < total ? f - si * per_seg : 0;
+            const qvp_piece m = piece_at(a.pieces, sm_merge[si]);
             ri[i] = e >> 5;
             dq[i] = e & 31;
-            s0[i] = second ? m1.seg_slot0 : m0.seg_slot0;
-            ns[i] = f < total ? (second ? m1.seg_nslots : m0.seg_nslots) : 0;
-            orow[i] = second ? orow1 : orow0;
+            s0[i] = m.seg_slot0;
+            ns[i] = f < total ? m.seg_nslots : 0;
+            orow[i] = (static_cast<uint64_t>(m.b) * p.num_q_heads + m.g * hpsG) * kD;
             mmax[i] = -INFINITY;
             lsum[i] = 0.f;
 #pragma unroll
@@ -589,9 +595,127 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
             }
         }
     }
-    if (threadIdx.x < static_cast<unsigned>(nm)) {
-        const int s0 = threadIdx.x == 0 ? m0.seg_slot0 : m1.seg_slot0;
-        __hip_atomic_store(&a.counters[s0], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int k = threadIdx.x; k < nm; k += kThreads) {
+        __hip_atomic_store(&a.counters[piece_at(a.pieces, sm_merge[k]).seg_slot0], 0, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+struct PrefixArgs {
+    const qvp_prefix_item* items;
+    int32_t* counters;
+    float* ws_ml;   // the main launch's workspace layout: [slot][group][2]
+    float* ws_acc;  // [slot][group][128]
+};
+
+// Shared-prefix launch: one workgroup per work item (tiles [t0, t1) of kv
+// head g shared by up to eight sequences). The eight waves are four column
+// blocks x two tile lanes: column block k holds sequences k * (16 / G) ..
+// in its MFMA columns (G query heads each), and the two tile lanes take the
+// item's tiles in turn, so each tile is fetched from HBM once and read by the
+// other three column blocks of its lane from L2. The tiles are whole (the
+// prefix ends before every member's last tile), so no mask applies. At the
+// end the two lanes of each column block merge through LDS and every member's
+// (m, l, O) goes to its slot with agent-scope stores; after they have
+// completed, one increment per member counts the chunk into its segment, whose
+// private pieces (main launch, later on the stream) complete and merge it.
+__global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(DecodeGeometry p, PrefixArgs a) {
+    __shared__ float sm_m[kWaves][16];
+    __shared__ float sm_l[kWaves][16];
+    __shared__ float sm_o[kWaves][16][kRowPad];
+    const auto* it = as_const(a.items) + blockIdx.x;
+    const int gq = it->g;
+    const int t0 = it->t0;
+    const int t1 = it->t1;
+    const int nmem = it->nmem;
+    const int b0 = it->b[0];
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15;
+    const int j = lane >> 4;
+    const int G = static_cast<int>(p.group);
+    const int mpb = 16 / G;   // sequences per column block
+    const int ncol = mpb * G;
+    const int cb = wave & 3;  // column block
+    const int tl = wave >> 2; // tile lane
+    // Column c: sequence cb * mpb + c / G, query head c % G of kv head gq;
+    // columns past the block's last sequence repeat it and are never stored.
+    const int cc = min(c, ncol - 1);
+    const int mem = min(cb * mpb + cc / G, nmem - 1);
+    const int bq = as_const(a.items)[blockIdx.x].b[mem];
+    const uint16_t* qp = static_cast<const uint16_t*>(p.query) +
+                         (static_cast<uint64_t>(bq) * p.num_q_heads + gq * G + cc % G) * kD;
+    u32x4 qop[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i + 8 * j);
+
+    const auto* row = as_const(p.tables) + static_cast<uint64_t>(b0) * p.max_nb;
+    auto ref = [&](int t) {
+        TileRef r{};
+        r.b = b0;
+        r.g = gq;
+        r.t = t;
+        r.ctx = t1 * kTileTokens;
+        r.blk0 = row[(t * kTileTokens) >> p.tpb_shift];
+        r.blk1 = row[(t * kTileTokens + 16) >> p.tpb_shift];
+        return r;
+    };
+    floatx4 o[8];
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+    const int end_tok = t1 * kTileTokens;
+    // One tile in flight per wave, the frames of the tile after it resolved
+    // while the current one is computed.
+    KvTile nxt;
+    int t = t0 + tl;
+    TileRef r2{};
+    if (t < t1) load_tile(p, ref(t), c, j, nxt);
+    if (t + 2 < t1) r2 = ref(t + 2);
+    for (; t < t1; t += 2) {
+        KvTile cur = nxt;
+        if (t + 2 < t1) load_tile(p, r2, c, j, nxt);
+        if (t + 4 < t1) r2 = ref(t + 4);
+        compute_tile(cur, qop, t * kTileTokens, end_tok - 1, end_tok, p.scale_log2, j, m_run, l_run, o);
+    }
+    l_run = sum_over_j(l_run);
+    if (j == 0) {
+        sm_m[wave][c] = m_run;
+        sm_l[wave][c] = l_run;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int n = 0; n < 8; ++n) sm_o[wave][c][32 * j + 8 * r + n] = o[n][r];
+    lds_barrier();
+    for (int e = threadIdx.x; e < 4 * 16 * kD; e += kThreads) {
+        const int blk = e >> 11;
+        const int col = (e >> 7) & 15;
+        const int dd = e & (kD - 1);
+        const int m = blk * mpb + col / G;
+        if (col >= ncol || m >= nmem) continue;
+        // A lane with no tile holds -inf, 0 and zeros.
+        const float m1 = sm_m[blk][col];
+        const float m2 = sm_m[blk + 4][col];
+        const float mx = fmaxf(m1, m2);
+        const float f1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - mx);
+        const float f2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - mx);
+        const float acc = sm_o[blk][col][dd] * f1 + sm_o[blk + 4][col][dd] * f2;
+        const uint64_t ri = static_cast<uint64_t>(as_const(a.items)[blockIdx.x].slot[m]) * G + col % G;
+        __hip_atomic_store(&a.ws_acc[ri * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (dd == 0) {
+            const float lsum = sm_l[blk][col] * f1 + sm_l[blk + 4][col] * f2;
+            __hip_atomic_store(&a.ws_ml[ri * 2 + 0], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.ws_ml[ri * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    // Every wave's slot stores have completed before any member is counted.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < nmem) {
+        (void)__hip_atomic_fetch_add(&a.counters[as_const(a.items)[blockIdx.x].seg_slot0[threadIdx.x]], 1,
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -747,7 +871,11 @@ std::vector<uint64_t> cut_ranges(const std::vector<uint64_t>& pos_cum, uint32_t 
         while (p < T) {
             const uint64_t rem = pos_cum[sg + 1] - p;
             if (acc + static_cast<double>(rem) >= target) {
-                cut = p + static_cast<uint64_t>(target - acc + 0.5);
+                // The target can fall before p when the boundary cost just
+                // added overshot it (segments shorter than that cost): cut at
+                // the segment's start then.
+                const double off = target - acc + 0.5;
+                cut = p + (off > 0.0 ? static_cast<uint64_t>(off) : 0u);
                 break;
             }
             acc += static_cast<double>(rem);
@@ -770,6 +898,76 @@ std::vector<uint64_t> cut_ranges(const std::vector<uint64_t>& pos_cum, uint32_t 
         pos = cut;
     }
     return bd;
+}
+
+// Shared prefixes. A prefix group is up to 4 x (16 / G) sequences (four
+// column blocks of 16 / G sequences of G query heads each) whose block lists
+// agree over their first `tiles` 32-token tiles. Only whole tiles of shared
+// frames count, and every member keeps at least its last tile for the main
+// launch, so the prefix tiles are full and every member segment ends in an
+// ordinary piece (which completes the segment's merge).
+constexpr uint32_t kPrefixMinTiles = 4;
+constexpr uint64_t kPrefixMinChunkTiles = 8;
+constexpr uint64_t kPrefixMaxChunks = 8;
+
+struct PrefixGroup {
+    int nmem{0};
+    uint32_t b[kPrefixMaxMembers]{};
+    uint32_t tiles{0};
+    int chunks{0};
+};
+
+std::vector<PrefixGroup> find_prefix_groups(const ScheduleInput& in, const DecodeGeometry& g, uint32_t hps) {
+    std::vector<PrefixGroup> out;
+    if (hps != 1 || in.partition_tiles != 0 || g.tile_group != 0 || g.group == 0 || g.group > 16 || in.tpb == 0) {
+        return out;
+    }
+    const int cap = std::min<int>(kPrefixMaxMembers, 4 * static_cast<int>(16 / g.group));
+    if (cap < 2) return out;
+    // Sequences with at least one shared-candidate frame, ordered by their
+    // first frame (then by index): forks of one prompt end up adjacent.
+    std::vector<uint32_t> order;
+    for (uint32_t b = 0; b < in.num_seqs; ++b) {
+        if (in.cu_blocks[b + 1] > in.cu_blocks[b]) order.push_back(b);
+    }
+    std::stable_sort(order.begin(), order.end(), [&](uint32_t x, uint32_t y) {
+        return in.ids[in.cu_blocks[x]] < in.ids[in.cu_blocks[y]];
+    });
+    auto tiles_of = [&](uint32_t b) { return (static_cast<uint32_t>(in.lens[b]) + kTileTokens - 1) / kTileTokens; };
+    size_t i = 0;
+    while (i < order.size()) {
+        size_t e = i + 1;
+        while (e < order.size() && in.ids[in.cu_blocks[order[e]]] == in.ids[in.cu_blocks[order[i]]]) ++e;
+        for (size_t g0 = i; g0 + 1 < e; g0 += cap) {
+            const size_t g1 = std::min(e, g0 + cap);
+            if (g1 - g0 < 2) break;
+            // Frames every member shares with the first one, from the start.
+            const uint32_t* ids0 = in.ids + in.cu_blocks[order[g0]];
+            uint32_t common = in.cu_blocks[order[g0] + 1] - in.cu_blocks[order[g0]];
+            uint32_t min_tiles = tiles_of(order[g0]);
+            for (size_t k = g0 + 1; k < g1; ++k) {
+                const uint32_t b = order[k];
+                const uint32_t* ids = in.ids + in.cu_blocks[b];
+                const uint32_t nb = std::min(common, in.cu_blocks[b + 1] - in.cu_blocks[b]);
+                uint32_t n = 0;
+                while (n < nb && ids[n] == ids0[n]) ++n;
+                common = n;
+                min_tiles = std::min(min_tiles, tiles_of(b));
+            }
+            const uint64_t shared_tokens = static_cast<uint64_t>(common) * in.tpb;
+            uint32_t tiles = static_cast<uint32_t>(shared_tokens / kTileTokens);
+            if (min_tiles == 0) continue;
+            tiles = std::min(tiles, min_tiles - 1);
+            if (tiles < kPrefixMinTiles) continue;
+            PrefixGroup pg;
+            pg.nmem = static_cast<int>(g1 - g0);
+            for (int m = 0; m < pg.nmem; ++m) pg.b[m] = order[g0 + m];
+            pg.tiles = tiles;
+            out.push_back(pg);
+        }
+        i = e;
+    }
+    return out;
 }
 
 }  // namespace
@@ -808,7 +1006,10 @@ bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g) {
     return s.weights == head_group_weights(g, s.hps, nq);
 }
 
-int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry& g) {
+namespace {
+
+// The schedule, with shared-prefix groups when allow_prefix.
+int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry& g, bool allow_prefix) {
     const uint32_t num_kv_heads = g.num_kv_heads;
     uint32_t max_wgs = 0;
     QVP_TRY(device_max_wgs(&max_wgs));
@@ -817,11 +1018,26 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     for (uint32_t b = 0; b < nseq; ++b) {
         pos_cum[b + 1] = pos_cum[b] + (static_cast<uint64_t>(in.lens[b]) + kTileTokens - 1) / kTileTokens;
     }
-    const uint64_t T = pos_cum[nseq];
-    const uint32_t hps = head_group_size(num_kv_heads, T, max_wgs);
+    const uint32_t hps = head_group_size(num_kv_heads, pos_cum[nseq], max_wgs);
     const uint32_t nq = num_kv_heads / hps;
     const std::vector<double> weights = head_group_weights(g, hps, nq);
     s.valid = false;
+
+    // Shared prefixes: sequences whose block tables start with the same
+    // frames (forks of one prompt) have those tiles decoded once for the
+    // whole group by a launch before the main one; the main launch covers
+    // each sequence's tiles from start[b] on.
+    std::vector<PrefixGroup> groups = allow_prefix ? find_prefix_groups(in, g, hps) : std::vector<PrefixGroup>{};
+    std::vector<uint32_t> start(nseq, 0);
+    for (const PrefixGroup& pg : groups) {
+        for (int m = 0; m < pg.nmem; ++m) start[pg.b[m]] = pg.tiles;
+    }
+    if (!groups.empty()) {
+        for (uint32_t b = 0; b < nseq; ++b) {
+            pos_cum[b + 1] = pos_cum[b] + (static_cast<uint64_t>(in.lens[b]) + kTileTokens - 1) / kTileTokens - start[b];
+        }
+    }
+    const uint64_t T = pos_cum[nseq];
 
     // Segments (b, q): sequence b's kv heads q * hps .. q * hps + hps - 1. With
     // hps kv heads per segment the eight waves of a workgroup split as hps
@@ -847,7 +1063,12 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
             cut_room += (pos_cum[b + 1] - pos_cum[b] + in.partition_tiles - 1) / in.partition_tiles;
         }
     }
-    const uint64_t max_ranges = std::max<uint64_t>(1, std::min<uint64_t>((T + tl - 1) / tl, cut_room));
+    // With shared prefixes the main launch holds the members' private tails,
+    // often a tile or two each: one tile per range then keeps them spread
+    // over the CUs instead of queued behind one another in a few ranges.
+    const uint64_t min_range_tiles = groups.empty() ? tl : 1;
+    const uint64_t max_ranges =
+        std::max<uint64_t>(1, std::min<uint64_t>((T + min_range_tiles - 1) / min_range_tiles, cut_room));
     const uint32_t R = static_cast<uint32_t>(std::min<uint64_t>(std::max<uint32_t>(1, max_wgs / nq), max_ranges));
     const uint32_t W = R * nq;
     std::vector<uint32_t> Rq(nq, R);
@@ -898,8 +1119,8 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
             qvp_piece pc{};
             pc.b = static_cast<int32_t>(b);
             pc.g = static_cast<int32_t>(rr.q);
-            pc.t0 = static_cast<int32_t>(pos - pos_cum[b]);
-            pc.t1 = static_cast<int32_t>(end - pos_cum[b]);
+            pc.t0 = static_cast<int32_t>(pos - pos_cum[b] + start[b]);
+            pc.t1 = static_cast<int32_t>(end - pos_cum[b] + start[b]);
             pc.ctx = static_cast<int32_t>(in.lens[b]);
             pc.slot = -1;
             pc.seg_slot0 = -1;
@@ -918,6 +1139,22 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     const size_t nseg = static_cast<size_t>(nseq) * nq;
     std::vector<int32_t> seg_count(nseg, 0), seg_base(nseg, -1), seg_next(nseg, 0);
     for (const qvp_piece& pc : pieces) ++seg_count[static_cast<size_t>(pc.b) * nq + pc.g];
+    // A shared prefix is cut into chunks of about equal size, so that the
+    // prefix launch has about one work item per CU; each chunk is one more
+    // piece (and slot) of every member's segment, and comes first in it.
+    uint64_t prefix_tiles = 0;
+    for (const PrefixGroup& pg : groups) prefix_tiles += static_cast<uint64_t>(pg.tiles) * nq;
+    const uint64_t chunk_tiles = std::max<uint64_t>(kPrefixMinChunkTiles, (prefix_tiles + max_wgs - 1) / max_wgs);
+    for (PrefixGroup& pg : groups) {
+        pg.chunks = static_cast<int>(std::min<uint64_t>(kPrefixMaxChunks, (pg.tiles + chunk_tiles - 1) / chunk_tiles));
+        for (int m = 0; m < pg.nmem; ++m) {
+            for (uint32_t q = 0; q < nq; ++q) {
+                const size_t k = static_cast<size_t>(pg.b[m]) * nq + q;
+                seg_count[k] += pg.chunks;
+                seg_next[k] = pg.chunks;
+            }
+        }
+    }
     int32_t next_slot = 0;
     for (size_t k = 0; k < nseg; ++k) {
         if (seg_count[k] > 1) {
@@ -932,18 +1169,46 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
         pc.seg_slot0 = seg_base[k];
         pc.seg_nslots = seg_count[k];
     }
-    // The kernel counts in only the first and the last piece of a range.
+    std::vector<qvp_prefix_item>& items = s.plan_prefix;
+    items.clear();
+    for (const PrefixGroup& pg : groups) {
+        for (uint32_t q = 0; q < nq; ++q) {
+            for (int ch = 0; ch < pg.chunks; ++ch) {
+                qvp_prefix_item it{};
+                it.g = static_cast<int32_t>(q);
+                it.t0 = static_cast<int32_t>(static_cast<int64_t>(pg.tiles) * ch / pg.chunks);
+                it.t1 = static_cast<int32_t>(static_cast<int64_t>(pg.tiles) * (ch + 1) / pg.chunks);
+                it.nmem = pg.nmem;
+                for (int m = 0; m < kPrefixMaxMembers; ++m) {
+                    const int mm = std::min(m, pg.nmem - 1);
+                    const size_t k = static_cast<size_t>(pg.b[mm]) * nq + q;
+                    it.b[m] = static_cast<int32_t>(pg.b[mm]);
+                    it.seg_slot0[m] = seg_base[k];
+                    it.slot[m] = seg_base[k] + ch;
+                }
+                items.push_back(it);
+            }
+        }
+    }
+    // The kernel counts in at most kMaxMergesPerWg partial pieces per range:
+    // without shared prefixes only a range's first and last piece are
+    // partial; a schedule whose prefix groups would exceed the bound (many
+    // tiny forked sequences in one range) is planned without them.
     uint32_t max_partial = 0;
     for (uint32_t w = 0; w < Wn; ++w) {
         uint32_t n = 0;
         for (int32_t pi = wg_begin[w]; pi < wg_begin[w + 1]; ++pi) {
             if (pieces[pi].slot < 0) continue;
             ++n;
-            if (pi != wg_begin[w] && pi != wg_begin[w + 1] - 1) {
+            if (groups.empty() && pi != wg_begin[w] && pi != wg_begin[w + 1] - 1) {
                 return fail(QVP_ERR_INVALID_ARGUMENT, "schedule puts a partial segment inside workgroup %u's range", w);
             }
         }
         max_partial = std::max(max_partial, n);
+    }
+    if (max_partial > static_cast<uint32_t>(kMaxMergesPerWg)) {
+        if (!groups.empty()) return plan_schedule(s, in, g, false);
+        return fail(QVP_ERR_INVALID_ARGUMENT, "schedule gives a workgroup %u partial pieces", max_partial);
     }
 
     // Piece results are held in LDS until a range is done when the largest
@@ -961,7 +1226,8 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     s.off_counters = s.off_pieces + align_ints(pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)));
     s.off_first = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
     const size_t first_words = static_cast<size_t>(Wn) * kWaves * kFirstWords;
-    s.total = s.off_first + align_ints(first_words);
+    s.off_prefix = s.off_first + align_ints(first_words);
+    s.total = s.off_prefix + align_ints(items.size() * (sizeof(qvp_prefix_item) / sizeof(int32_t)));
 
     s.pack_generation = in.generation;
     s.num_kv_heads = num_kv_heads;
@@ -975,7 +1241,15 @@ int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeo
     s.num_slots = static_cast<uint32_t>(next_slot);
     s.hps = hps;
     s.max_partial_pieces_per_wg = max_partial;
+    s.num_prefix_items = static_cast<uint32_t>(items.size());
+    s.prefix_groups = static_cast<uint32_t>(groups.size());
     return QVP_OK;
+}
+
+}  // namespace
+
+int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry& g) {
+    return plan_schedule(s, in, g, true);
 }
 
 void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t* h) {
@@ -987,6 +1261,8 @@ void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t
     std::copy(wg_begin.begin(), wg_begin.end(), h + s.off_wg_begin);
     const int32_t* praw = reinterpret_cast<const int32_t*>(pieces.data());
     std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
+    const int32_t* xraw = reinterpret_cast<const int32_t*>(s.plan_prefix.data());
+    std::copy(xraw, xraw + s.plan_prefix.size() * (sizeof(qvp_prefix_item) / sizeof(int32_t)), h + s.off_prefix);
     // Each wave's first tile, resolved to frames here (the kernel's
     // next_tile and resolve_tile for its first step), written straight into
     // the staging buffer (its other words stay zero).
@@ -1085,6 +1361,26 @@ int mfma_prepare_schedule(qvp_batch* batch, const DecodeGeometry& g, hipStream_t
     return QVP_OK;
 }
 
+uint64_t mfma_prefix_slot_bound(const qvp_batch* batch) {
+    // A sequence can be a shared-prefix member only if another sequence
+    // starts with the same frame; each member gets at most kPrefixMaxChunks
+    // prefix slots per kv head.
+    const std::vector<uint32_t>& cu = batch->host_cu_blocks;
+    const std::vector<uint32_t>& ids = batch->host_ids;
+    if (cu.size() < 3) return 0;
+    std::vector<uint32_t> first;
+    for (size_t b = 0; b + 1 < cu.size(); ++b) {
+        if (cu[b + 1] > cu[b]) first.push_back(ids[cu[b]]);
+    }
+    std::sort(first.begin(), first.end());
+    uint64_t members = 0;
+    for (size_t i = 0; i < first.size(); ++i) {
+        const bool dup = (i > 0 && first[i - 1] == first[i]) || (i + 1 < first.size() && first[i + 1] == first[i]);
+        members += dup ? 1u : 0u;
+    }
+    return members * kPrefixMaxChunks;
+}
+
 uint64_t mfma_workspace_bytes(const qvp_batch* batch, uint32_t group, uint32_t head_dim) {
     const uint64_t rows = static_cast<uint64_t>(batch->sched.num_slots) * batch->sched.hps * group;
     return round_up(rows * 2 * sizeof(float), 256) + round_up(rows * head_dim * sizeof(float), 256);
@@ -1117,6 +1413,16 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
         return fail(QVP_ERR_INVALID_ARGUMENT, "the batch's schedule was planned for another tile engine");
     }
     DecodeGeometry gk = g;
+    if (s.num_prefix_items > 0) {
+        PrefixArgs pa{};
+        pa.items = reinterpret_cast<const qvp_prefix_item*>(s.words + s.off_prefix);
+        pa.counters = a.counters;
+        pa.ws_ml = a.ws_ml;
+        pa.ws_acc = a.ws_acc;
+        void* pargs[] = {&gk, &pa};
+        QVP_HIP(hipLaunchKernel(reinterpret_cast<const void*>(&decode_prefix_groups), dim3(s.num_prefix_items),
+                                dim3(kThreads), pargs, 0, stream));
+    }
     void* kargs[] = {&gk, &a};
     QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs + copy_wgs), dim3(kThreads), kargs,
                             s.lds_bytes, stream));

@@ -178,8 +178,12 @@ int qvp_decode_workspace_bytes(const qvp_batch* batch, uint32_t num_query_heads,
     if (bytes == nullptr) return fail(QVP_ERR_INVALID_ARGUMENT, "bytes is NULL");
     qvp_packed_view v{};
     QVP_TRY(qvp_batch_view(batch, &v));
+    // Shared-prefix slots come on top of the persistent kernel's own bound.
+    const uint64_t prefix_rows = qvp::mfma_prefix_slot_bound(batch) * num_query_heads;
     *bytes = std::max(qvp::generic_workspace_bytes(v, num_query_heads, head_dim),
-                      mfma_bound_bytes(v, num_query_heads, head_dim));
+                      mfma_bound_bytes(v, num_query_heads, head_dim) +
+                          qvp::round_up(prefix_rows * 2 * sizeof(float), 256) +
+                          qvp::round_up(prefix_rows * head_dim * sizeof(float), 256));
     return QVP_OK;
 }
 
@@ -260,6 +264,8 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         plan.deferred_results = sc.defer ? 1u : 0u;
         plan.tile_engine = g.tile_group != 0 ? QVP_TILE_VECTOR : QVP_TILE_MATRIX;
         plan.split_tokens = sc.partition_tiles * qvp::kScheduleTileTokens;
+        plan.shared_prefix_groups = sc.prefix_groups;
+        plan.shared_prefix_items = sc.num_prefix_items;
     } else {
         const bool f32 = qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens,
                                                     reinterpret_cast<uintptr_t>(a->query),

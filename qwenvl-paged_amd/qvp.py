@@ -80,6 +80,8 @@ class DecodeArgs(ctypes.Structure):
         ("workspace_bytes", c_uint64),
         ("split_event", c_void_p),
         ("tile_engine", c_uint32),
+        ("shared_prefix_groups", c_uint32),
+        ("shared_prefix_items", c_uint32),
     ]
 
 
@@ -139,6 +141,8 @@ class DecodePlan(ctypes.Structure):
         ("deferred_results", c_uint32),
         ("query_group", c_uint32),
         ("tile_engine", c_uint32),
+        ("shared_prefix_groups", c_uint32),
+        ("shared_prefix_items", c_uint32),
     ]
 
 

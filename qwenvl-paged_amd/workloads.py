@@ -244,3 +244,46 @@ def custom(context_lens, num_query_heads: int, num_kv_heads: int, head_dim: int,
     return Workload("custom", tokens_per_block, num_layers, num_query_heads, num_kv_heads, head_dim, kv_dtype,
                     scale if scale is not None else 1.0 / math.sqrt(head_dim), ctx, ids, cu, pool, seed,
                     layer=layer, split_tokens=split_tokens, q_sigma=q_sigma, kv_sigma=kv_sigma)
+
+
+def forked(prompt_lens, branches, extra_tokens, num_query_heads: int, num_kv_heads: int, head_dim: int = 128,
+           kv_dtype: int = DTYPE_BF16, tokens_per_block: int = 16, seed: int = 11, solo_lens=(),
+           spare: float = 0.1) -> Workload:
+    """Parallel-sampling batch: prompt p (prompt_lens[p] tokens) forked into
+    branches[p] sequences that share the prompt's whole blocks (the same frame
+    ids, as KVCacheManager::fork leaves them), each with its own copy of the
+    prompt's partial tail block and its own later blocks; branch k of prompt p
+    holds extra_tokens[p][k] tokens past the prompt. `solo_lens` adds
+    unshared sequences. Frames come from a seeded shuffled pool."""
+    tpb = tokens_per_block
+    ctx: list[int] = []
+    shared_of: list[int] = []
+    for p, (plen, nb) in enumerate(zip(prompt_lens, branches)):
+        for k in range(nb):
+            ctx.append(int(plen) + int(extra_tokens[p][k]))
+            shared_of.append(p)
+    for n in solo_lens:
+        ctx.append(int(n))
+        shared_of.append(-1)
+    shared_blocks = [int(plen) // tpb for plen in prompt_lens]
+    need = sum(shared_blocks) + sum((c + tpb - 1) // tpb - (shared_blocks[s] if s >= 0 else 0)
+                                    for c, s in zip(ctx, shared_of))
+    pool = max(int(math.ceil(need * (1.0 + spare))), need + 1)
+    order = list(shuffled_allocation_order(pool, seed))
+    prompt_frames = []
+    for n in shared_blocks:
+        prompt_frames.append(order[:n])
+        order = order[n:]
+    ids: list[int] = []
+    cu = [0]
+    for c, s in zip(ctx, shared_of):
+        nb = (c + tpb - 1) // tpb
+        own = shared_blocks[s] if s >= 0 else 0
+        ids.extend(prompt_frames[s] if s >= 0 else [])
+        ids.extend(order[: nb - own])
+        order = order[nb - own:]
+        cu.append(len(ids))
+    ctx_a = np.asarray(ctx, dtype=np.uint32)
+    return Workload("forked", tpb, 1, num_query_heads, num_kv_heads, head_dim, kv_dtype,
+                    1.0 / math.sqrt(head_dim), ctx_a, np.asarray(ids, dtype=np.uint32),
+                    np.asarray(cu, dtype=np.uint32), pool, seed, q_sigma=1.0, kv_sigma=0.5)

@@ -1,0 +1,83 @@
+"""GPU parity of the shared-prefix decode: sequences forked from one prompt
+share the prompt's frames (the page-table state KVCacheManager::fork leaves,
+reference src/KVCacheManager.cpp fork), and the persistent decode reads those
+frames once for the whole group (a launch before the main one) while every
+sequence's own tail runs as ordinary pieces. The result must equal the
+reference's per-sequence decode (PagedAttention.h:53-127) at the bf16 bar;
+the oracle decodes each sequence over its own block list, so sharing is
+invisible to it."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import qvp
+import workloads as W
+from helpers import GpuRun, assert_close_16bit, assert_close_bf16, oracle_decode
+
+pytestmark = pytest.mark.gpu
+
+
+def _extra(seed: int, branches, lo: int = 1, hi: int = 120):
+    rng = np.random.default_rng(seed)
+    return [list(rng.integers(lo, hi, size=n)) for n in branches]
+
+
+def _check(w: W.Workload, expect_groups: int | None = None):
+    run = GpuRun(w)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got32 = run.decode(out_dtype=qvp.DTYPE_F32)
+    plan = run.batch.decode_plan()
+    assert plan["kernel"] == "mfma"
+    if expect_groups is not None:
+        assert plan["shared_prefix_groups"] == expect_groups, plan
+        assert plan["shared_prefix_items"] >= expect_groups * w.num_kv_heads, plan
+    stats = assert_close_bf16(got32, ref32, f"{w.name} fp32 out")
+    got16 = run.decode(out_dtype=qvp.DTYPE_BF16)
+    assert_close_16bit(got16, ref32, qvp.DTYPE_BF16, f"{w.name} bf16 out")
+    return run, got32, stats
+
+
+def test_forks_of_three_prompts_at_the_7b_shape():
+    # Group of 8 (the most a query group of 7 fits: four column blocks of two
+    # sequences), of 3 and of 2, beside two unshared sequences.
+    branches = [8, 3, 2]
+    w = W.forked([1000, 2100, 333], branches, _extra(1, branches), 28, 4, solo_lens=[700, 50])
+    _check(w, expect_groups=3)
+
+
+@pytest.mark.parametrize("hq,hkv,per_group", [(4, 4, 8), (16, 4, 8), (64, 4, 4), (32, 8, 8)])
+def test_query_group_sizes_set_the_group_capacity(hq, hkv, per_group):
+    # 16 // G sequences per column block, four blocks, at most eight: a fork of
+    # ten splits into groups of per_group and the rest (a lone rest is left
+    # to the main launch).
+    branches = [10]
+    w = W.forked([1500], branches, _extra(2, branches), hq, hkv)
+    full, rest = divmod(10, per_group)
+    _check(w, expect_groups=full + (1 if rest >= 2 else 0))
+
+
+def test_prefix_shorter_than_the_minimum_is_decoded_per_sequence():
+    branches = [4]
+    w = W.forked([100], branches, _extra(3, branches), 28, 4)  # 6 shared blocks = 3 tiles
+    _check(w, expect_groups=0)
+
+
+def test_branch_ending_inside_the_shared_tail_block():
+    # Branches of one token past a prompt that ends mid-block: each branch's
+    # last block is its own copy, so the shared frames stop one block early.
+    branches = [5]
+    w = W.forked([1031], branches, [[1, 1, 2, 1, 3]], 28, 4)
+    _check(w, expect_groups=1)
+
+
+def test_config4_shape_matches_the_oracle_and_repeats_bit_for_bit():
+    # The copy-on-write configuration's decode: 16 prompts of 2048 tokens x 8
+    # branches, each one token into its own tail block (ctx 2049).
+    branches = [8] * 16
+    w = W.forked([2048] * 16, branches, [[1] * 8] * 16, 28, 4)
+    run, got, _ = _check(w, expect_groups=16)
+    for _ in range(3):
+        again = run.decode(out_dtype=qvp.DTYPE_F32)
+        assert np.array_equal(again, got), "shared-prefix decode is not deterministic"
