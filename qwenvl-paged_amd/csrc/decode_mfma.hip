@@ -601,6 +601,10 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     }
 }
 
+// Dynamic LDS of the shared-prefix launch: one 32-token tile (16 KiB) per wave.
+constexpr uint32_t kPrefixLdsBytes = kWaves * 16 * 64 * sizeof(u32x4);
+static_assert(kWaves * 16 * kRowPad * sizeof(float) <= kPrefixLdsBytes, "lane merge reuses the tile slots");
+
 struct PrefixArgs {
     const qvp_prefix_item* items;
     int32_t* counters;
@@ -612,8 +616,8 @@ struct PrefixArgs {
 // head g shared by up to eight sequences). The eight waves are four column
 // blocks x two tile lanes: column block k holds sequences k * (16 / G) ..
 // in its MFMA columns (G query heads each), and the two tile lanes take the
-// item's tiles in turn, so each tile is fetched from HBM once and read by the
-// other three column blocks of its lane from L2. The tiles are whole (the
+// item's tiles in steps of eight: each wave fetches one tile of the step and
+// copies it to LDS, where the other column blocks read it. The tiles are whole (the
 // prefix ends before every member's last tile), so no mask applies. At the
 // end the two lanes of each column block merge through LDS and every member's
 // (m, l, O) goes to its slot with agent-scope stores; after they have
@@ -622,7 +626,10 @@ struct PrefixArgs {
 __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(DecodeGeometry p, PrefixArgs a) {
     __shared__ float sm_m[kWaves][16];
     __shared__ float sm_l[kWaves][16];
-    __shared__ float sm_o[kWaves][16][kRowPad];
+    // One tile per wave, [wave][register][lane] (kPrefixLdsBytes), reused for
+    // the lanes' merge once the tiles are done.
+    extern __shared__ u32x4 sm_tiles[];
+    float(&sm_o)[kWaves][16][kRowPad] = *reinterpret_cast<float(*)[kWaves][16][kRowPad]>(sm_tiles);
     const auto* it = as_const(a.items) + blockIdx.x;
     const int gq = it->g;
     const int t0 = it->t0;
@@ -666,18 +673,45 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(Deco
     float m_run = -INFINITY;
     float l_run = 0.f;
     const int end_tok = t1 * kTileTokens;
-    // One tile in flight per wave, the frames of the tile after it resolved
-    // while the current one is computed.
+    // Steps of eight tiles: wave w fetches tile w of the step (one tile in
+    // flight per wave, the frames of its next one resolved meanwhile) and
+    // copies it to its LDS slot; wave (cb, tl) then runs tiles 4 tl .. 4 tl + 3
+    // of the step for its column block, its own from registers first and the
+    // other three from LDS. Each tile is read from HBM once, with eight
+    // distinct tiles in flight per workgroup.
     KvTile nxt;
-    int t = t0 + tl;
     TileRef r2{};
-    if (t < t1) load_tile(p, ref(t), c, j, nxt);
-    if (t + 2 < t1) r2 = ref(t + 2);
-    for (; t < t1; t += 2) {
-        KvTile cur = nxt;
-        if (t + 2 < t1) load_tile(p, r2, c, j, nxt);
-        if (t + 4 < t1) r2 = ref(t + 4);
-        compute_tile(cur, qop, t * kTileTokens, end_tok - 1, end_tok, p.scale_log2, j, m_run, l_run, o);
+    if (t0 + wave < t1) load_tile(p, ref(t0 + wave), c, j, nxt);
+    if (t0 + kWaves + wave < t1) r2 = ref(t0 + kWaves + wave);
+    u32x4* const my_slot = sm_tiles + wave * 16 * 64 + lane;
+    for (int s0 = t0; s0 < t1; s0 += kWaves) {
+        const int tw = s0 + wave;
+        KvTile cur;
+        if (tw < t1) {
+            cur = nxt;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) my_slot[r * 64] = cur.k[r >> 2][r & 3];
+#pragma unroll
+            for (int r = 0; r < 8; ++r) my_slot[(8 + r) * 64] = cur.v[r];
+        }
+        if (tw + kWaves < t1) load_tile(p, r2, c, j, nxt);
+        if (tw + 2 * kWaves < t1) r2 = ref(tw + 2 * kWaves);
+        lds_barrier();
+#pragma unroll 1
+        for (int x = 0; x < 4; ++x) {
+            const int k = 4 * tl + ((cb + x) & 3);
+            const int t = s0 + k;
+            if (t >= t1) continue;
+            if (x > 0) {
+                const u32x4* src = sm_tiles + k * 16 * 64 + lane;
+#pragma unroll
+                for (int r = 0; r < 8; ++r) cur.k[r >> 2][r & 3] = src[r * 64];
+#pragma unroll
+                for (int r = 0; r < 8; ++r) cur.v[r] = src[(8 + r) * 64];
+            }
+            compute_tile(cur, qop, t * kTileTokens, end_tok - 1, end_tok, p.scale_log2, j, m_run, l_run, o);
+        }
+        lds_barrier();
     }
     l_run = sum_over_j(l_run);
     if (j == 0) {
@@ -764,6 +798,8 @@ int device_max_wgs(uint32_t* wgs) {
                 QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, tg), hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
             }
         }
+        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_prefix_groups),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kPrefixLdsBytes)));
         int cus = 0;
         QVP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         g_dev_wgs[dev] = static_cast<uint32_t>(std::max(1, cus) * kWgsPerCu);
@@ -1421,7 +1457,7 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
         pa.ws_acc = a.ws_acc;
         void* pargs[] = {&gk, &pa};
         QVP_HIP(hipLaunchKernel(reinterpret_cast<const void*>(&decode_prefix_groups), dim3(s.num_prefix_items),
-                                dim3(kThreads), pargs, 0, stream));
+                                dim3(kThreads), pargs, kPrefixLdsBytes, stream));
     }
     void* kargs[] = {&gk, &a};
     QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs + copy_wgs), dim3(kThreads), kargs,
