@@ -81,3 +81,72 @@ def test_config4_shape_matches_the_oracle_and_repeats_bit_for_bit():
     for _ in range(3):
         again = run.decode(out_dtype=qvp.DTYPE_F32)
         assert np.array_equal(again, got), "shared-prefix decode is not deterministic"
+
+
+@pytest.mark.parametrize("tpb", [32, 64])
+def test_larger_blocks(tpb):
+    # A 32-token tile is one block (tpb 32) or half of one (tpb 64); the
+    # prefix launch resolves its frames through the table's tpb shift.
+    branches = [6, 3]
+    w = W.forked([1500, 700], branches, _extra(5, branches), 28, 4, tokens_per_block=tpb, solo_lens=[900])
+    _check(w, expect_groups=2)
+
+
+def test_captured_decode_with_shared_prefixes_replays_bit_for_bit():
+    # Both launches (prefix, then the private tails that complete the
+    # merges) in one graph: the counters the prefix launch raises are reset by
+    # the merging workgroups, so every replay starts from zero.
+    branches = [8, 4]
+    w = W.forked([1200, 2600], branches, _extra(6, branches), 28, 4, solo_lens=[333])
+    stream = qvp.Stream()
+    run = GpuRun(w)
+    run.batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, 0, stream)
+    ws = qvp.DeviceBuffer(run.batch.workspace_bytes(w.num_query_heads, w.head_dim))
+    n = w.num_seqs * w.num_query_heads * w.head_dim
+    out = qvp.DeviceBuffer(n * 4)
+    args = qvp.decode_args(query=run.q.ptr, out=out.ptr, kv_base=run.pool.base, block_stride=run.pool.stride,
+                           batch=run.batch, kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_F32, layer=w.layer,
+                           num_layers=w.num_layers, num_query_heads=w.num_query_heads,
+                           num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, tokens_per_block=w.tokens_per_block,
+                           scale=w.scale, strides=w.strides, workspace=ws.ptr, workspace_bytes=ws.nbytes)
+    qvp.paged_decode(args, stream)
+    eager = out.download(np.float32, (n,), stream)
+    assert run.batch.decode_plan()["shared_prefix_groups"] == 2
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    assert_close_bf16(eager.reshape(ref32.shape), ref32, "eager")
+    other = GpuRun(W.forked([900], [5], _extra(7, [5]), 28, 4, seed=12))
+    with qvp.Graph.capture(stream) as graph:
+        qvp.paged_decode(args, stream)
+    for replay in range(4):
+        out.fill(0xFF, stream)
+        graph.launch(stream)
+        stream.synchronize()
+        assert np.array_equal(out.download(np.float32, (n,), stream), eager), f"replay {replay}"
+        other.decode(stream=stream)
+    graph.destroy()
+
+
+def test_allocation_free_entry_point_with_shared_prefixes():
+    branches = [8]
+    w = W.forked([1800], branches, _extra(8, branches), 28, 4, solo_lens=[64, 2000])
+    run = GpuRun(w)
+    stream = qvp.Stream()
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    run.batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, 0, stream)
+    n = w.num_seqs * w.num_query_heads * w.head_dim
+    out = qvp.DeviceBuffer(n * 4)
+    args = qvp.decode_args(query=run.q.ptr, out=out.ptr, kv_base=run.pool.base, block_stride=run.pool.stride,
+                           batch=run.batch, kv_dtype=w.kv_dtype, out_dtype=qvp.DTYPE_F32, layer=w.layer,
+                           num_layers=w.num_layers, num_query_heads=w.num_query_heads,
+                           num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, tokens_per_block=w.tokens_per_block,
+                           scale=w.scale, strides=w.strides)
+    # The schedule is built by a first (allocating) decode; the allocation-free
+    # call then runs on the library's scratch array.
+    qvp.paged_decode(args, stream)
+    first = out.download(np.float32, (n,), stream)
+    out.fill(0xFF, stream)
+    qvp.paged_decode_noalloc(args, stream)
+    got = out.download(np.float32, (n,), stream)
+    assert run.batch.decode_plan()["shared_prefix_groups"] == 1
+    assert np.array_equal(got, first)
+    assert_close_bf16(got.reshape(ref32.shape), ref32, "no-alloc")
