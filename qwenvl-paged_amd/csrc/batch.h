@@ -19,15 +19,18 @@ struct qvp_piece {
 // head g for nmem sequences whose block tables hold the same frames over
 // those tiles (member b[0]'s table supplies them), decoded once for all of
 // them. Member m's partial result goes to workspace slot slot[m] of its
-// (sequence, kv head) segment, whose completion counter is
-// counters[seg_slot0[m]]; the segment's other pieces (its private suffix)
-// are ordinary pieces of the main decode launch.
+// (sequence, kv head) segment of nslots[m] slots, whose completion counter
+// is counters[seg_slot0[m]]. The segment's other slots are the other chunks
+// of the prefix and its private suffix: a short suffix is one entry of the
+// prefix launch's suffix list (a qvp_piece, one wave each), a longer one is
+// made of ordinary pieces of the main decode launch.
 constexpr int kPrefixMaxMembers = 8;
 struct qvp_prefix_item {
     int32_t g, t0, t1, nmem;
     int32_t b[kPrefixMaxMembers];
     int32_t slot[kPrefixMaxMembers];
     int32_t seg_slot0[kPrefixMaxMembers];
+    int32_t nslots[kPrefixMaxMembers];
 };
 
 // The last enqueued consumer of a device buffer: its stream, and an event
@@ -51,6 +54,8 @@ struct qvp_reader {
 //                          two block ids; piece -1 when it has none) and the
 //                          workgroup's piece range (begin, end)
 //   prefix[num_prefix_items] qvp_prefix_item (shared-prefix launch)
+//   suffix[num_suffix]     qvp_piece: short private suffixes of prefix-group
+//                          members, decoded by the shared-prefix launch
 struct qvp_schedule {
     bool valid{false};
     // Device words of the schedule in use: either the batch's packed buffer
@@ -61,6 +66,7 @@ struct qvp_schedule {
     std::vector<int32_t> plan_wg_begin;
     std::vector<qvp_piece> plan_pieces;
     std::vector<qvp_prefix_item> plan_prefix;
+    std::vector<qvp_piece> plan_suffix;
     uint64_t pack_generation{0};
     uint32_t num_kv_heads{0};
     uint32_t group{0};  // query heads per kv head (sizes the deferred LDS and the slots)
@@ -78,8 +84,10 @@ struct qvp_schedule {
     // Shared prefixes decoded once for their sequences (a launch before the
     // main one): work items and the sequence groups they came from.
     uint32_t num_prefix_items{0};
+    uint32_t num_suffix{0};  // entries of the suffix list (eight per workgroup of that launch)
     uint32_t prefix_groups{0};
-    size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, off_first{0}, off_prefix{0}, total{0};  // int32 units
+    size_t off_wg_begin{0}, off_pieces{0}, off_counters{0}, off_first{0}, off_prefix{0}, off_suffix{0},
+        total{0};  // int32 units
     // Two pinned staging buffers, used in turn: rebuilding the schedule for
     // step n + 1 waits only for the upload of the rebuild before last, which
     // the stream reaches once step n - 1's decode is done, so the host can

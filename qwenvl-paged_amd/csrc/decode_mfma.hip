@@ -607,10 +607,92 @@ static_assert(kWaves * 16 * kRowPad * sizeof(float) <= kPrefixLdsBytes, "lane me
 
 struct PrefixArgs {
     const qvp_prefix_item* items;
+    const qvp_piece* suffix;  // short private suffixes, eight per workgroup after the items
     int32_t* counters;
     float* ws_ml;   // the main launch's workspace layout: [slot][group][2]
     float* ws_acc;  // [slot][group][128]
+    void* out;
+    int num_items;
+    int num_suffix;
 };
+
+// Segments the prefix launch completes hold only its own slots: the prefix
+// chunks and a short suffix (kPrefixMaxChunks + 1, checked where the planner's
+// limits are defined).
+constexpr int kPrefixMaxSlots = 9;
+
+// Final merge of the (sequence, kv head) segments a prefix-launch workgroup
+// completed: segs[i] = (sequence, kv head, first slot, slots). Slots written
+// by other workgroups of the launch are read with agent-scope loads. Each
+// segment's counter returns to zero for the next launch.
+template <typename OutT>
+__device__ void merge_prefix_segments(const DecodeGeometry& p, const PrefixArgs& a, int n, const int (*segs)[4]) {
+    // Work items are four consecutive dims of one row; each round issues the
+    // slot loads of kMergeBatch items per thread together (one 8-byte load of
+    // the row's (m, l) and two of its accumulators per slot), so the merge
+    // costs about one round trip per round.
+    const int G = static_cast<int>(p.group);
+    const int per_seg = G * (kD / 4);
+    const int total = n * per_seg;
+    OutT* out = static_cast<OutT*>(a.out);
+    for (int f0 = threadIdx.x; f0 < total; f0 += kThreads * kMergeBatch) {
+        int ri[kMergeBatch], dq[kMergeBatch], s0[kMergeBatch], ns[kMergeBatch];
+        uint64_t orow[kMergeBatch];
+        uint64_t ml[kMergeBatch][kPrefixMaxSlots], o01[kMergeBatch][kPrefixMaxSlots], o23[kMergeBatch][kPrefixMaxSlots];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const int f = f0 + i * kThreads;
+            const int si = f < total ? f / per_seg : 0;
+            const int e = f < total ? f - si * per_seg : 0;
+            ri[i] = e >> 5;
+            dq[i] = e & 31;
+            s0[i] = segs[si][2];
+            ns[i] = f < total ? min(segs[si][3], kPrefixMaxSlots) : 0;
+            orow[i] = (static_cast<uint64_t>(segs[si][0]) * p.num_q_heads + segs[si][1] * G + ri[i]) * kD;
+#pragma unroll
+            for (int x = 0; x < kPrefixMaxSlots; ++x) {
+                ml[i][x] = 0;
+                o01[i][x] = 0;
+                o23[i][x] = 0;
+                if (x < ns[i]) {
+                    const uint64_t row = static_cast<uint64_t>(s0[i] + x) * G + ri[i];
+                    ml[i][x] = __hip_atomic_load(reinterpret_cast<const uint64_t*>(a.ws_ml + row * 2), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+                    const uint64_t* op = reinterpret_cast<const uint64_t*>(a.ws_acc + row * kD + 4 * dq[i]);
+                    o01[i][x] = __hip_atomic_load(op, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    o23[i][x] = __hip_atomic_load(op + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            if (f0 + i * kThreads >= total) continue;
+            float mmax = -INFINITY;
+#pragma unroll
+            for (int x = 0; x < kPrefixMaxSlots; ++x) {
+                if (x < ns[i]) mmax = fmaxf(mmax, __uint_as_float(static_cast<uint32_t>(ml[i][x])));
+            }
+            float lsum = 0.f;
+            float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int x = 0; x < kPrefixMaxSlots; ++x) {
+                const float m = __uint_as_float(static_cast<uint32_t>(ml[i][x]));
+                const float f = x < ns[i] && m != -INFINITY ? fast_exp2(m - mmax) : 0.f;
+                lsum += __uint_as_float(static_cast<uint32_t>(ml[i][x] >> 32)) * f;
+                acc[0] += __uint_as_float(static_cast<uint32_t>(o01[i][x])) * f;
+                acc[1] += __uint_as_float(static_cast<uint32_t>(o01[i][x] >> 32)) * f;
+                acc[2] += __uint_as_float(static_cast<uint32_t>(o23[i][x])) * f;
+                acc[3] += __uint_as_float(static_cast<uint32_t>(o23[i][x] >> 32)) * f;
+            }
+            OutT* dst = out + orow[i] + 4 * dq[i];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) dst[k] = from_float<OutT>(acc[k] / lsum);
+        }
+    }
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        __hip_atomic_store(&a.counters[segs[i][2]], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
 
 // Shared-prefix launch: one workgroup per work item (tiles [t0, t1) of kv
 // head g shared by up to eight sequences). The eight waves are four column
@@ -621,15 +703,100 @@ struct PrefixArgs {
 // prefix ends before every member's last tile), so no mask applies. At the
 // end the two lanes of each column block merge through LDS and every member's
 // (m, l, O) goes to its slot with agent-scope stores; after they have
-// completed, one increment per member counts the chunk into its segment, whose
-// private pieces (main launch, later on the stream) complete and merge it.
+// completed, one increment per member counts the chunk into its segment.
+// Workgroups after the items decode short private suffixes, one segment per
+// wave (tiles [t0, t1) of the member's own frames, masked at its context
+// end), and count them in the same way. The workgroup whose increment
+// completes a segment merges it and writes the output; a segment with a long
+// suffix is completed by its pieces in the main launch, later on the stream.
+template <typename OutT>
 __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(DecodeGeometry p, PrefixArgs a) {
     __shared__ float sm_m[kWaves][16];
     __shared__ float sm_l[kWaves][16];
+    __shared__ int sm_seg[kWaves][4];
+    __shared__ int sm_nseg;
     // One tile per wave, [wave][register][lane] (kPrefixLdsBytes), reused for
     // the lanes' merge once the tiles are done.
     extern __shared__ u32x4 sm_tiles[];
     float(&sm_o)[kWaves][16][kRowPad] = *reinterpret_cast<float(*)[kWaves][16][kRowPad]>(sm_tiles);
+    if (static_cast<int>(blockIdx.x) >= a.num_items) {
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+        const int lane = threadIdx.x & 63;
+        const int c = lane & 15;
+        const int j = lane >> 4;
+        const int G = static_cast<int>(p.group);
+        const int e = (static_cast<int>(blockIdx.x) - a.num_items) * kWaves + wave;
+        const bool have = e < a.num_suffix;
+        qvp_piece d{};
+        if (have) {
+            d = piece_at(a.suffix, e);
+            const uint16_t* qp = static_cast<const uint16_t*>(p.query) +
+                                 (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + min(c, G - 1)) * kD;
+            u32x4 qop[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i + 8 * j);
+            const auto* row = as_const(p.tables) + static_cast<uint64_t>(d.b) * p.max_nb;
+            auto sref = [&](int t) {
+                TileRef r{};
+                r.b = d.b;
+                r.g = d.g;
+                r.t = t;
+                r.ctx = d.ctx;
+                r.blk0 = row[min(t * kTileTokens, d.ctx - 1) >> p.tpb_shift];
+                r.blk1 = row[min(t * kTileTokens + 16, d.ctx - 1) >> p.tpb_shift];
+                return r;
+            };
+            floatx4 o[8];
+#pragma unroll
+            for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+            float m_run = -INFINITY;
+            float l_run = 0.f;
+            KvTile nxt;
+            TileRef r2{};
+            load_tile(p, sref(d.t0), c, j, nxt);
+            if (d.t0 + 1 < d.t1) r2 = sref(d.t0 + 1);
+            for (int t = d.t0; t < d.t1; ++t) {
+                KvTile cur = nxt;
+                if (t + 1 < d.t1) load_tile(p, r2, c, j, nxt);
+                if (t + 2 < d.t1) r2 = sref(t + 2);
+                compute_tile(cur, qop, t * kTileTokens, d.ctx - 1, d.ctx, p.scale_log2, j, m_run, l_run, o);
+            }
+            l_run = sum_over_j(l_run);
+            if (c < G) {
+                const uint64_t ri = static_cast<uint64_t>(d.slot) * G + c;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int n = 0; n < 8; ++n) {
+                        __hip_atomic_store(&a.ws_acc[ri * kD + 32 * j + 8 * r + n], o[n][r], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    }
+                if (j == 0) {
+                    __hip_atomic_store(&a.ws_ml[ri * 2 + 0], m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&a.ws_ml[ri * 2 + 1], l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
+        // Every wave's slot stores have completed before any segment is counted.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (threadIdx.x == 0) sm_nseg = 0;
+        __syncthreads();
+        if (have && lane == 0) {
+            const int done = __hip_atomic_fetch_add(&a.counters[d.seg_slot0], 1, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+            if (done == d.seg_nslots - 1) {
+                const int at = __hip_atomic_fetch_add(&sm_nseg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                sm_seg[at][0] = d.b;
+                sm_seg[at][1] = d.g;
+                sm_seg[at][2] = d.seg_slot0;
+                sm_seg[at][3] = d.seg_nslots;
+            }
+        }
+        __syncthreads();
+        const int nseg = __builtin_amdgcn_readfirstlane(sm_nseg);
+        if (nseg > 0) merge_prefix_segments<OutT>(p, a, nseg, sm_seg);
+        return;
+    }
     const auto* it = as_const(a.items) + blockIdx.x;
     const int gq = it->g;
     const int t0 = it->t0;
@@ -746,10 +913,36 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(Deco
     }
     // Every wave's slot stores have completed before any member is counted.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (threadIdx.x == 0) sm_nseg = 0;
     __syncthreads();
     if (static_cast<int>(threadIdx.x) < nmem) {
-        (void)__hip_atomic_fetch_add(&a.counters[as_const(a.items)[blockIdx.x].seg_slot0[threadIdx.x]], 1,
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int mi = static_cast<int>(threadIdx.x);
+        const int seg0 = as_const(a.items)[blockIdx.x].seg_slot0[mi];
+        const int nsl = as_const(a.items)[blockIdx.x].nslots[mi];
+        const int done = __hip_atomic_fetch_add(&a.counters[seg0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == nsl - 1) {
+            const int at = __hip_atomic_fetch_add(&sm_nseg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            sm_seg[at][0] = as_const(a.items)[blockIdx.x].b[mi];
+            sm_seg[at][1] = gq;
+            sm_seg[at][2] = seg0;
+            sm_seg[at][3] = nsl;
+        }
+    }
+    __syncthreads();
+    const int nseg = __builtin_amdgcn_readfirstlane(sm_nseg);
+    if (nseg > 0) merge_prefix_segments<OutT>(p, a, nseg, sm_seg);
+}
+
+template <typename OutT>
+const void* prefix_kernel_for() {
+    return reinterpret_cast<const void*>(&decode_prefix_groups<OutT>);
+}
+
+const void* prefix_kernel(uint32_t out_dtype) {
+    switch (out_dtype) {
+        case QVP_DTYPE_F32: return prefix_kernel_for<float>();
+        case QVP_DTYPE_BF16: return prefix_kernel_for<uint16_t>();
+        default: return prefix_kernel_for<_Float16>();
     }
 }
 
@@ -798,8 +991,10 @@ int device_max_wgs(uint32_t* wgs) {
                 QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, tg), hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
             }
         }
-        QVP_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_prefix_groups),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kPrefixLdsBytes)));
+        for (uint32_t dt : {QVP_DTYPE_F32, QVP_DTYPE_BF16, QVP_DTYPE_F16}) {
+            QVP_HIP(hipFuncSetAttribute(prefix_kernel(dt), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kPrefixLdsBytes)));
+        }
         int cus = 0;
         QVP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
         g_dev_wgs[dev] = static_cast<uint32_t>(std::max(1, cus) * kWgsPerCu);
@@ -945,6 +1140,9 @@ std::vector<uint64_t> cut_ranges(const std::vector<uint64_t>& pos_cum, uint32_t 
 constexpr uint32_t kPrefixMinTiles = 4;
 constexpr uint64_t kPrefixMinChunkTiles = 8;
 constexpr uint64_t kPrefixMaxChunks = 8;
+static_assert(kPrefixMaxSlots == kPrefixMaxChunks + 1, "prefix-launch merge holds every slot of a segment");
+// Private suffixes of at most this many tiles are decoded by the prefix launch.
+constexpr uint32_t kSuffixMaxTiles = 4;
 
 struct PrefixGroup {
     int nmem{0};
@@ -1065,8 +1263,16 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     // each sequence's tiles from start[b] on.
     std::vector<PrefixGroup> groups = allow_prefix ? find_prefix_groups(in, g, hps) : std::vector<PrefixGroup>{};
     std::vector<uint32_t> start(nseq, 0);
+    // A member whose private suffix is short has it decoded by the prefix
+    // launch too (one wave per segment) and leaves the main launch.
+    std::vector<uint8_t> short_suffix(nseq, 0);
     for (const PrefixGroup& pg : groups) {
-        for (int m = 0; m < pg.nmem; ++m) start[pg.b[m]] = pg.tiles;
+        for (int m = 0; m < pg.nmem; ++m) {
+            const uint32_t b = pg.b[m];
+            const uint32_t tiles = (in.lens[b] + kTileTokens - 1) / kTileTokens;
+            short_suffix[b] = tiles - pg.tiles <= kSuffixMaxTiles;
+            start[b] = short_suffix[b] ? tiles : pg.tiles;
+        }
     }
     if (!groups.empty()) {
         for (uint32_t b = 0; b < nseq; ++b) {
@@ -1131,7 +1337,7 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     // in positions of this segment shape (each position is hps tiles over
     // kWaves waves) that is kPieceBoundaryTiles * kWaves / hps.
     const double cb = kPieceBoundaryTiles * kWaves / hps;
-    for (uint32_t q = 0; q < nq; ++q) {
+    for (uint32_t q = 0; q < nq && T > 0; ++q) {
         const std::vector<uint64_t> bd = cut_ranges(pos_cum, Rq[q], cb, in.partition_tiles);
         for (uint32_t r = 0; r < Rq[q]; ++r) ranges.push_back({bd[r], bd[r + 1], q});
     }
@@ -1178,15 +1384,24 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     // A shared prefix is cut into chunks of about equal size, so that the
     // prefix launch has about one work item per CU; each chunk is one more
     // piece (and slot) of every member's segment, and comes first in it.
+    // The short suffixes take workgroups of the same launch, eight segments
+    // each.
     uint64_t prefix_tiles = 0;
-    for (const PrefixGroup& pg : groups) prefix_tiles += static_cast<uint64_t>(pg.tiles) * nq;
-    const uint64_t chunk_tiles = std::max<uint64_t>(kPrefixMinChunkTiles, (prefix_tiles + max_wgs - 1) / max_wgs);
+    uint64_t n_suffix = 0;
+    for (const PrefixGroup& pg : groups) {
+        prefix_tiles += static_cast<uint64_t>(pg.tiles) * nq;
+        for (int m = 0; m < pg.nmem; ++m) n_suffix += short_suffix[pg.b[m]] ? nq : 0;
+    }
+    const uint64_t suffix_wgs = (n_suffix + kWaves - 1) / kWaves;
+    const uint64_t chunk_wgs = max_wgs > suffix_wgs + 1 ? max_wgs - suffix_wgs : 1;
+    const uint64_t chunk_tiles = std::max<uint64_t>(kPrefixMinChunkTiles, (prefix_tiles + chunk_wgs - 1) / chunk_wgs);
     for (PrefixGroup& pg : groups) {
         pg.chunks = static_cast<int>(std::min<uint64_t>(kPrefixMaxChunks, (pg.tiles + chunk_tiles - 1) / chunk_tiles));
         for (int m = 0; m < pg.nmem; ++m) {
+            const int extra = short_suffix[pg.b[m]] ? 1 : 0;
             for (uint32_t q = 0; q < nq; ++q) {
                 const size_t k = static_cast<size_t>(pg.b[m]) * nq + q;
-                seg_count[k] += pg.chunks;
+                seg_count[k] += pg.chunks + extra;
                 seg_next[k] = pg.chunks;
             }
         }
@@ -1221,8 +1436,31 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
                     it.b[m] = static_cast<int32_t>(pg.b[mm]);
                     it.seg_slot0[m] = seg_base[k];
                     it.slot[m] = seg_base[k] + ch;
+                    it.nslots[m] = seg_count[k];
                 }
                 items.push_back(it);
+            }
+        }
+    }
+    // Short suffixes: the slot after the member's prefix chunks.
+    std::vector<qvp_piece>& suffix = s.plan_suffix;
+    suffix.clear();
+    for (const PrefixGroup& pg : groups) {
+        for (int m = 0; m < pg.nmem; ++m) {
+            const uint32_t b = pg.b[m];
+            if (!short_suffix[b]) continue;
+            for (uint32_t q = 0; q < nq; ++q) {
+                const size_t k = static_cast<size_t>(b) * nq + q;
+                qvp_piece pc{};
+                pc.b = static_cast<int32_t>(b);
+                pc.g = static_cast<int32_t>(q);
+                pc.t0 = static_cast<int32_t>(pg.tiles);
+                pc.t1 = static_cast<int32_t>(start[b]);
+                pc.ctx = static_cast<int32_t>(in.lens[b]);
+                pc.slot = seg_base[k] + seg_next[k];
+                pc.seg_slot0 = seg_base[k];
+                pc.seg_nslots = seg_count[k];
+                suffix.push_back(pc);
             }
         }
     }
@@ -1263,7 +1501,8 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     s.off_first = s.off_counters + align_ints(std::max<int32_t>(next_slot, 1));
     const size_t first_words = static_cast<size_t>(Wn) * kWaves * kFirstWords;
     s.off_prefix = s.off_first + align_ints(first_words);
-    s.total = s.off_prefix + align_ints(items.size() * (sizeof(qvp_prefix_item) / sizeof(int32_t)));
+    s.off_suffix = s.off_prefix + align_ints(items.size() * (sizeof(qvp_prefix_item) / sizeof(int32_t)));
+    s.total = s.off_suffix + align_ints(suffix.size() * (sizeof(qvp_piece) / sizeof(int32_t)));
 
     s.pack_generation = in.generation;
     s.num_kv_heads = num_kv_heads;
@@ -1278,6 +1517,7 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     s.hps = hps;
     s.max_partial_pieces_per_wg = max_partial;
     s.num_prefix_items = static_cast<uint32_t>(items.size());
+    s.num_suffix = static_cast<uint32_t>(suffix.size());
     s.prefix_groups = static_cast<uint32_t>(groups.size());
     return QVP_OK;
 }
@@ -1299,6 +1539,8 @@ void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t
     std::copy(praw, praw + pieces.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_pieces);
     const int32_t* xraw = reinterpret_cast<const int32_t*>(s.plan_prefix.data());
     std::copy(xraw, xraw + s.plan_prefix.size() * (sizeof(qvp_prefix_item) / sizeof(int32_t)), h + s.off_prefix);
+    const int32_t* sraw = reinterpret_cast<const int32_t*>(s.plan_suffix.data());
+    std::copy(sraw, sraw + s.plan_suffix.size() * (sizeof(qvp_piece) / sizeof(int32_t)), h + s.off_suffix);
     // Each wave's first tile, resolved to frames here (the kernel's
     // next_tile and resolve_tile for its first step), written straight into
     // the staging buffer (its other words stay zero).
@@ -1452,16 +1694,24 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     if (s.num_prefix_items > 0) {
         PrefixArgs pa{};
         pa.items = reinterpret_cast<const qvp_prefix_item*>(s.words + s.off_prefix);
+        pa.suffix = reinterpret_cast<const qvp_piece*>(s.words + s.off_suffix);
         pa.counters = a.counters;
         pa.ws_ml = a.ws_ml;
         pa.ws_acc = a.ws_acc;
+        pa.out = out;
+        pa.num_items = static_cast<int>(s.num_prefix_items);
+        pa.num_suffix = static_cast<int>(s.num_suffix);
+        const uint32_t grid = s.num_prefix_items + (s.num_suffix + kWaves - 1) / kWaves;
         void* pargs[] = {&gk, &pa};
-        QVP_HIP(hipLaunchKernel(reinterpret_cast<const void*>(&decode_prefix_groups), dim3(s.num_prefix_items),
-                                dim3(kThreads), pargs, kPrefixLdsBytes, stream));
+        QVP_HIP(hipLaunchKernel(prefix_kernel(out_dtype), dim3(grid), dim3(kThreads), pargs, kPrefixLdsBytes, stream));
     }
-    void* kargs[] = {&gk, &a};
-    QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs + copy_wgs), dim3(kThreads), kargs,
-                            s.lds_bytes, stream));
+    // Every sequence may be covered by the prefix launch (then only a carried
+    // upload, if any, needs this one).
+    if (s.num_wgs + copy_wgs > 0) {
+        void* kargs[] = {&gk, &a};
+        QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs + copy_wgs), dim3(kThreads),
+                                kargs, s.lds_bytes, stream));
+    }
     // The merge runs inside the kernel; the event still marks the split/merge
     // boundary for callers that time the two phases.
     if (split_event != nullptr) QVP_HIP(hipEventRecord(split_event, stream));
