@@ -150,3 +150,25 @@ def test_allocation_free_entry_point_with_shared_prefixes():
     assert run.batch.decode_plan()["shared_prefix_groups"] == 1
     assert np.array_equal(got, first)
     assert_close_bf16(got.reshape(ref32.shape), ref32, "no-alloc")
+
+
+def test_long_and_short_private_tails_in_one_batch():
+    # Branches with tails of at most four tiles are finished by the prefix
+    # launch; longer tails (up to 900 tokens here) are pieces of the
+    # persistent decode, which completes and merges those segments.
+    branches = [6, 4]
+    extra = [[1, 3, 500, 40, 900, 127], [2, 640, 5, 96]]
+    w = W.forked([1400, 2050], branches, extra, 28, 4, solo_lens=[1200])
+    run, got32, _ = _check(w, expect_groups=2)
+    plan = run.batch.decode_plan()
+    assert plan["workgroups"] > 0, plan  # the long tails need the persistent decode
+
+
+def test_half_precision_output_from_the_prefix_launch():
+    branches = [8]
+    w = W.forked([2048], branches, [[1] * 8], 28, 4)
+    run = GpuRun(w)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F16)
+    assert run.batch.decode_plan()["workgroups"] == 0  # every tail was short: one launch
+    assert_close_16bit(got, ref32, qvp.DTYPE_F16, "f16 out")
