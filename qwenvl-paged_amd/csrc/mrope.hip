@@ -232,7 +232,8 @@ extern "C" int qvp_mrope_positions(qvp_mrope* m, const qvp_mrope_span* spans, co
     hipStream_t s = qvp::as_stream(stream);
     const int slot = m->parity;
     if (m->staging_done[slot] == nullptr) {
-        QVP_HIP(hipEventCreateWithFlags(&m->staging_done[slot], hipEventDisableTiming));
+        // Host-side reuse of pinned staging only: no system-scope release.
+        QVP_HIP(hipEventCreateWithFlags(&m->staging_done[slot], hipEventDisableTiming | hipEventDisableSystemFence));
     }
     // The staging buffer about to be refilled may still be read by the copy of
     // the call before last.

@@ -125,8 +125,13 @@ int qvp_batch_create(qvp_batch** batch) {
     *batch = nullptr;
     qvp_batch* b = new (std::nothrow) qvp_batch();
     if (b == nullptr) return fail(QVP_ERR_OUT_OF_MEMORY, "batch descriptor");
+    // The staging events only tell the host that the device has finished
+    // reading pinned memory; no device write needs to become visible to the
+    // host through them, so they skip the system-scope release (a cache
+    // writeback between two decodes when a decode carries an upload).
     for (int i = 0; i < 2; ++i) {
-        hipError_t err = hipEventCreateWithFlags(&b->staging_done[i], hipEventDisableTiming);
+        hipError_t err =
+            hipEventCreateWithFlags(&b->staging_done[i], hipEventDisableTiming | hipEventDisableSystemFence);
         if (err != hipSuccess) {
             if (i == 1) (void)hipEventDestroy(b->staging_done[0]);
             delete b;

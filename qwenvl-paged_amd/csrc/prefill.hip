@@ -481,7 +481,10 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
     });
     if (items.size() > 0x7fffffffu) return fail(QVP_ERR_INVALID_ARGUMENT, "too many prefill items");
     const size_t ints = items.size() * (sizeof(qvp::PrefillItem) / sizeof(int32_t));
-    if (plan.staging_done == nullptr) QVP_HIP(hipEventCreateWithFlags(&plan.staging_done, hipEventDisableTiming));
+    // Host-side reuse of pinned staging only: no system-scope release.
+    if (plan.staging_done == nullptr) {
+        QVP_HIP(hipEventCreateWithFlags(&plan.staging_done, hipEventDisableTiming | hipEventDisableSystemFence));
+    }
     if (plan.staging_pending) {
         QVP_HIP(hipEventSynchronize(plan.staging_done));
         plan.staging_pending = false;
