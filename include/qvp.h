@@ -342,8 +342,11 @@ int qvp_batch_upload(qvp_batch* batch, void* stream);
  * call is refused with QVP_ERR_CAPACITY before anything is enqueued. Every
  * call on a device shares that device's array: calls that overlap on one
  * device (e.g. on two streams) race and must be ordered by the caller. The
- * array needs no initial contents (every word the kernels read was written
- * earlier in the same launch). */
+ * array needs no initial contents: every word the kernels read was written
+ * earlier in the same call (with shared prefixes, the prefix launch writes
+ * slots the main launch then reads; the two run back to back on the stream,
+ * so another call on the device must not be enqueued between them, i.e. the
+ * caller orders whole calls). */
 int qvp_paged_decode_noalloc(const qvp_decode_args* args, void* stream);
 
 /* The work decomposition of the last qvp_paged_decode enqueued on a batch.

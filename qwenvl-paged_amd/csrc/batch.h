@@ -166,16 +166,19 @@ struct PendingUpload {
     size_t n16{0};
     uint32_t tail{0};
 };
-// Enqueues the batch's own pending upload (its current pack) on `stream`.
-int flush_own_upload(qvp_batch* batch, hipStream_t stream);
+// Enqueues the batch's own pending upload (its current pack) on `stream`,
+// after the slot's previous reader when that ran on another stream. Without
+// may_allocate no event object is created (the host waits instead).
+int flush_own_upload(qvp_batch* batch, hipStream_t stream, bool may_allocate = true);
 // Takes one pending upload registered on `stream` by a batch other than
 // `exclude`; returns false when there is none. The caller enqueues the copy
 // and then calls finish_taken_upload on the same stream.
 bool take_pending_upload(hipStream_t stream, const qvp_batch* exclude, PendingUpload* out);
 int finish_taken_upload(const PendingUpload& u, hipStream_t stream);
 // Makes `stream` wait on the device for a buffer's last reader when that
-// reader was enqueued on another stream.
-int wait_for_reader(qvp_reader& r, hipStream_t stream);
+// reader was enqueued on another stream. Without may_allocate no event object
+// is created: the host then waits for the reader's stream.
+int wait_for_reader(qvp_reader& r, hipStream_t stream, bool may_allocate = true);
 // Records `stream` as a buffer's last reader (call after its kernels);
 // `writer` is the stream that wrote the buffer. Without may_allocate no event
 // object is created.

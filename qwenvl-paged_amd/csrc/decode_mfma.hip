@@ -617,8 +617,8 @@ struct PrefixArgs {
 };
 
 // Segments the prefix launch completes hold only its own slots: the prefix
-// chunks and a short suffix (kPrefixMaxChunks + 1, checked where the planner's
-// limits are defined).
+// chunks and a short suffix (kPrefixMaxChunks + 1). plan_schedule drops the
+// shared prefixes of a batch whose plan would give such a segment more.
 constexpr int kPrefixMaxSlots = 9;
 
 // Final merge of the (sequence, kv head) segments a prefix-launch workgroup
@@ -1403,6 +1403,19 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
                 const size_t k = static_cast<size_t>(pg.b[m]) * nq + q;
                 seg_count[k] += pg.chunks + extra;
                 seg_next[k] = pg.chunks;
+            }
+        }
+    }
+    // A segment whose every piece is in the prefix launch (a short-suffix
+    // member's) is merged there, from at most kPrefixMaxSlots slots held in
+    // registers; a plan that would give one more is planned without groups.
+    for (const PrefixGroup& pg : groups) {
+        for (int m = 0; m < pg.nmem; ++m) {
+            if (!short_suffix[pg.b[m]]) continue;
+            for (uint32_t q = 0; q < nq; ++q) {
+                if (seg_count[static_cast<size_t>(pg.b[m]) * nq + q] > kPrefixMaxSlots) {
+                    return plan_schedule(s, in, g, false);
+                }
             }
         }
     }

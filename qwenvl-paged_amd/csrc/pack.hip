@@ -91,9 +91,12 @@ int finish_taken_upload(const PendingUpload& u, hipStream_t stream) {
     return QVP_OK;
 }
 
-int flush_own_upload(qvp_batch* batch, hipStream_t stream) {
+int flush_own_upload(qvp_batch* batch, hipStream_t stream, bool may_allocate) {
     const int slot = batch->current;
     if (!batch->upload_pending[slot]) return QVP_OK;
+    // The pack waited on its own stream for the slot's previous reader; an
+    // upload enqueued on another stream has to wait for that reader too.
+    QVP_TRY(wait_for_reader(batch->readers[slot], stream, may_allocate));
     unregister_pending(batch);
     QVP_TRY(pull_from_pinned(batch->device[slot], batch->staging[slot], batch->upload_bytes[slot], stream));
     PendingUpload u{};
@@ -452,11 +455,18 @@ int qvp_batch_upload(qvp_batch* batch, void* stream) {
 
 namespace qvp {
 
-int wait_for_reader(qvp_reader& r, hipStream_t stream) {
+int wait_for_reader(qvp_reader& r, hipStream_t stream, bool may_allocate) {
     if (!r.pending || r.stream == stream) return QVP_OK;
     if (!r.recorded) {
         // The reader's stream has the read enqueued; an event recorded on it
         // now completes after that read (and whatever followed it there).
+        // Without an event object and leave to create one, the host waits
+        // for that stream instead.
+        if (r.event == nullptr && !may_allocate) {
+            QVP_HIP(hipStreamSynchronize(r.stream));
+            r.pending = false;
+            return QVP_OK;
+        }
         if (r.event == nullptr) QVP_HIP(hipEventCreateWithFlags(&r.event, hipEventDisableTiming));
         QVP_HIP(hipEventRecord(r.event, r.stream));
         r.recorded = true;

@@ -215,6 +215,17 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         }
         QVP_TRY(scratch_address(&ws));
     }
+    // A pack left pending by qvp_pack_ahead is uploaded before its decode;
+    // under graph capture the copy would replay from staging a later pack
+    // rewrites, so a capture neither uploads nor carries one. Refused before
+    // anything (a schedule upload included) is enqueued.
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    QVP_HIP(hipStreamIsCapturing(s, &capture));
+    const bool capturing = capture != hipStreamCaptureStatusNone;
+    if (capturing && batch->upload_pending[batch->current]) {
+        return fail(QVP_ERR_INVALID_ARGUMENT,
+                    "the batch's qvp_pack_ahead upload is still pending: enqueue it (qvp_batch_upload) before capture");
+    }
     if (mfma) {
         QVP_TRY(qvp::mfma_prepare_schedule(batch, g, s, !no_alloc));
         need = qvp::mfma_workspace_bytes(batch, g.group, g.head_dim);
@@ -234,17 +245,7 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
     } else if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
     }
-    // A pack left pending by qvp_pack_ahead is uploaded before its decode;
-    // under graph capture the copy would replay from staging a later pack
-    // rewrites, so a capture neither uploads nor carries one.
-    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-    QVP_HIP(hipStreamIsCapturing(s, &capture));
-    const bool capturing = capture != hipStreamCaptureStatusNone;
-    if (capturing && batch->upload_pending[batch->current]) {
-        return fail(QVP_ERR_INVALID_ARGUMENT,
-                    "the batch's qvp_pack_ahead upload is still pending: enqueue it (qvp_batch_upload) before capture");
-    }
-    QVP_TRY(qvp::flush_own_upload(batch, s));
+    QVP_TRY(qvp::flush_own_upload(batch, s, !no_alloc));
     qvp_decode_plan plan{};
     plan.query_group = g.group;
     int status = QVP_OK;

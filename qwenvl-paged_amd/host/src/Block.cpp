@@ -16,8 +16,12 @@ bool LogicalBlock::empty() const noexcept { return token_count == 0; }
 
 namespace {
 
-std::size_t round_up(std::size_t value, std::size_t alignment) noexcept {
-    return alignment == 0 ? value : (value + alignment - 1) / alignment * alignment;
+// Bytes of a host frame for `shape`: whole alignment units, at least one, so
+// the request is one std::aligned_alloc accepts and data() is never null,
+// even for a shape with a zero extent.
+std::size_t host_frame_bytes(const BlockShape& shape, std::size_t alignment) noexcept {
+    const std::size_t units = (shape.byte_size() + alignment - 1) / alignment;
+    return (units == 0 ? 1 : units) * alignment;
 }
 
 }  // namespace
@@ -28,15 +32,13 @@ void PhysicalBlock::Release::operator()(std::byte* p) const noexcept {
 
 PhysicalBlock::PhysicalBlock(PhysicalBlockId id, BlockShape shape, HostMemoryOptions memory_options)
     : id_(id), shape_(shape), memory_options_(memory_options) {
+    // An alignment of 0 in the options means the library default; the options
+    // themselves are kept as given (alignment_bytes() reports them).
     const std::size_t alignment =
         memory_options_.alignment_bytes == 0 ? kDefaultBlockAlignmentBytes : memory_options_.alignment_bytes;
-    // aligned_alloc wants a size that is a multiple of the alignment, and
-    // never zero.
-    std::size_t bytes = round_up(shape_.byte_size(), alignment);
-    if (bytes == 0) bytes = alignment;
-    storage_ = std::unique_ptr<std::byte, Release>(static_cast<std::byte*>(std::aligned_alloc(alignment, bytes)),
-                                                   Release{true});
-    size_bytes_ = bytes;
+    size_bytes_ = host_frame_bytes(shape_, alignment);
+    storage_ = std::unique_ptr<std::byte, Release>(
+        static_cast<std::byte*>(std::aligned_alloc(alignment, size_bytes_)), Release{true});
 }
 
 PhysicalBlock::PhysicalBlock(PhysicalBlockId id, BlockShape shape, HostMemoryOptions memory_options,
@@ -58,7 +60,9 @@ bool PhysicalBlock::pinned_memory_requested() const noexcept { return memory_opt
 BlockPlacement PhysicalBlock::placement() const noexcept { return placement_; }
 
 void PhysicalBlock::swap(PhysicalBlock& other) noexcept {
-    // The id stays with the block; the storage and what describes it move.
+    // Exchanges frames: storage, padded size, placement, and the shape and
+    // options that describe the bytes. Ids are not exchanged, so each object
+    // still answers to the slot the allocator keeps it in.
     std::swap(shape_, other.shape_);
     std::swap(memory_options_, other.memory_options_);
     std::swap(size_bytes_, other.size_bytes_);

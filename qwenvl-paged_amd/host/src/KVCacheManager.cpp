@@ -20,8 +20,9 @@ bool CacheView::valid() const noexcept {
 
 const std::byte* CacheView::block_bytes(LogicalBlockIndex index) const noexcept {
     if (!valid()) return nullptr;
-    // lookup() faults on swapped-out entries too: their frame went back to
-    // the pool and may hold another sequence's data now.
+    // A swapped-out entry owns no frame (its bytes sit in a swap slot, and
+    // the frame id it last had is free for the allocator to reuse), so
+    // lookup() answers nullopt for it as for an unmapped one.
     const std::optional<PhysicalBlockId> frame = block_table->lookup(index);
     const PhysicalBlock* b = frame ? allocator->block(*frame) : nullptr;
     return b != nullptr ? b->data() : nullptr;

@@ -5,9 +5,13 @@
 // src/SwapBackend.cpp:10-51), which the replay test checks over a random
 // operation mix.
 #include "../../oracle/trace_driver.h"
+#include "../../qwenvl-paged_amd/host/bench/kv_pattern.h"
 #include "device_harness.h"
 #include "golden_path.h"
+#include "qvp.h"
+#include "qwenvl_paged/KVAppend.h"
 
+#include <deque>
 #include <map>
 #include <random>
 
@@ -358,4 +362,197 @@ TEST(DeviceAllocatorTest, DeviceEngineReproducesTheConfig5Trace) {
     EXPECT_TRUE(log == expected) << golden::first_difference(log, expected);
     EXPECT_TRUE(allocator.synchronize());
     EXPECT_GT(allocator.swap_launches(), 0u);
+}
+
+namespace {
+
+float bf16_value(std::uint16_t bits) {
+    const std::uint32_t u = static_cast<std::uint32_t>(bits) << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+// Device work of the swap-beside-engine test: K/V rows of the seeded pattern
+// appended through KVAppendBatch, and batched decodes into their own output
+// buffers, all enqueued on the allocator's engine stream without waiting.
+struct EngineSteps {
+    static constexpr std::uint32_t kHq = 28, kHkv = 4, kD = 128, kRow = kHkv * kD, kQRow = kHq * kD;
+
+    explicit EngineSteps(DeviceHarness& harness) : h(harness) {}
+    ~EngineSteps() {
+        for (void* p : buffers) (void)qvp_free(p);
+    }
+
+    void* device_copy(const std::vector<std::uint16_t>& host) {
+        void* d = nullptr;
+        if (qvp_malloc(&d, host.size() * 2) != QVP_OK) return nullptr;
+        buffers.push_back(d);
+        if (qvp_memcpy_htod(d, host.data(), host.size() * 2, h.allocator.stream()) != QVP_OK) return nullptr;
+        return d;
+    }
+
+    // Rows [from, to) of sequence seq.
+    bool append(SequenceId seq, std::uint32_t from, std::uint32_t to) {
+        std::vector<SequenceId> seqs;
+        std::vector<TokenPosition> pos;
+        std::vector<std::uint16_t>& k = staged.emplace_back(static_cast<std::size_t>(to - from) * kRow);
+        std::vector<std::uint16_t>& v = staged.emplace_back(static_cast<std::size_t>(to - from) * kRow);
+        for (std::uint32_t t = from; t < to; ++t) {
+            seqs.push_back(seq);
+            pos.push_back(t);
+            kv_pattern::kv_row(seq, t, 0, k.data() + static_cast<std::size_t>(t - from) * kRow, kRow);
+            kv_pattern::kv_row(seq, t, 1, v.data() + static_cast<std::size_t>(t - from) * kRow, kRow);
+        }
+        void* dk = device_copy(k);
+        void* dv = device_copy(v);
+        if (dk == nullptr || dv == nullptr) return false;
+        KVAppendBatch batch;
+        const bool ok = batch.append(h.cache, h.allocator, seqs, pos, 0, 1, dk, dv);
+        if (!ok) std::fprintf(stderr, "append: %s\n", batch.last_error().c_str());
+        return ok;
+    }
+
+    struct Decoded {
+        std::vector<SequenceId> seqs;
+        std::vector<std::uint32_t> lens;
+        void* out;
+    };
+
+    bool decode(const std::vector<SequenceId>& seqs, const std::vector<std::uint32_t>& lens) {
+        std::vector<CacheView> views;
+        for (SequenceId s : seqs) views.push_back(*h.cache.cache_view(s));
+        if (query == nullptr) {
+            std::vector<std::uint16_t> q(8 * kQRow);
+            for (std::uint32_t r = 0; r < 8; ++r) kv_pattern::query_row(r, q.data() + r * kQRow, kQRow);
+            query_host = q;
+            query = device_copy(q);
+            if (query == nullptr) return false;
+        }
+        void* out = nullptr;
+        if (qvp_malloc(&out, seqs.size() * kQRow * 4) != QVP_OK) return false;
+        buffers.push_back(out);
+        batches.emplace_back();
+        PagedAttentionBatch& b = batches.back();
+        if (!b.decode(views, lens, 0, kHq, 1.0f / std::sqrt(128.0f), query, out, ElementType::F32)) {
+            std::fprintf(stderr, "decode: %s\n", b.last_error().c_str());
+            return false;
+        }
+        decoded.push_back({seqs, lens, out});
+        return true;
+    }
+
+    DeviceHarness& h;
+    std::deque<std::vector<std::uint16_t>> staged;  // host rows, alive until the copies ran
+    std::deque<PagedAttentionBatch> batches;         // packed arrays read by enqueued decodes
+    std::vector<void*> buffers;
+    std::vector<std::uint16_t> query_host;
+    void* query{nullptr};
+    std::vector<Decoded> decoded;
+};
+
+}  // namespace
+
+TEST(DeviceAllocatorTest, SwapsBesideDecodesAndAppendsKeepEveryByte) {
+    // Engine work enqueued while swap batches still run on the side stream,
+    // with no host read or write of a frame (which would flush and wait) in
+    // between: a sequence swapped out has its frames taken at once by a new
+    // sequence whose append overwrites them (the append must wait for the
+    // gathers), a sequence swapped back in lands in frames a decode enqueued
+    // just before still reads (the scatters must wait for it), and a token
+    // appended right after a swap-in writes a frame its scatter fills. Every
+    // decode must equal float64 attention over the pattern's rows, and every
+    // frame of the surviving sequences must hold exactly those rows.
+    DeviceHarness h(shape_of(16, 1, 4, 128, 2), 256, 256);
+    ASSERT_TRUE(h.ready());
+    EngineSteps e(h);
+    const std::uint32_t lenA = 1500, lenB = 1200, lenC = 1500, lenD = 1000;
+    for (auto [id, n] : {std::pair<SequenceId, std::uint32_t>{1, lenA}, {2, lenB}}) {
+        ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{id, id, {}, {}}));
+        ASSERT_TRUE(h.cache.reserve_tokens(id, n));
+        ASSERT_TRUE(e.append(id, 0, n));
+    }
+    ASSERT_TRUE(e.decode({1, 2}, {lenA, lenB}));
+    const std::vector<PhysicalBlockId> a_frames = [&] {
+        std::vector<PhysicalBlockId> f;
+        for (const BlockTableEntry& x : h.cache.cache_view(1)->block_table->entries()) f.push_back(x.physical_id);
+        return f;
+    }();
+    // A out; C takes A's frames and overwrites them.
+    ASSERT_EQ(h.cache.swap_out_sequence(1), 94u);
+    ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{3, 3, {}, {}}));
+    ASSERT_TRUE(h.cache.reserve_tokens(3, lenC));
+    std::size_t reused = 0;
+    for (const BlockTableEntry& x : h.cache.cache_view(3)->block_table->entries()) {
+        reused += std::count(a_frames.begin(), a_frames.end(), x.physical_id);
+    }
+    EXPECT_EQ(reused, a_frames.size());  // LIFO free list: C holds every frame A left
+    ASSERT_TRUE(e.append(3, 0, lenC));
+    ASSERT_TRUE(e.decode({2, 3}, {lenB, lenC}));
+    // B released while that decode may still read it; A comes back into B's frames.
+    h.cache.release_sequence(2);
+    ASSERT_TRUE(h.cache.swap_in_sequence(1));
+    ASSERT_TRUE(h.cache.reserve_tokens(1, 1));
+    ASSERT_TRUE(e.append(1, lenA, lenA + 1));
+    ASSERT_TRUE(e.decode({1, 3}, {lenA + 1, lenC}));
+    // C out, D over its frames, then C back in place of D.
+    ASSERT_EQ(h.cache.swap_out_sequence(3), 94u);
+    ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{4, 4, {}, {}}));
+    ASSERT_TRUE(h.cache.reserve_tokens(4, lenD));
+    ASSERT_TRUE(e.append(4, 0, lenD));
+    ASSERT_TRUE(e.decode({1, 4}, {lenA + 1, lenD}));
+    h.cache.release_sequence(4);
+    ASSERT_TRUE(h.cache.swap_in_sequence(3));
+    ASSERT_TRUE(e.decode({3, 1}, {lenC, lenA + 1}));
+    EXPECT_GT(h.allocator.swap_launches(), 0u);
+    ASSERT_TRUE(h.allocator.synchronize());
+
+    for (std::size_t k = 0; k < e.decoded.size(); ++k) {
+        const EngineSteps::Decoded& dec = e.decoded[k];
+        std::vector<float> got(dec.seqs.size() * EngineSteps::kQRow);
+        ASSERT_EQ(qvp_memcpy_dtoh(got.data(), dec.out, got.size() * 4, h.allocator.stream()), QVP_OK);
+        ASSERT_EQ(qvp_stream_synchronize(h.allocator.stream()), QVP_OK);
+        for (std::size_t b = 0; b < dec.seqs.size(); ++b) {
+            const SequenceId s = dec.seqs[b];
+            // Cache every row of the sequence once, as float.
+            std::vector<float> K(static_cast<std::size_t>(dec.lens[b]) * EngineSteps::kRow), V(K.size());
+            std::vector<std::uint16_t> row(EngineSteps::kRow);
+            for (std::uint32_t t = 0; t < dec.lens[b]; ++t) {
+                kv_pattern::kv_row(s, t, 0, row.data(), row.size());
+                for (std::uint32_t i = 0; i < EngineSteps::kRow; ++i) K[t * EngineSteps::kRow + i] = bf16_value(row[i]);
+                kv_pattern::kv_row(s, t, 1, row.data(), row.size());
+                for (std::uint32_t i = 0; i < EngineSteps::kRow; ++i) V[t * EngineSteps::kRow + i] = bf16_value(row[i]);
+            }
+            std::vector<float> q(EngineSteps::kQRow);
+            for (std::uint32_t i = 0; i < EngineSteps::kQRow; ++i) q[i] = bf16_value(e.query_host[b * EngineSteps::kQRow + i]);
+            const auto expect = textbook_attention(
+                q, EngineSteps::kHq, EngineSteps::kHkv, EngineSteps::kD, dec.lens[b], 1.0f / std::sqrt(128.0f),
+                [&](auto t, auto kh, auto d) { return double(K[t * EngineSteps::kRow + kh * EngineSteps::kD + d]); },
+                [&](auto t, auto kh, auto d) { return double(V[t * EngineSteps::kRow + kh * EngineSteps::kD + d]); });
+            for (std::size_t i = 0; i < expect.size(); ++i) {
+                const double tol = 2e-3 + std::fabs(expect[i]) / 256.0;
+                ASSERT_NEAR(got[b * EngineSteps::kQRow + i], expect[i], tol)
+                    << "decode " << k << " sequence " << s << " element " << i;
+            }
+        }
+    }
+    // Frames of A (swapped out, in, one token appended) and C (swapped out and in).
+    for (auto [s, n] : {std::pair<SequenceId, std::uint32_t>{1, lenA + 1}, {3, lenC}}) {
+        const auto view = h.cache.cache_view(s);
+        ASSERT_TRUE(view.has_value());
+        std::vector<std::uint16_t> expect(EngineSteps::kRow), frame(h.allocator.block_stride() / 2);
+        for (std::uint32_t j = 0; j < (n + 15) / 16; ++j) {
+            const auto f = view->block_table->lookup(j);
+            ASSERT_TRUE(f.has_value());
+            ASSERT_TRUE(h.allocator.read_block_bytes(*f, 0, frame.data(), frame.size() * 2));
+            for (std::uint32_t t = 0; t < 16 && j * 16 + t < n; ++t) {
+                for (std::uint32_t st = 0; st < 2; ++st) {
+                    kv_pattern::kv_row(s, j * 16 + t, st, expect.data(), expect.size());
+                    const std::uint16_t* at = frame.data() + st * 16 * EngineSteps::kRow + t * EngineSteps::kRow;
+                    ASSERT_EQ(std::memcmp(at, expect.data(), expect.size() * 2), 0)
+                        << "sequence " << s << " position " << j * 16 + t << " stream " << st;
+                }
+            }
+        }
+    }
 }

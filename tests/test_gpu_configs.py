@@ -19,6 +19,7 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+import kv_pattern as KP
 import qvp
 import workloads as W
 from helpers import assert_close_16bit, assert_close_bf16, oracle_decode, to_f32
@@ -32,7 +33,7 @@ def run(name: str, *args: str) -> dict:
     exe = BENCH / name
     assert exe.exists(), f"{exe} is missing: run __graft_entry__.build() first"
     print(f"running {name} {' '.join(args)}", flush=True)
-    proc = subprocess.run([str(exe), *args], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=100)
+    proc = subprocess.run([str(exe), *args], stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True, timeout=110)
     print(proc.stdout, proc.stderr)
     assert proc.returncode == 0, proc.stderr + proc.stdout
     return json.loads(proc.stdout.strip().splitlines()[-1])
@@ -79,6 +80,68 @@ def test_continuous_batching_trace_full_size_matches_the_reference(tmp_path, eng
     assert r["swapped_out_blocks"] > 0 and r["swapped_in_blocks"] > 0
     got, expected = log.read_text(), _reference_config5_log()
     assert got == expected, _first_difference(got, expected)
+
+
+# One record of trace_bench's --verify-dump: step, sequence, batch row,
+# context length, then the sequence's decode output (28 heads x 128, bf16).
+_DUMP_RECORD = np.dtype([("step", "<u4"), ("seq", "<u4"), ("row", "<u4"), ("len", "<u4"), ("out", "<u2", (28 * 128,))])
+
+
+def _oracle_check_dump(path: Path) -> int:
+    """Rebuilds each dumped sequence's K/V from the seeded pattern (one frame
+    per logical block, layer 0, K rows then V rows) and its query from the
+    batch row, decodes them with the oracle and compares with the dumped bf16
+    outputs. Returns the number of records checked."""
+    recs = np.fromfile(path, dtype=_DUMP_RECORD)
+    assert len(recs) > 0, "empty verify dump"
+    tpb, hkv, hq, d = 16, 4, 28, 128
+    for chunk in np.array_split(recs, -(-len(recs) // 12)):
+        lens = chunk["len"].astype(np.int64)
+        nb = (lens + tpb - 1) // tpb
+        cu = np.zeros(len(chunk) + 1, np.uint32)
+        cu[1:] = np.cumsum(nb)
+        total = int(cu[-1])
+        frames = np.zeros((total, 2, tpb, hkv * d), np.uint16)
+        for r, rec in enumerate(chunk):
+            pos = np.arange(int(rec["len"]), dtype=np.int64)
+            f = int(cu[r]) + pos // tpb
+            for st in (0, 1):
+                frames[f, st, pos % tpb] = KP.kv_rows(int(rec["seq"]), pos, st, hkv * d)
+        w = W.Workload("config5_checks", tpb, 1, hq, hkv, d, qvp.DTYPE_BF16, 1.0 / np.sqrt(d),
+                       chunk["len"].astype(np.uint32), np.arange(total, dtype=np.uint32), cu, total, seed=0)
+        query = KP.query_rows(chunk["row"], hq * d).reshape(len(chunk), hq, d)
+        _, ref32 = oracle_decode(w, frames.reshape(-1).view(np.uint8), query)
+        got = chunk["out"].reshape(len(chunk), hq, d)
+        assert_close_16bit(got, ref32, qvp.DTYPE_BF16,
+                           f"config5 decode at steps {chunk['step'].min()}..{chunk['step'].max()}")
+    return len(recs)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("engine,in_flight", [("0", "2"), ("1", "2"), ("0", "1")],
+                         ids=["decode-only", "full-engine-step", "one-step-at-a-time"])
+def test_continuous_batching_trace_full_size_bytes(tmp_path, engine, in_flight):
+    """config5 at full size with the bytes checked, not only the decisions
+    (reference tests/EndToEnd.test.cpp:311-351: a preempted request resumes
+    with an intact cache; swap semantics src/MemoryAllocator.cpp:105-152).
+    Every K/V row is a seeded function of (sequence, position), written by
+    the append kernel; swap gathers and scatters run on the side stream beside
+    the engine's appends and decodes with two steps in flight. After every
+    resume, and for four sequences every 40 steps, the driver copies the
+    sequence's frames behind its decode and compares every row below its
+    length with the pattern (no mismatch allowed), and the decode outputs it
+    dumps equal the oracle's decode of the same rows at the bf16 bar. The
+    decisions still equal the reference's log."""
+    log, dump = tmp_path / "trace.log", tmp_path / "checks.bin"
+    r = run("trace_bench", "--requests", "200", "--seed", "5", "--engine", engine, "--in-flight", in_flight,
+            "--verify", "1", "--check-every", "40", "--verify-dump", str(dump), "--log", str(log))
+    assert r["verify"] and r["finished"] == 200 and r["drained"]
+    assert r["row_mismatches"] == 0, r["first_mismatch"]
+    assert r["resumes"] > 0 and r["resume_checks"] == r["resumes"] and r["unchecked_resumes"] == 0
+    assert r["sequence_checks"] > r["resume_checks"] and r["rows_checked"] > 500_000
+    got, expected = log.read_text(), _reference_config5_log()
+    assert got == expected, _first_difference(got, expected)
+    assert _oracle_check_dump(dump) == r["decode_records"] == r["sequence_checks"]
 
 
 @pytest.mark.gpu

@@ -225,3 +225,40 @@ def test_pack_ahead_without_a_carrier():
     c.destroy()
     qvp.paged_decode(a, s)  # no pending upload of a destroyed batch is carried
     s.synchronize()
+
+
+@pytest.mark.parametrize("enqueue", ["upload", "decode"])
+def test_pack_ahead_upload_on_another_stream_waits_for_the_slots_last_decode(enqueue):
+    """Steps 0 and 1 are packed and decoded on stream P, step 0's decode
+    queued behind a dozen decodes of another batch; step 2 is packed ahead on
+    P into step 0's buffer and its upload enqueued on stream D (by
+    qvp_batch_upload, or by the batch's own decode on D). The upload has to
+    wait for step 0's decode on P: every step's output equals a plain
+    pack-then-decode of its lengths, bit for bit."""
+    w = W.config2(seed=47, num_seqs=64)
+    run = GpuRun(w)
+    P, D = qvp.Stream(), qvp.Stream()
+    lens = [np.maximum(w.context_lens.astype(np.int64) - d, 1).astype(np.uint32) for d in (0, 150, 400)]
+    b = qvp.Batch()
+    outs = [qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4) for _ in range(3)]
+    args = [_args(run, w, run.q, outs[i], b) for i in range(3)]
+    busy_out = qvp.DeviceBuffer(w.num_seqs * w.num_query_heads * w.head_dim * 4)
+    busy = _args(run, w, run.q, busy_out, run.batch)
+    run.batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks, stream=P, decode=busy)
+    print(f"case: pack-ahead upload on a second stream via {enqueue}", flush=True)
+    b.pack(w.ids, w.cu_blocks, lens[0], 16, w.num_pool_blocks, stream=P, decode=args[0])
+    for _ in range(12):
+        qvp.paged_decode(busy, P)
+    qvp.paged_decode(args[0], P)
+    b.pack(w.ids, w.cu_blocks, lens[1], 16, w.num_pool_blocks, stream=P, decode=args[1])
+    qvp.paged_decode(args[1], P)
+    b.pack(w.ids, w.cu_blocks, lens[2], 16, w.num_pool_blocks, stream=P, decode=args[2], ahead=True)
+    if enqueue == "upload":
+        b.upload(D)
+    qvp.paged_decode(args[2], D)
+    D.synchronize()
+    P.synchronize()
+    for i in range(3):
+        got = outs[i].download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim))
+        ref = _plain_decode(run, w, lens[i])
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"step {i} differs from a plain pack"

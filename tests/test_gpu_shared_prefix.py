@@ -14,7 +14,7 @@ import pytest
 
 import qvp
 import workloads as W
-from helpers import GpuRun, assert_close_16bit, assert_close_bf16, oracle_decode
+from helpers import GpuRun, assert_close_16bit, assert_close_bf16, oracle_decode, tiled_pool_image
 
 pytestmark = pytest.mark.gpu
 
@@ -172,3 +172,28 @@ def test_half_precision_output_from_the_prefix_launch():
     got = run.decode(out_dtype=qvp.DTYPE_F16)
     assert run.batch.decode_plan()["workgroups"] == 0  # every tail was short: one launch
     assert_close_16bit(got, ref32, qvp.DTYPE_F16, "f16 out")
+
+
+@pytest.mark.parametrize("prompts,grouped", [(40, True), (900, False)], ids=["few-forks", "many-tiny-forks"])
+def test_many_tiny_forks_are_planned_without_shared_prefixes(prompts, grouped):
+    # Prompts of 4 shared tiles forked 8 ways, each branch 5 private tiles
+    # past them (too long for the prefix launch), 3 kv heads (one per
+    # segment: 85 ranges per head). With 40 prompts the prefix groups are
+    # used; with 900 (7,200 branches) every range would hold ~85 partial
+    # private tails, more than the 64 merges a workgroup tracks in LDS, so the
+    # planner drops the shared prefixes and the plain per-sequence schedule
+    # decodes the batch.
+    branches = [8] * prompts
+    extra = _extra(9, branches, lo=129, hi=161)
+    w = W.forked([128] * prompts, branches, extra, 3, 3)
+    run = GpuRun(w, image=tiled_pool_image(w))
+    print(f"case: {prompts} prompts x 8 branches, grouped={grouped}", flush=True)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    plan = run.batch.decode_plan()
+    assert plan["kernel"] == "mfma"
+    if grouped:
+        assert plan["shared_prefix_groups"] == prompts, plan
+    else:
+        assert plan["shared_prefix_groups"] == 0, plan
+    assert_close_bf16(got, ref32, f"{prompts} prompts")
