@@ -43,6 +43,8 @@ __device__ inline const __attribute__((address_space(4))) T* as_const(const T* p
     return (const __attribute__((address_space(4))) T*)(ptr);
 }
 
+// Plain loads: with the non-temporal hint (which speeds up the bf16 decode)
+// this kernel ran the config2-shaped fp32 batch in 219 us instead of 136 us.
 __device__ inline floatx4 load4f(const uint8_t* ptr) { return *reinterpret_cast<const floatx4*>(ptr); }
 
 __global__ __launch_bounds__(kF32Threads, 2) void decode_f32_grouped(DecodeGeometry p, F32SplitArgs sa) {

@@ -199,20 +199,22 @@ __device__ inline void load_tile(const DecodeGeometry& p, const TileRef& r, int 
         const int ktok = tok0 + 16 * u + (c >> 2) + 4 * (c & 3);
         const uint8_t* kp = frame + p.k_off + static_cast<uint64_t>(ktok & tmask) * p.token_stride + 16u * j;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tile.k[u][i] = load16(kp + 64 * i);
+        for (int i = 0; i < 4; ++i) tile.k[u][i] = load16_stream(kp + 64 * i);
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
             const int q = 4 * u + qq;
             const int vtok = tok0 + 4 * q + j;
             const uint8_t* vp = frame + p.v_off + static_cast<uint64_t>(vtok & tmask) * p.token_stride + 16u * c;
-            tile.v[q] = load16(vp);
+            tile.v[q] = load16_stream(vp);
         }
     }
 }
 
 // kVG = 0: matrix-core tiles; 1, 2: vector tiles for query groups up to kVG.
-template <typename OutT, int kVG>
+// kF16: the cache holds IEEE binary16 elements (matrix-core tiles only).
+template <typename OutT, int kVG, bool kF16>
 __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(DecodeGeometry p, MfmaArgs a) {
+    static_assert(!kF16 || kVG == 0, "vector tiles read bf16 caches");
     __shared__ VectorTileLds<kVG> vt;
     __shared__ float sm_m[kWaves][16];
     __shared__ float sm_l[kWaves][16];
@@ -350,7 +352,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
                 if (has2) load_tile(p, r2, c, j, nxt);
                 has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
                 if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
-                compute_tile(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
+                compute_tile<kF16>(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
             }
 
             // This wave's state for (piece, head g) goes to LDS in row layout.
@@ -946,21 +948,23 @@ const void* prefix_kernel(uint32_t out_dtype) {
     }
 }
 
-// The kernel instantiation for an output type and a tile engine.
+// The kernel instantiation for an output type, a tile engine and the cache's
+// element type (fp16 caches run matrix-core tiles only).
 template <typename OutT>
-const void* kernel_for_group(uint32_t tile_group) {
+const void* kernel_for_group(uint32_t tile_group, bool f16) {
+    if (f16) return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0, true>);
     switch (tile_group) {
-        case 0: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0>);
-        case 1: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 1>);
-        default: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 2>);
+        case 0: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0, false>);
+        case 1: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 1, false>);
+        default: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 2, false>);
     }
 }
 
-const void* decode_kernel(uint32_t out_dtype, uint32_t tile_group) {
+const void* decode_kernel(uint32_t out_dtype, uint32_t tile_group, bool f16) {
     switch (out_dtype) {
-        case QVP_DTYPE_F32: return kernel_for_group<float>(tile_group);
-        case QVP_DTYPE_BF16: return kernel_for_group<uint16_t>(tile_group);
-        default: return kernel_for_group<_Float16>(tile_group);
+        case QVP_DTYPE_F32: return kernel_for_group<float>(tile_group, f16);
+        case QVP_DTYPE_BF16: return kernel_for_group<uint16_t>(tile_group, f16);
+        default: return kernel_for_group<_Float16>(tile_group, f16);
     }
 }
 
@@ -988,8 +992,11 @@ int device_max_wgs(uint32_t* wgs) {
         for (uint32_t dt : {QVP_DTYPE_F32, QVP_DTYPE_BF16, QVP_DTYPE_F16}) {
             for (uint32_t tg : kTileGroups) {
                 const int dyn = static_cast<int>(kMaxLdsBytes - static_lds_bytes(tg));
-                QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, tg), hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
+                QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, tg, false), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            dyn));
             }
+            QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, 0, true), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        static_cast<int>(kMaxLdsBytes - static_lds_bytes(0))));
         }
         for (uint32_t dt : {QVP_DTYPE_F32, QVP_DTYPE_BF16, QVP_DTYPE_F16}) {
             QVP_HIP(hipFuncSetAttribute(prefix_kernel(dt), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1153,7 +1160,9 @@ struct PrefixGroup {
 
 std::vector<PrefixGroup> find_prefix_groups(const ScheduleInput& in, const DecodeGeometry& g, uint32_t hps) {
     std::vector<PrefixGroup> out;
-    if (hps != 1 || in.partition_tiles != 0 || g.tile_group != 0 || g.group == 0 || g.group > 16 || in.tpb == 0) {
+    // The shared-prefix launch reads bf16 caches with matrix-core tiles.
+    if (hps != 1 || in.partition_tiles != 0 || g.tile_group != 0 || g.kv_f16 != 0 || g.group == 0 || g.group > 16 ||
+        in.tpb == 0) {
         return out;
     }
     const int cap = std::min<int>(kPrefixMaxMembers, 4 * static_cast<int>(16 / g.group));
@@ -1224,14 +1233,15 @@ bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_
     const bool aligned = (g.block_stride % 16 == 0) && (g.k_off % 16 == 0) && (g.v_off % 16 == 0) &&
                          (g.token_stride % 16 == 0) && (g.head_stride % 16 == 0) && (kv_base_addr % 16 == 0) &&
                          (query_addr % 16 == 0);
-    return kv_dtype == QVP_DTYPE_BF16 && g.head_dim == kD && g.group >= 1 && g.group <= 16 && pow2 && g.tpb >= 16 &&
-           aligned && g.scale_log2 > 0.0f;
+    return (kv_dtype == QVP_DTYPE_BF16 || kv_dtype == QVP_DTYPE_F16) && g.head_dim == kD && g.group >= 1 &&
+           g.group <= 16 && pow2 && g.tpb >= 16 && aligned && g.scale_log2 > 0.0f;
 }
 
 bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g) {
     const qvp_schedule& s = batch->sched;
     if (!s.valid || s.pack_generation != batch->generation || s.num_kv_heads != g.num_kv_heads ||
-        s.group != g.group || s.tile_group != g.tile_group || s.partition_tiles != batch->partition_tiles) {
+        s.group != g.group || s.tile_group != g.tile_group || s.kv_f16 != g.kv_f16 ||
+        s.partition_tiles != batch->partition_tiles) {
         return false;
     }
     uint32_t max_wgs = 0;
@@ -1521,6 +1531,7 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     s.num_kv_heads = num_kv_heads;
     s.group = g.group;
     s.tile_group = g.tile_group;
+    s.kv_f16 = g.kv_f16;
     s.partition_tiles = in.partition_tiles;
     s.max_wgs = max_wgs;
     s.weights = weights;
@@ -1705,6 +1716,7 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     }
     DecodeGeometry gk = g;
     if (s.num_prefix_items > 0) {
+        if (g.kv_f16 != 0) return fail(QVP_ERR_INVALID_ARGUMENT, "shared-prefix schedule for an fp16 cache");
         PrefixArgs pa{};
         pa.items = reinterpret_cast<const qvp_prefix_item*>(s.words + s.off_prefix);
         pa.suffix = reinterpret_cast<const qvp_piece*>(s.words + s.off_suffix);
@@ -1722,8 +1734,8 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     // upload, if any, needs this one).
     if (s.num_wgs + copy_wgs > 0) {
         void* kargs[] = {&gk, &a};
-        QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group), dim3(s.num_wgs + copy_wgs), dim3(kThreads),
-                                kargs, s.lds_bytes, stream));
+        QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group, g.kv_f16 != 0), dim3(s.num_wgs + copy_wgs),
+                                dim3(kThreads), kargs, s.lds_bytes, stream));
     }
     // The merge runs inside the kernel; the event still marks the split/merge
     // boundary for callers that time the two phases.

@@ -16,7 +16,10 @@
 // sampled heads of four sequences match float64 attention within the bf16
 // tolerance. Times (medians of HIP event pairs) the whole step through
 // PagedAttentionBatch::decode -- block-table walk, pack and schedule upload,
-// decode -- and the decode kernel alone, and reports the schedule.
+// decode -- one step at a time (the stream idle while the host works), the
+// same steps enqueued back to back as an engine loop runs them (decode() per
+// step, and pack_ahead() pairs whose uploads ride in the previous decode;
+// pipelined_steps.h), and the decode kernel alone, and reports the schedule.
 //
 // Output: one JSON line. Usage: config3_bench [--seqs N] [--lo T] [--hi T] [--reps N] [--split T]
 // (--split: split-K partition in tokens, 512 by default; 0 lets the decode cut
@@ -26,6 +29,8 @@
 #include "qwenvl_paged/MRope.h"
 #include "qwenvl_paged/MemoryAllocator.h"
 #include "qwenvl_paged/PagedAttention.h"
+
+#include "pipelined_steps.h"
 
 #include <algorithm>
 #include <cmath>
@@ -274,6 +279,12 @@ int main(int argc, char** argv) {
     }
     std::sort(times.begin(), times.end());
     const float step_ms = times.empty() ? 0.f : times[times.size() / 2];
+    PagedAttentionBatch ahead_a, ahead_b;
+    ahead_a.set_split_tokens(split);
+    ahead_b.set_split_tokens(split);
+    const pipelined_steps::Forms piped = pipelined_steps::run_forms(
+        attn, ahead_a, ahead_b, tagged, ctx, 0, kHq, scale, dq, dout, ElementType::BF16, stream,
+        static_cast<int>(std::max<std::uint32_t>(reps, 10)));
     // The decode kernel alone: the packed batch of the last step decoded
     // again (its schedule is cached), as the engine does for every layer of
     // a step after the first.
@@ -367,13 +378,19 @@ int main(int argc, char** argv) {
         "{\"mode\": \"config3_multimodal\", \"sequences\": %u, \"cached_tokens\": %llu, \"image_tokens\": %llu, "
         "\"metadata_roundtrip\": %s, \"position_rows\": %llu, \"positions_match_closed_form\": %s, "
         "\"tagged_equals_untagged_bitwise\": %s, \"step_us_median\": %.3f, \"step_tokens_per_s\": %.1f, "
+        "\"pipelined_step_us\": %.3f, \"pack_ahead_step_us\": %.3f, \"host_us_per_step\": %.3f, "
+        "\"pack_ahead_host_us_per_step\": %.3f, \"pipelined_over_kernel\": %.4f, \"pack_ahead_over_kernel\": %.4f, "
+        "\"pack_ahead_tokens_per_s\": %.1f, "
         "\"decode_us_median\": %.3f, \"decode_GBps\": %.1f, "
         "\"decode_frac_of_8TBps\": %.4f, \"decode_tokens_per_s\": %.1f, \"plan\": {\"kernel\": %u, \"workgroups\": %u, "
         "\"pieces\": %u, \"slots\": %u, \"kv_heads_per_segment\": %u, \"split_tokens\": %u, \"query_group\": %u}, \"checked_elements\": %zu, "
         "\"worst_excess_over_tolerance\": %.3g, \"decode_within_tolerance\": %s}\n",
         seqs, static_cast<unsigned long long>(tokens), static_cast<unsigned long long>(image_tokens),
         metadata_roundtrip ? "true" : "false", static_cast<unsigned long long>(rows), positions_ok ? "true" : "false",
-        tagged_equals_plain ? "true" : "false", step_ms * 1e3, seqs / (step_ms * 1e-3), decode_ms * 1e3, (kv_bytes + qo) / (decode_ms * 1e-3) / 1e9,
+        tagged_equals_plain ? "true" : "false", step_ms * 1e3, seqs / (step_ms * 1e-3), piped.loop.gpu_us_per_step,
+        piped.ahead.gpu_us_per_step, piped.loop.host_us_per_step, piped.ahead.host_us_per_step,
+        piped.loop.gpu_us_per_step / (decode_ms * 1e3), piped.ahead.gpu_us_per_step / (decode_ms * 1e3),
+        seqs / (piped.ahead.gpu_us_per_step * 1e-6), decode_ms * 1e3, (kv_bytes + qo) / (decode_ms * 1e-3) / 1e9,
         (kv_bytes + qo) / (decode_ms * 1e-3) / 8e12, seqs / (decode_ms * 1e-3), plan.kernel, plan.workgroups,
         plan.pieces, plan.slots, plan.kv_heads_per_segment, plan.split_tokens, plan.query_group, checked, worst,
         worst <= 0.0 ? "true" : "false");

@@ -13,8 +13,11 @@
 //
 // Timing (medians of HIP event pairs): step_us_median is a whole
 // PagedAttentionBatch::decode call (block-table walk, pack and schedule upload,
-// decode); decode_us_median the decode kernel alone, relaunched on the packed
-// batch.
+// decode) one step at a time, the stream idle while the host works;
+// pipelined_step_us / pack_ahead_step_us the same steps enqueued back to back
+// as an engine loop runs them (decode() per step, and pack_ahead() pairs whose
+// uploads ride in the previous decode; pipelined_steps.h); decode_us_median
+// the decode kernel alone, relaunched on the packed batch.
 //
 // --layers N stores all N layers of the model in each frame (N = 28: whole
 // Qwen2-VL-7B frames of 917,504 B, so each copy-on-write copy moves 28x the
@@ -25,6 +28,8 @@
 #include "qwenvl_paged/KVCacheManager.h"
 #include "qwenvl_paged/MemoryAllocator.h"
 #include "qwenvl_paged/PagedAttention.h"
+
+#include "pipelined_steps.h"
 
 #include <algorithm>
 #include <chrono>
@@ -232,6 +237,10 @@ int main(int argc, char** argv) {
     }
     std::sort(times.begin(), times.end());
     const float step_ms = times[times.size() / 2];
+    PagedAttentionBatch ahead_a, ahead_b;
+    const pipelined_steps::Forms piped =
+        pipelined_steps::run_forms(attn, ahead_a, ahead_b, views, lens, 0, kHq, scale, dq, dout, ElementType::BF16,
+                                   stream, static_cast<int>(std::max<std::uint32_t>(reps, 20)));
     // The decode kernel alone: the last step's packed batch decoded again (its
     // work schedule is cached), as an engine decodes the other layers of a
     // step.
@@ -322,12 +331,17 @@ int main(int argc, char** argv) {
         "{\"mode\": \"config4_cow\", \"layers\": %u, \"prompts\": %u, \"branches_per_prompt\": %u, \"cow_pairs\": %zu, "
         "\"pending_before_flush\": %zu, \"copy_launches\": %llu, \"copy_us_median\": %.3f, \"copy_read_plus_write_GBps\": "
         "%.1f, \"frames_equal_host_allocator\": %s, \"copies_equal_source\": %s, \"decode_branches\": %u, "
-        "\"decode_ctx\": %u, \"step_us_median\": %.3f, \"decode_us_median\": %.3f, \"decode_logical_GBps\": %.1f, \"decode_unique_GBps\": "
+        "\"decode_ctx\": %u, \"step_us_median\": %.3f, \"pipelined_step_us\": %.3f, \"pack_ahead_step_us\": %.3f, "
+        "\"host_us_per_step\": %.3f, \"pack_ahead_host_us_per_step\": %.3f, \"pipelined_over_kernel\": %.4f, "
+        "\"pack_ahead_over_kernel\": %.4f, \"decode_us_median\": %.3f, \"decode_logical_GBps\": %.1f, \"decode_unique_GBps\": "
         "%.1f, \"decode_tokens_per_s\": %.1f, \"checked_elements\": %zu, \"worst_excess_over_tolerance\": %.3g, "
         "\"decode_within_tolerance\": %s}\n",
         layers, prompts, branches, copies.size(), pending, static_cast<unsigned long long>(copy_launches), copy_ms * 1e3,
         copy_bytes / (copy_ms * 1e-3) / 1e9, frames_equal ? "true" : "false", copies_equal ? "true" : "false", nb,
-        ctx, step_ms * 1e3, decode_ms * 1e3, (logical + qo) / (decode_ms * 1e-3) / 1e9, (unique + qo) / (decode_ms * 1e-3) / 1e9,
+        ctx, step_ms * 1e3, piped.loop.gpu_us_per_step, piped.ahead.gpu_us_per_step, piped.loop.host_us_per_step,
+        piped.ahead.host_us_per_step, piped.loop.gpu_us_per_step / (decode_ms * 1e3),
+        piped.ahead.gpu_us_per_step / (decode_ms * 1e3), decode_ms * 1e3, (logical + qo) / (decode_ms * 1e-3) / 1e9,
+        (unique + qo) / (decode_ms * 1e-3) / 1e9,
         nb / (decode_ms * 1e-3), checked, worst, worst <= 0.0 ? "true" : "false");
     (void)qvp_free(dq);
     (void)qvp_free(dout);

@@ -10,6 +10,7 @@ Outputs (git-ignored, shipped with the tree):
   build/bench/cow_bench             copy-on-write configuration driver (GPU)
   build/bench/trace_bench           continuous-batching trace driver (GPU)
   build/bench/config3_bench         long-context multimodal decode driver (GPU)
+  build/bench/engine_bench          config2 decode through PagedAttentionBatch over CacheViews (GPU)
 
 libqvp.so must be built first (qwenvl-paged_amd/build.py does both).
 """
@@ -65,7 +66,8 @@ TEST_BINARIES = {
 
 
 # Benchmark drivers of the copy-on-write and continuous-batching configurations.
-BENCH_BINARIES = {"cow_bench": "cow_bench.cpp", "trace_bench": "trace_bench.cpp", "config3_bench": "config3_bench.cpp"}
+BENCH_BINARIES = {"cow_bench": "cow_bench.cpp", "trace_bench": "trace_bench.cpp", "config3_bench": "config3_bench.cpp",
+                  "engine_bench": "engine_bench.cpp"}
 
 
 def _run(cmd: list[str]) -> None:

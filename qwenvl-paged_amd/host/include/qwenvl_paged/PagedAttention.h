@@ -18,6 +18,7 @@
 #include "qwenvl_paged/KVCacheManager.h"
 
 #include <cstdint>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -83,6 +84,26 @@ public:
     bool decode(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
                 std::uint32_t layer, std::uint32_t num_query_heads, float scale, const void* device_query,
                 void* device_out, ElementType out_type);
+    // Pipelined steps (two objects used in turn): pack_ahead() does all of
+    // decode()'s host work for the next step -- checks, the page-table walk,
+    // the pack and the decode's work schedule -- but leaves the step's upload
+    // waiting in pinned staging, to be carried by the next decode that
+    // another PagedAttentionBatch (or qvp_paged_decode on another batch)
+    // enqueues on the allocator's stream, in the tail of that launch;
+    // decode_packed() then enqueues this object's decode (and the upload
+    // itself if no launch carried it). The engine loop:
+    //     b.pack_ahead(step n + 1); a.decode_packed();  // step n carries n + 1's upload
+    //     a.pack_ahead(step n + 2); b.decode_packed();  // ...
+    // The views are read at pack_ahead(); the cache must not move or rewrite
+    // the frames they name before decode_packed() has been enqueued, and a
+    // frame the previous step's decode reads must not be released or swapped
+    // out by the next step's bookkeeping before that decode is enqueued.
+    // Refused calls return false with nothing enqueued (decode_packed()
+    // refuses when nothing is packed).
+    bool pack_ahead(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                    std::uint32_t layer, std::uint32_t num_query_heads, float scale, const void* device_query,
+                    void* device_out, ElementType out_type);
+    bool decode_packed();
     // Causal prefill: for every sequence b the new positions p in
     // [first_new[b], context_lens[b]) each attend to tokens [0, p] -- the
     // reference's decode applied per position with context_len = p + 1
@@ -115,6 +136,11 @@ private:
     // when given (qvp_pack_for_decode).
     bool upload(const std::vector<std::uint32_t>& context_lens, std::uint32_t tokens_per_block,
                 const qvp_decode_args* decode, void* stream);
+    // Checks, walk and the decode's arguments (into args_) shared by decode()
+    // and pack_ahead().
+    bool prepare(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                 std::uint32_t layer, std::uint32_t num_query_heads, float scale, const void* device_query,
+                 void* device_out, ElementType out_type, void*& stream);
 
     qvp_batch* batch_{nullptr};
     std::uint32_t num_pool_blocks_{0};
@@ -123,6 +149,11 @@ private:
     std::string last_error_;
     std::uint32_t split_tokens_{0};
     int cache_type_override_{-1};
+    // The decode's arguments of the last decode() / pack_ahead(), and the
+    // stream of the last pack_ahead().
+    std::unique_ptr<qvp_decode_args> args_;
+    void* packed_stream_{nullptr};
+    bool packed_ready_{false};
 };
 
 }  // namespace qwenvl_paged

@@ -315,6 +315,10 @@ bool MemoryAllocator::retire_swap_batches() {
 
 bool MemoryAllocator::order_engine_after_swaps(const PhysicalBlockId* frames, std::size_t n, bool writes) {
     if (config_.placement != BlockPlacement::Device || swap_events_.empty()) return true;
+    // Batches finish in launch order: when the engine stream already waits
+    // for (or the host has seen the end of) the newest one, no frame needs a
+    // look.
+    if (swap_events_.back().epoch <= std::max(completed_epoch_, engine_waited_epoch_)) return true;
     // A read depends on the last scatter into the frame; a write also on the
     // last gather out of it (which must have read the old bytes first).
     std::uint64_t need = 0;

@@ -5,6 +5,7 @@
 
 #include "qvp.h"
 
+#include <algorithm>
 #include <cstring>
 #include <type_traits>
 #include <utility>
@@ -92,12 +93,26 @@ bool refuse(std::string msg) {
 
 // Frames of logical blocks 0 .. ceil(ctx / tpb) - 1, QVP_UNMAPPED_BLOCK for a
 // block that is unmapped or swapped out (the packer then refuses the batch).
+// A table that grew by appending (entry k holds logical block k, the usual
+// case) is read in one pass over its entries; one with holes goes through
+// entry() per block.
 void collect_blocks(const CacheView& view, std::uint32_t context_len, std::vector<std::uint32_t>& ids) {
     const std::uint32_t tpb = view.layout.shape.tokens_per_block;
     const std::uint32_t needed = (context_len + tpb - 1) / tpb;
-    for (std::uint32_t j = 0; j < needed; ++j) {
+    const std::vector<BlockTableEntry>& entries = view.block_table->entries();
+    const std::size_t base = ids.size();
+    ids.resize(base + needed);
+    std::uint32_t* out = ids.data() + base;
+    std::uint32_t j = 0;
+    const std::uint32_t dense = static_cast<std::uint32_t>(std::min<std::size_t>(needed, entries.size()));
+    for (; j < dense; ++j) {
+        const BlockTableEntry& e = entries[j];
+        if (e.logical.index != j) break;
+        out[j] = e.swap_slot.has_value() ? QVP_UNMAPPED_BLOCK : e.physical_id;
+    }
+    for (; j < needed; ++j) {
         const BlockTableEntry* e = view.block_table->entry(j);
-        ids.push_back((e == nullptr || e->swap_slot.has_value()) ? QVP_UNMAPPED_BLOCK : e->physical_id);
+        out[j] = (e == nullptr || e->swap_slot.has_value()) ? QVP_UNMAPPED_BLOCK : e->physical_id;
     }
 }
 
@@ -349,16 +364,17 @@ bool PagedAttentionBatch::upload(const std::vector<std::uint32_t>& context_lens,
     return true;
 }
 
-bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
-                                 std::uint32_t layer, std::uint32_t num_query_heads, float scale,
-                                 const void* device_query, void* device_out, ElementType out_type) {
+bool PagedAttentionBatch::prepare(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                                  std::uint32_t layer, std::uint32_t num_query_heads, float scale,
+                                  const void* device_query, void* device_out, ElementType out_type, void*& stream) {
     int cache_type = 0;
-    void* stream = nullptr;
     if (!pack(views, context_lens, layer, num_query_heads, device_query, device_out, cache_type, stream)) return false;
     const KVBlockLayout& layout = views.front().layout;
     const BlockShape& shape = layout.shape;
     const MemoryAllocator* allocator = views.front().allocator;
-    qvp_decode_args args{};
+    if (!args_) args_ = std::make_unique<qvp_decode_args>();
+    qvp_decode_args& args = *args_;
+    args = qvp_decode_args{};
     args.query = device_query;
     args.out = device_out;
     args.kv_base = allocator->device_base();
@@ -377,8 +393,48 @@ bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std:
     args.stream_stride = layout.stream_stride();
     args.layer_stride = layout.layer_stride();
     args.scale = scale;
-    if (!upload(context_lens, shape.tokens_per_block, &args, stream)) return false;
-    if (qvp_paged_decode(&args, stream) != QVP_OK) return fail(std::string("decode: ") + qvp_last_error());
+    return true;
+}
+
+bool PagedAttentionBatch::decode(const std::vector<CacheView>& views, const std::vector<std::uint32_t>& context_lens,
+                                 std::uint32_t layer, std::uint32_t num_query_heads, float scale,
+                                 const void* device_query, void* device_out, ElementType out_type) {
+    void* stream = nullptr;
+    packed_ready_ = false;
+    if (!prepare(views, context_lens, layer, num_query_heads, scale, device_query, device_out, out_type, stream)) {
+        return false;
+    }
+    const qvp_decode_args* args = args_.get();
+    if (!upload(context_lens, views.front().layout.shape.tokens_per_block, args, stream)) return false;
+    if (qvp_paged_decode(args, stream) != QVP_OK) return fail(std::string("decode: ") + qvp_last_error());
+    return true;
+}
+
+bool PagedAttentionBatch::pack_ahead(const std::vector<CacheView>& views,
+                                     const std::vector<std::uint32_t>& context_lens, std::uint32_t layer,
+                                     std::uint32_t num_query_heads, float scale, const void* device_query,
+                                     void* device_out, ElementType out_type) {
+    void* stream = nullptr;
+    packed_ready_ = false;
+    if (!prepare(views, context_lens, layer, num_query_heads, scale, device_query, device_out, out_type, stream)) {
+        return false;
+    }
+    const qvp_decode_args* args = args_.get();
+    if (qvp_pack_ahead(batch_, static_cast<std::uint32_t>(context_lens.size()), ids_.empty() ? nullptr : ids_.data(),
+                       cu_.data(), context_lens.data(), views.front().layout.shape.tokens_per_block, num_pool_blocks_,
+                       split_tokens_, args, stream) != QVP_OK) {
+        return fail(std::string("pack: ") + qvp_last_error());
+    }
+    packed_stream_ = stream;
+    packed_ready_ = true;
+    return true;
+}
+
+bool PagedAttentionBatch::decode_packed() {
+    if (!packed_ready_) return fail("nothing packed: call pack_ahead() first");
+    packed_ready_ = false;
+    const qvp_decode_args* args = args_.get();
+    if (qvp_paged_decode(args, packed_stream_) != QVP_OK) return fail(std::string("decode: ") + qvp_last_error());
     return true;
 }
 
@@ -386,6 +442,7 @@ bool PagedAttentionBatch::prefill(const std::vector<CacheView>& views, const std
                                   const std::vector<std::uint32_t>& first_new, std::uint32_t layer,
                                   std::uint32_t num_query_heads, float scale, const void* device_query,
                                   void* device_out, ElementType out_type) {
+    packed_ready_ = false;
     if (first_new.size() != views.size()) return fail("views and first_new differ in size");
     for (std::size_t b = 0; b < first_new.size() && b < context_lens.size(); ++b) {
         if (first_new[b] >= context_lens[b]) return fail("first new position is not below the context length");

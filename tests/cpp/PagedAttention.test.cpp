@@ -386,3 +386,78 @@ TEST(PagedAttentionBatchTest, OneLaunchDecodesEveryViewLikeTheSingleCalls) {
     (void)qvp_free(dq);
     (void)qvp_free(dout);
 }
+
+TEST(PagedAttentionBatchTest, PackAheadPairsDecodeLikeDecode) {
+    // Two objects in turn, each step packed ahead (its upload riding in the
+    // previous step's decode launch) and decoded by decode_packed(): every
+    // step's output is bit-equal to decode() of the same step. The
+    // Qwen2-VL-7B head shape, so the persistent MFMA kernel runs.
+    DeviceHarness h(shape_of(16, 1, 4, 128, 2), 256);
+    ASSERT_TRUE(h.ready());
+    const std::uint32_t base[] = {200, 700, 1100, 333, 900, 64};
+    constexpr std::uint32_t kSteps = 5;
+    for (SequenceId s = 1; s <= 6; ++s) {
+        ASSERT_TRUE(h.cache.create_sequence(SequenceMetadata{s, s, {}, {}}));
+        ASSERT_TRUE(h.cache.reserve_tokens(s, base[s - 1] + kSteps));
+    }
+    // K/V: every frame of the pool gets a pattern (one write per frame).
+    std::vector<std::uint16_t> frame(h.allocator.block_stride() / 2);
+    for (PhysicalBlockId f = 0; f < 256; ++f) {
+        for (std::size_t i = 0; i < frame.size(); ++i) {
+            frame[i] = bf16(mix_pattern({f, static_cast<std::uint32_t>(i)})).bits;
+        }
+        ASSERT_TRUE(h.allocator.write_block_bytes(f, 0, frame.data(), frame.size() * 2));
+    }
+    std::vector<CacheView> views;
+    for (SequenceId s = 1; s <= 6; ++s) views.push_back(*h.cache.cache_view(s));
+    const std::size_t qn = views.size() * 28 * 128;
+    std::vector<std::uint16_t> q(qn);
+    for (std::size_t i = 0; i < qn; ++i) q[i] = bf16(mix_pattern({5u, static_cast<std::uint32_t>(i)})).bits;
+    void* dq = nullptr;
+    ASSERT_EQ(qvp_malloc(&dq, qn * 2), QVP_OK);
+    ASSERT_EQ(qvp_memcpy_htod(dq, q.data(), qn * 2, h.allocator.stream()), QVP_OK);
+    std::vector<void*> outs(kSteps, nullptr), refs(kSteps, nullptr);
+    for (std::uint32_t r = 0; r < kSteps; ++r) {
+        ASSERT_EQ(qvp_malloc(&outs[r], qn * 4), QVP_OK);
+        ASSERT_EQ(qvp_malloc(&refs[r], qn * 4), QVP_OK);
+    }
+    auto lens_of = [&](std::uint32_t r) {
+        std::vector<std::uint32_t> l;
+        for (std::uint32_t b : base) l.push_back(b + r);
+        return l;
+    };
+    const float scale = 1.0f / std::sqrt(128.0f);
+    PagedAttentionBatch a, b;
+    EXPECT_FALSE(a.decode_packed());  // nothing packed yet
+    EXPECT_FALSE(a.last_error().empty());
+    PagedAttentionBatch* cur = &a;
+    PagedAttentionBatch* nxt = &b;
+    ASSERT_TRUE(cur->pack_ahead(views, lens_of(0), 0, 28, scale, dq, outs[0], ElementType::F32)) << cur->last_error();
+    for (std::uint32_t r = 0; r < kSteps; ++r) {
+        if (r + 1 < kSteps) {
+            ASSERT_TRUE(nxt->pack_ahead(views, lens_of(r + 1), 0, 28, scale, dq, outs[r + 1], ElementType::F32))
+                << nxt->last_error();
+        }
+        ASSERT_TRUE(cur->decode_packed()) << cur->last_error();
+        std::swap(cur, nxt);
+    }
+    EXPECT_FALSE(a.decode_packed());  // each pack is decoded once
+    PagedAttentionBatch plain;
+    for (std::uint32_t r = 0; r < kSteps; ++r) {
+        ASSERT_TRUE(plain.decode(views, lens_of(r), 0, 28, scale, dq, refs[r], ElementType::F32)) << plain.last_error();
+    }
+    ASSERT_EQ(qvp_stream_synchronize(h.allocator.stream()), QVP_OK);
+    for (std::uint32_t r = 0; r < kSteps; ++r) {
+        std::vector<std::uint32_t> got(qn), ref(qn);
+        ASSERT_EQ(qvp_memcpy_dtoh(got.data(), outs[r], qn * 4, h.allocator.stream()), QVP_OK);
+        ASSERT_EQ(qvp_memcpy_dtoh(ref.data(), refs[r], qn * 4, h.allocator.stream()), QVP_OK);
+        ASSERT_EQ(qvp_stream_synchronize(h.allocator.stream()), QVP_OK);
+        EXPECT_TRUE(got == ref) << "step " << r;
+    }
+    qvp_decode_plan plan{};
+    ASSERT_EQ(qvp_decode_plan_info(a.packed(), &plan), QVP_OK);
+    EXPECT_EQ(plan.kernel, QVP_DECODE_MFMA);
+    for (void* p : outs) (void)qvp_free(p);
+    for (void* p : refs) (void)qvp_free(p);
+    (void)qvp_free(dq);
+}

@@ -60,8 +60,10 @@ def test_split_kernels_follow_the_split_size(kv_dtype, split):
         w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=11, kv_sigma=1.0)
         run = GpuRun(w)
     else:
-        w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F16, seed=11)
-        w32 = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=11, kv_sigma=0.5)
+        # head_dim 64: fp16 caches with head_dim 128 run the persistent MFMA
+        # kernel (tests/test_gpu_decode_f16.py).
+        w = W.custom(lens, 28, 4, 64, kv_dtype=qvp.DTYPE_F16, seed=11)
+        w32 = W.custom(lens, 28, 4, 64, kv_dtype=qvp.DTYPE_F32, seed=11, kv_sigma=0.5)
         image = w32.pool_image().view(np.float32).astype(np.float16).view(np.uint8)
         run = GpuRun(w, image=image, query=w32.query().astype(np.float16).view(np.uint16))
     _, ref32 = oracle_decode(w, run.image, run.query)
@@ -377,16 +379,17 @@ def test_multi_layer_frames_read_only_the_requested_layer():
 
 
 def test_fp16_cache_generic_path():
-    print("case: fp16 cache", flush=True)
-    w = W.custom([50, 130], 8, 2, 128, kv_dtype=qvp.DTYPE_F16, seed=3)
+    print("case: fp16 cache, head_dim 96 (generic kernel)", flush=True)
+    w = W.custom([50, 130], 8, 2, 96, kv_dtype=qvp.DTYPE_F16, seed=3)
     # fp16 pool: reinterpret the fp32 draws rounded to fp16.
-    image32 = W.custom([50, 130], 8, 2, 128, kv_dtype=qvp.DTYPE_F32, seed=3)
+    image32 = W.custom([50, 130], 8, 2, 96, kv_dtype=qvp.DTYPE_F32, seed=3)
     raw = image32.pool_image().view(np.float32)
     image = raw.astype(np.float16).view(np.uint8)
     q = image32.query().astype(np.float16).view(np.uint16)
     run = GpuRun(w, image=image, query=q)
     _, ref32 = oracle_decode(w, image, q)
     got = run.decode(out_dtype=qvp.DTYPE_F32)
+    assert run.batch.decode_plan()["kernel"] == "generic"
     assert_close_bf16(got, ref32, "fp16 cache")
 
 
