@@ -594,49 +594,58 @@ def swap_bench(steps: int, warmup: int) -> int:
     return 0
 
 
-def fp32_bench(steps: int, warmup: int, cpu_reps: int, with_cpu: bool) -> int:
+def dtype_bench(kv_dtype: int, steps: int, warmup: int, pools_n: int, cpu_reps: int, with_cpu: bool) -> int:
     """The config2 batch (same 64 context lengths, Hq28/Hkv4/D128, block 16)
-    with an fp32 cache -- the reference's paged_attention_decode<float> --
-    on the fp32 matrix-core kernel; one step = one decode call (kernel and
-    split merge)."""
+    with an fp32 or fp16 cache -- the reference's paged_attention_decode<T>
+    for T = float or a two-byte half -- on the persistent matrix-core decode
+    (fp32 or f16 MFMA tiles; free cost-balanced cuts as in the headline);
+    `pools_n` pool copies rotate between steps. One step = one decode call;
+    the kernel's average launch duration is two HIP events around the K
+    steps, over K."""
+    name = "fp32" if kv_dtype == qvp.DTYPE_F32 else "fp16"
     c2 = W.config2()
-    w = W.custom(list(c2.context_lens), 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=2, spare=0.1)
-    w.name = "config2-shape fp32"
+    w = W.custom(list(c2.context_lens), 28, 4, 128, kv_dtype=kv_dtype, seed=2, spare=0.1)
+    w.name = f"config2-shape {name}"
     rng = np.random.default_rng(2)
-    chunk = rng.normal(0, 0.5, 16_777_259).astype(np.float32)
-    total = w.num_pool_blocks * w.block_stride // 4
+    chunk = W.to_elements(rng.normal(0, 0.5, 16_777_259).astype(np.float32), kv_dtype)
+    total = w.num_pool_blocks * w.block_stride // chunk.itemsize
     image = np.tile(chunk, -(-total // chunk.size))[:total].view(np.uint8)
     query = w.query()
-    pool = qvp.BlockPool(w.num_pool_blocks, w.block_bytes)
-    pool.upload_all(image)
+    pools = []
+    for _ in range(max(1, pools_n)):
+        pool = qvp.BlockPool(w.num_pool_blocks, w.block_bytes)
+        pool.upload_all(image)
+        pools.append(pool)
     q = qvp.DeviceBuffer.from_array(query)
     out = qvp.DeviceBuffer(w.num_seqs * 28 * 128 * 4)
     stream = qvp.Stream()
     batch = qvp.Batch()
-    batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks, 512, stream)
+    batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks, 0, stream)
     ws = qvp.DeviceBuffer(batch.workspace_bytes(28, 128))
-    args = qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=pool.base, block_stride=pool.stride, batch=batch,
-                           kv_dtype=qvp.DTYPE_F32, out_dtype=qvp.DTYPE_F32, layer=0, num_layers=1,
-                           num_query_heads=28, num_kv_heads=4, head_dim=128, tokens_per_block=16, scale=w.scale,
-                           workspace=ws.ptr, workspace_bytes=ws.nbytes)
-    for _ in range(warmup):
-        qvp.paged_decode(args, stream)
+    args = [qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=pool.base, block_stride=pool.stride, batch=batch,
+                            kv_dtype=kv_dtype, out_dtype=qvp.DTYPE_F32, layer=0, num_layers=1,
+                            num_query_heads=28, num_kv_heads=4, head_dim=128, tokens_per_block=16, scale=w.scale,
+                            workspace=ws.ptr, workspace_bytes=ws.nbytes) for pool in pools]
+    for i in range(max(warmup, 200)):
+        qvp.paged_decode(args[i % len(args)], stream)
     stream.synchronize()
     e0, e1 = qvp.Event(), qvp.Event()
     e0.record(stream)
-    for _ in range(steps):
-        qvp.paged_decode(args, stream)
+    for i in range(steps):
+        qvp.paged_decode(args[i % len(args)], stream)
     e1.record(stream)
     stream.synchronize()
     ms = e0.elapsed_ms(e1) / steps
     algo = w.algorithmic_bytes()
     gbs = algo / (ms * 1e-3) / 1e9
-    line = {"mode": "fp32", "kernel": "decode_f32_grouped + merge_splits", "workload": w.name,
-            "data": "synthetic N(0,1) q, N(0,0.5) K/V, fp32", "steps": steps, "ms_per_step": round(ms, 5),
+    plan = batch.decode_plan()
+    line = {"mode": name, "kernel": plan["kernel"], "decode_plan": plan, "workload": w.name,
+            "data": f"synthetic N(0,1) q, N(0,0.5) K/V, {name}, {len(pools)} rotating pool copies",
+            "steps": steps, "ms_per_step": round(ms, 5),
             "algorithmic_bytes_per_step": algo, "decode_tokens_per_s": round(w.num_seqs / (ms * 1e-3), 1),
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                          "frac": round(gbs / PEAK_HBM_GBPS, 4)}}
-    if with_cpu:
+    if with_cpu and kv_dtype == qvp.DTYPE_F32:
         line["cpu_baseline"] = cpu_baseline(w, image, query, cpu_reps)
     print(json.dumps(line))
     return 0
@@ -726,6 +735,7 @@ def main() -> int:
     ap.add_argument("--swap", action="store_true", help="time swap-out / swap-in of whole 7B frames")
     ap.add_argument("--copy", action="store_true", help="time copy_blocks of 128 frame pairs at 7B frame sizes")
     ap.add_argument("--fp32", action="store_true", help="time the config2 batch with an fp32 cache")
+    ap.add_argument("--fp16", action="store_true", help="time the config2 batch with an fp16 cache")
     ap.add_argument("--tiles", action="store_true",
                     help="time matrix-core against vector-ALU decode tiles at GQA groups 1, 2 and 7")
     ap.add_argument("--torch-sdpa", action="store_true", help=argparse.SUPPRESS)
@@ -751,8 +761,9 @@ def main() -> int:
         return mrope_bench(args.steps, args.warmup, not args.no_cpu)
     if args.swap:
         return swap_bench(args.steps, args.warmup)
-    if args.fp32:
-        return fp32_bench(args.steps, args.warmup, args.cpu_reps, not args.no_cpu)
+    if args.fp32 or args.fp16:
+        return dtype_bench(qvp.DTYPE_F32 if args.fp32 else qvp.DTYPE_F16, args.steps, args.warmup, args.pools,
+                           args.cpu_reps, not args.no_cpu)
     if args.tiles:
         return tiles_bench(args.steps, args.warmup, args.pools)
     if args.torch_sdpa:

@@ -77,7 +77,7 @@ struct qvp_schedule {
     uint32_t max_partial_pieces_per_wg{0};
     uint32_t hps{1};  // kv heads per segment
     uint32_t tile_group{0};  // DecodeGeometry::tile_group the LDS budget was planned for
-    uint32_t kv_f16{0};      // DecodeGeometry::kv_f16 (fp16 caches plan no shared prefixes)
+    uint32_t kv_elem{0};     // DecodeGeometry::kv_elem (only bf16 caches plan shared prefixes)
     uint32_t partition_tiles{0};  // ranges cut only at multiples of this many tiles of a sequence (0: anywhere)
     std::vector<double> weights;  // streaming weight per kv-head group the ranges were cut for
     bool defer{false};            // piece results held in LDS until a range is done

@@ -34,10 +34,15 @@ struct DecodeGeometry {
     // Persistent kernel: 0 for matrix-core tiles, else vector tiles for query
     // groups up to this bound (1, 2, 4 or 8).
     uint32_t tile_group;
-    // Persistent kernel: 1 when the cache (and query) elements are IEEE
-    // binary16, 0 for bf16.
-    uint32_t kv_f16;
+    // Persistent kernel: the cache's (and query's) element type, kElemBf16,
+    // kElemF16 or kElemF32.
+    uint32_t kv_elem;
 };
+
+// Element codes of DecodeGeometry::kv_elem.
+constexpr uint32_t kElemBf16 = 0;
+constexpr uint32_t kElemF16 = 1;
+constexpr uint32_t kElemF32 = 2;
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -81,8 +86,9 @@ constexpr uint32_t kVectorTilesUpToGroup = 0;
 // whether the persistent MFMA kernel runs this decode.
 int decode_geometry(const qvp_decode_args* a, const qvp_packed_view& v, DecodeGeometry* g, bool* supported_mfma);
 
-// MFMA path (bf16 or fp16, head_dim 128, group <= 16, power-of-two tpb >=
-// 16): persistent workgroups over a balanced schedule built from the batch.
+// MFMA path (bf16, fp16 or fp32, head_dim 128, group <= 16, power-of-two tpb
+// >= 16, scale > 0): persistent workgroups over a balanced schedule built from
+// the batch.
 bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr,
                     uintptr_t kv_base_addr);
 

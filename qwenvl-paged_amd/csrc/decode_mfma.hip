@@ -47,6 +47,7 @@
 //   as hi + lo (hi = P truncated to bf16, lo = P - hi rounded to bf16), which
 //   keeps the weights at about 2^-16 relative error. C register r of PV MFMA n
 //   in lane (c, j) is O[head c][dim 32j + 8r + n].
+#include "f32_tile.h"
 #include "mfma_tile.h"
 #include "valu_tile.h"
 
@@ -211,10 +212,16 @@ __device__ inline void load_tile(const DecodeGeometry& p, const TileRef& r, int 
 }
 
 // kVG = 0: matrix-core tiles; 1, 2: vector tiles for query groups up to kVG.
-// kF16: the cache holds IEEE binary16 elements (matrix-core tiles only).
-template <typename OutT, int kVG, bool kF16>
+// kElem: the cache's element type (kElemBf16, kElemF16, kElemF32); fp16 and
+// fp32 caches run matrix-core tiles only.
+template <typename OutT, int kVG, uint32_t kElem>
 __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(DecodeGeometry p, MfmaArgs a) {
-    static_assert(!kF16 || kVG == 0, "vector tiles read bf16 caches");
+    static_assert(kElem == kElemBf16 || kVG == 0, "vector tiles read bf16 caches");
+    constexpr bool kF16 = kElem == kElemF16;
+    constexpr bool kF32 = kElem == kElemF32;
+    // Query words per lane: eight bf16 / fp16 elements each of four MFMA
+    // k-groups, or four fp32 elements each of eight (f32_tile.h).
+    constexpr int kQWords = kF32 ? 8 : 4;
     __shared__ VectorTileLds<kVG> vt;
     __shared__ float sm_m[kWaves][16];
     __shared__ float sm_l[kWaves][16];
@@ -299,7 +306,10 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     // tile's loads are in flight (nxt) and the block ids of the tile after that
     // are being fetched (r2), so no table lookup sits between a tile's arrival
     // and the issue of the following loads. (pi2, t2) is the cursor of r2.
+    // fp32 caches: a 32-token tile is two 16-token halves, loaded one half
+    // ahead; `pend` is the tile whose second half is still to be loaded.
     KvTile nxt;
+    TileRef pend{};
     int pi2 = fd[0];
     int t2 = fd[1];
     bool have_partial = false;
@@ -310,7 +320,13 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
         r0.t = t2;
         r0.blk0 = fd[3];
         r0.blk1 = fd[4];
-        load_tile(p, r0, c, j, nxt);
+        if constexpr (kF32) {
+            load_half_f32(p.kv_base, p.block_stride, p.head_stride, p.k_off, p.v_off, p.token_stride, p.tpb, r0.g,
+                          r0.blk0, r0.t * kTileTokens, c, j, nxt);
+            pend = r0;
+        } else {
+            load_tile(p, r0, c, j, nxt);
+        }
     }
     has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
     TileRef r2{};
@@ -323,22 +339,38 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     // first tile is computed (a select on them would wait at once). The next
     // piece's query is loaded when a piece starts, so it has arrived when
     // that piece's first tile is computed.
-    auto load_query = [&](int pi, u32x4 (&qo)[4]) {
+    // (fp32: lane (c, j) holds dims 32j .. 32j + 31 of head c, f32_tile.h.)
+    auto load_query = [&](int pi, u32x4 (&qo)[kQWords]) {
         const qvp_piece d = piece_at(a.pieces, pi);
-        const uint16_t* q = static_cast<const uint16_t*>(p.query) +
-                            (static_cast<uint64_t>(d.b) * p.num_q_heads + (d.g * hps + hl) * G + min(c, G - 1)) * kD;
+        const uint64_t row = (static_cast<uint64_t>(d.b) * p.num_q_heads + (d.g * hps + hl) * G + min(c, G - 1)) * kD;
+        if constexpr (kF32) {
+            const float* q = static_cast<const float*>(p.query) + row + 32 * j;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qo[i] = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
+            for (int i = 0; i < 8; ++i) qo[i] = *reinterpret_cast<const u32x4*>(q + 4 * i);
+        } else {
+            const uint16_t* q = static_cast<const uint16_t*>(p.query) + row;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qo[i] = *reinterpret_cast<const u32x4*>(q + 32 * i + 8 * j);
+        }
     };
-    u32x4 qnext[4];
-    if (pb < pe) load_query(pb, qnext);
+    // fp32 loads each piece's query when the piece starts: holding the next
+    // one as well (32 more registers) made the kernel spill.
+    constexpr bool kQueryAhead = !kF32;
+    u32x4 qnext[kQueryAhead ? kQWords : 1];
+    if constexpr (kQueryAhead) {
+        if (pb < pe) load_query(pb, qnext);
+    }
     for (int pi = pb; pi < pe; ++pi) {
         const qvp_piece d = piece_at(a.pieces, pi);
         const int ctx = d.ctx;
-        u32x4 qop[4];
+        u32x4 qop[kQWords];
+        if constexpr (kQueryAhead) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) qop[i] = qnext[i];
-        if (pi + 1 < pe) load_query(pi + 1, qnext);
+            for (int i = 0; i < kQWords; ++i) qop[i] = qnext[i];
+            if (pi + 1 < pe) load_query(pi + 1, qnext);
+        } else {
+            load_query(pi, qop);
+        }
 
         if constexpr (kVG == 0) {
             floatx4 o[8];
@@ -347,12 +379,30 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
             float m_run = -INFINITY;
             float l_run = 0.f;
 
-            for (int t = d.t0 + tlane; t < d.t1; t += tl) {
-                KvTile cur = nxt;
-                if (has2) load_tile(p, r2, c, j, nxt);
-                has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
-                if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
-                compute_tile<kF16>(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
+            if constexpr (kF32) {
+                for (int t = d.t0 + tlane; t < d.t1; t += tl) {
+                    KvTile cur = nxt;  // first half of tile t
+                    load_half_f32(p.kv_base, p.block_stride, p.head_stride, p.k_off, p.v_off, p.token_stride, p.tpb,
+                                  pend.g, pend.blk1, pend.t * kTileTokens + 16, c, j, nxt);
+                    compute_half_f32(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
+                    cur = nxt;  // second half
+                    if (has2) {
+                        load_half_f32(p.kv_base, p.block_stride, p.head_stride, p.k_off, p.v_off, p.token_stride,
+                                      p.tpb, r2.g, r2.blk0, r2.t * kTileTokens, c, j, nxt);
+                        pend = r2;
+                    }
+                    has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
+                    if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
+                    compute_half_f32(cur, qop, t * kTileTokens + 16, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
+                }
+            } else {
+                for (int t = d.t0 + tlane; t < d.t1; t += tl) {
+                    KvTile cur = nxt;
+                    if (has2) load_tile(p, r2, c, j, nxt);
+                    has2 = has2 && next_tile(a, pe, tlane, tl, pi2, t2);
+                    if (has2) r2 = resolve_tile(p, a, pi2, t2, hl);
+                    compute_tile<kF16>(cur, qop, t * kTileTokens, ctx - 1, ctx, p.scale_log2, j, m_run, l_run, o);
+                }
             }
 
             // This wave's state for (piece, head g) goes to LDS in row layout.
@@ -951,20 +1001,21 @@ const void* prefix_kernel(uint32_t out_dtype) {
 // The kernel instantiation for an output type, a tile engine and the cache's
 // element type (fp16 caches run matrix-core tiles only).
 template <typename OutT>
-const void* kernel_for_group(uint32_t tile_group, bool f16) {
-    if (f16) return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0, true>);
+const void* kernel_for_group(uint32_t tile_group, uint32_t elem) {
+    if (elem == kElemF16) return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0, kElemF16>);
+    if (elem == kElemF32) return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0, kElemF32>);
     switch (tile_group) {
-        case 0: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0, false>);
-        case 1: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 1, false>);
-        default: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 2, false>);
+        case 0: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 0, kElemBf16>);
+        case 1: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 1, kElemBf16>);
+        default: return reinterpret_cast<const void*>(&decode_mfma_persistent<OutT, 2, kElemBf16>);
     }
 }
 
-const void* decode_kernel(uint32_t out_dtype, uint32_t tile_group, bool f16) {
+const void* decode_kernel(uint32_t out_dtype, uint32_t tile_group, uint32_t elem) {
     switch (out_dtype) {
-        case QVP_DTYPE_F32: return kernel_for_group<float>(tile_group, f16);
-        case QVP_DTYPE_BF16: return kernel_for_group<uint16_t>(tile_group, f16);
-        default: return kernel_for_group<_Float16>(tile_group, f16);
+        case QVP_DTYPE_F32: return kernel_for_group<float>(tile_group, elem);
+        case QVP_DTYPE_BF16: return kernel_for_group<uint16_t>(tile_group, elem);
+        default: return kernel_for_group<_Float16>(tile_group, elem);
     }
 }
 
@@ -992,11 +1043,13 @@ int device_max_wgs(uint32_t* wgs) {
         for (uint32_t dt : {QVP_DTYPE_F32, QVP_DTYPE_BF16, QVP_DTYPE_F16}) {
             for (uint32_t tg : kTileGroups) {
                 const int dyn = static_cast<int>(kMaxLdsBytes - static_lds_bytes(tg));
-                QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, tg, false), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                            dyn));
+                QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, tg, kElemBf16),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
             }
-            QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, 0, true), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kMaxLdsBytes - static_lds_bytes(0))));
+            for (uint32_t el : {kElemF16, kElemF32}) {
+                QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, 0, el), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            static_cast<int>(kMaxLdsBytes - static_lds_bytes(0))));
+            }
         }
         for (uint32_t dt : {QVP_DTYPE_F32, QVP_DTYPE_BF16, QVP_DTYPE_F16}) {
             QVP_HIP(hipFuncSetAttribute(prefix_kernel(dt), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1161,8 +1214,8 @@ struct PrefixGroup {
 std::vector<PrefixGroup> find_prefix_groups(const ScheduleInput& in, const DecodeGeometry& g, uint32_t hps) {
     std::vector<PrefixGroup> out;
     // The shared-prefix launch reads bf16 caches with matrix-core tiles.
-    if (hps != 1 || in.partition_tiles != 0 || g.tile_group != 0 || g.kv_f16 != 0 || g.group == 0 || g.group > 16 ||
-        in.tpb == 0) {
+    if (hps != 1 || in.partition_tiles != 0 || g.tile_group != 0 || g.kv_elem != kElemBf16 || g.group == 0 ||
+        g.group > 16 || in.tpb == 0) {
         return out;
     }
     const int cap = std::min<int>(kPrefixMaxMembers, 4 * static_cast<int>(16 / g.group));
@@ -1233,14 +1286,14 @@ bool mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_
     const bool aligned = (g.block_stride % 16 == 0) && (g.k_off % 16 == 0) && (g.v_off % 16 == 0) &&
                          (g.token_stride % 16 == 0) && (g.head_stride % 16 == 0) && (kv_base_addr % 16 == 0) &&
                          (query_addr % 16 == 0);
-    return (kv_dtype == QVP_DTYPE_BF16 || kv_dtype == QVP_DTYPE_F16) && g.head_dim == kD && g.group >= 1 &&
-           g.group <= 16 && pow2 && g.tpb >= 16 && aligned && g.scale_log2 > 0.0f;
+    return (kv_dtype == QVP_DTYPE_BF16 || kv_dtype == QVP_DTYPE_F16 || kv_dtype == QVP_DTYPE_F32) && g.head_dim == kD &&
+           g.group >= 1 && g.group <= 16 && pow2 && g.tpb >= 16 && aligned && g.scale_log2 > 0.0f;
 }
 
 bool mfma_schedule_current(const qvp_batch* batch, const DecodeGeometry& g) {
     const qvp_schedule& s = batch->sched;
     if (!s.valid || s.pack_generation != batch->generation || s.num_kv_heads != g.num_kv_heads ||
-        s.group != g.group || s.tile_group != g.tile_group || s.kv_f16 != g.kv_f16 ||
+        s.group != g.group || s.tile_group != g.tile_group || s.kv_elem != g.kv_elem ||
         s.partition_tiles != batch->partition_tiles) {
         return false;
     }
@@ -1531,7 +1584,7 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     s.num_kv_heads = num_kv_heads;
     s.group = g.group;
     s.tile_group = g.tile_group;
-    s.kv_f16 = g.kv_f16;
+    s.kv_elem = g.kv_elem;
     s.partition_tiles = in.partition_tiles;
     s.max_wgs = max_wgs;
     s.weights = weights;
@@ -1716,7 +1769,7 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     }
     DecodeGeometry gk = g;
     if (s.num_prefix_items > 0) {
-        if (g.kv_f16 != 0) return fail(QVP_ERR_INVALID_ARGUMENT, "shared-prefix schedule for an fp16 cache");
+        if (g.kv_elem != kElemBf16) return fail(QVP_ERR_INVALID_ARGUMENT, "shared-prefix schedule for a non-bf16 cache");
         PrefixArgs pa{};
         pa.items = reinterpret_cast<const qvp_prefix_item*>(s.words + s.off_prefix);
         pa.suffix = reinterpret_cast<const qvp_piece*>(s.words + s.off_suffix);
@@ -1734,7 +1787,7 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
     // upload, if any, needs this one).
     if (s.num_wgs + copy_wgs > 0) {
         void* kargs[] = {&gk, &a};
-        QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group, g.kv_f16 != 0), dim3(s.num_wgs + copy_wgs),
+        QVP_HIP(hipLaunchKernel(decode_kernel(out_dtype, s.tile_group, g.kv_elem), dim3(s.num_wgs + copy_wgs),
                                 dim3(kThreads), kargs, s.lds_bytes, stream));
     }
     // The merge runs inside the kernel; the event still marks the split/merge

@@ -153,18 +153,19 @@ int decode_geometry(const qvp_decode_args* a, const qvp_packed_view& v, DecodeGe
     g.group = a->num_query_heads / a->num_kv_heads;
     g.head_dim = a->head_dim;
     g.scale_log2 = a->scale * kLog2e;
-    g.kv_f16 = a->kv_dtype == QVP_DTYPE_F16 ? 1u : 0u;
+    g.kv_elem = a->kv_dtype == QVP_DTYPE_F16 ? kElemF16 : (a->kv_dtype == QVP_DTYPE_F32 ? kElemF32 : kElemBf16);
     *supported_mfma = mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
                                      reinterpret_cast<uintptr_t>(a->kv_base));
     if (a->tile_engine > QVP_TILE_VECTOR) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "unknown tile engine %u", a->tile_engine);
     }
     if (*supported_mfma) {
-        if (g.kv_f16 != 0 && a->tile_engine == QVP_TILE_VECTOR) {
-            return fail(QVP_ERR_INVALID_ARGUMENT, "vector tiles read bf16 caches; an fp16 cache runs matrix-core tiles");
+        if (g.kv_elem != kElemBf16 && a->tile_engine == QVP_TILE_VECTOR) {
+            return fail(QVP_ERR_INVALID_ARGUMENT, "vector tiles read bf16 caches; this cache runs matrix-core tiles");
         }
-        const bool vector = g.kv_f16 == 0 && (a->tile_engine == QVP_TILE_VECTOR ||
-                                              (a->tile_engine == QVP_TILE_AUTO && g.group <= kVectorTilesUpToGroup));
+        const bool vector = g.kv_elem == kElemBf16 &&
+                            (a->tile_engine == QVP_TILE_VECTOR ||
+                             (a->tile_engine == QVP_TILE_AUTO && g.group <= kVectorTilesUpToGroup));
         if (vector && g.group > kVectorTileMaxGroup) {
             return fail(QVP_ERR_INVALID_ARGUMENT, "vector tiles take query groups of at most %u (group %u)",
                         kVectorTileMaxGroup, g.group);

@@ -57,7 +57,9 @@ def test_split_kernels_follow_the_split_size(kv_dtype, split):
     print(f"case: split kernels dtype={kv_dtype} split={split}", flush=True)
     lens = [37, 600, 1500, 4096, 129, 2049]
     if kv_dtype == qvp.DTYPE_F32:
-        w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=11, kv_sigma=1.0)
+        # A negative scale: fp32 caches with a positive one run the persistent
+        # kernel (tests/test_gpu_decode_f32.py).
+        w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=11, kv_sigma=1.0, scale=-0.05)
         run = GpuRun(w)
     else:
         # head_dim 64: fp16 caches with head_dim 128 run the persistent MFMA
