@@ -155,7 +155,7 @@ def cpu_baseline(w: W.Workload, image: np.ndarray, query: np.ndarray, reps: int)
 
 
 # The decode kernel's sources: a traffic profile holds for the build of these.
-KERNEL_SOURCES = ["decode_mfma.hip", "mfma_tile.h", "valu_tile.h", "decode_common.h", "common.h", "batch.h"]
+KERNEL_SOURCES = ["decode_mfma.hip", "mfma_tile.h", "valu_tile.h", "f32_tile.h", "decode_common.h", "common.h", "batch.h"]
 
 
 def kernel_source_digest() -> str:
@@ -725,6 +725,8 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-probe", action="store_true", help="skip the HBM read-ceiling probe")
+    ap.add_argument("--no-engine", action="store_true",
+                    help="skip the engine-entry driver (profiling runs: its kernels would mix in)")
     ap.add_argument("--workload", choices=["config2", "config3"], default="config2")
     ap.add_argument("--cow", action="store_true", help="run the copy-on-write configuration driver")
     ap.add_argument("--trace", action="store_true", help="run the continuous-batching trace driver")
@@ -998,7 +1000,7 @@ def main() -> int:
     if probe is not None:
         probe["kernel_frac_of_probe"] = round(achieved / probe["read_GBps"], 4)
         line["read_ceiling"] = probe
-    if args.workload == "config2":
+    if args.workload == "config2" and not args.no_engine:
         # Tokens/s of the same batch through PagedAttentionBatch over
         # CacheViews (the engine's entry point), beside the C-ABI figures.
         line["engine_entry"] = engine_entry(w, w.seed, max(args.steps, 20))

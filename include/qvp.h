@@ -493,6 +493,25 @@ typedef struct qvp_append_args {
 int qvp_append_kv(const qvp_append_args* args, const uint32_t* frames, const uint32_t* slots,
                   uint32_t count, void* stream);
 
+/* A copy-on-write step in one launch: qvp_copy_blocks(src_ids, dst_ids,
+ * num_pairs, copy_bytes) followed by qvp_append_kv(args, frames, slots, count)
+ * on the pool args describes, with the same result bytes. This is the order
+ * the reference keeps within a step: KVCacheManager::ensure_token_writable
+ * copies a shared block (src/KVCacheManager.cpp:141-150, the memcpy of
+ * MemoryAllocator::copy_block, src/MemoryAllocator.cpp:76-85) before the
+ * harness stores the token's rows into the new frame
+ * (tests/PagedAttention.test.cpp:97-127). Every 16-byte unit of a destination
+ * frame is written once, from the appended row it lies in or else from the
+ * source frame. Refused before anything is enqueued: everything qvp_append_kv
+ * and qvp_copy_blocks refuse, more than 128 copies or 128 tokens, more than
+ * 64 tokens per block, frames of 2 GiB or more, K and V tensors of 4 GiB or
+ * more, copy_bytes not a multiple of 16, pools, rows or strides not 16-byte
+ * aligned, and a token row written into a frame that a copy reads (run the
+ * two calls apart for that). A pair with src == dst is a no-op. */
+int qvp_copy_append_kv(const qvp_append_args* args, const uint32_t* src_ids, const uint32_t* dst_ids,
+                       uint32_t num_pairs, uint64_t copy_bytes, const uint32_t* frames, const uint32_t* slots,
+                       uint32_t count, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* M-RoPE positions (PositionalEncodingSpan, KVCacheManager.h:23-78)        */
 /* ------------------------------------------------------------------------ */

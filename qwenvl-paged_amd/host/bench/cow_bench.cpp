@@ -3,15 +3,20 @@
 // layer) reserved with 2049 slots, so logical block 128 is a partially filled
 // tail shared by the prompt's branches; each prompt forks 8 branches (the
 // prompt keeps its reference), every branch's first decode token lands in the
-// shared tail, and the 128 copy-on-write materialisations of the step run as
-// one batched copy. Then one paged decode over the 128 branches.
+// shared tail, and the step -- the 128 copy-on-write materialisations and the
+// 128 tokens' K/V rows -- runs through KVAppendBatch as one launch (each
+// destination chunk copied, then overwritten by its rows). Then one paged
+// decode over the 128 branches.
 //
 // Checks: the device allocator takes the same decisions as a host-placement
-// allocator replaying the same calls (the reference's memcpy semantics), every
-// copied frame equals its source byte for byte, and the decode of sampled
-// branches matches float64 attention within the bf16 tolerance.
+// allocator replaying the same calls (the reference's memcpy semantics), the
+// whole device pool equals the host pool byte for byte, every copied frame
+// equals its source with the branch's rows over its slot, and the decode of
+// sampled branches matches float64 attention within the bf16 tolerance.
 //
-// Timing (medians of HIP event pairs): step_us_median is a whole
+// Timing (medians of HIP event pairs): copy_append_us_median is the one
+// launch of the step's copies and rows (copy_us_median the copies alone,
+// copy_then_append_us_median the two launches); step_us_median is a whole
 // PagedAttentionBatch::decode call (block-table walk, pack and schedule upload,
 // decode) one step at a time, the stream idle while the host works;
 // pipelined_step_us / pack_ahead_step_us the same steps enqueued back to back
@@ -25,6 +30,7 @@
 //
 // Output: one JSON line. Usage: cow_bench [--prompts N] [--branches N] [--reps N] [--layers N]
 #include "qvp.h"
+#include "qwenvl_paged/KVAppend.h"
 #include "qwenvl_paged/KVCacheManager.h"
 #include "qwenvl_paged/MemoryAllocator.h"
 #include "qwenvl_paged/PagedAttention.h"
@@ -148,47 +154,103 @@ int main(int argc, char** argv) {
     }
     check(dev.synchronize(), "sync");
 
-    // The step's copy-on-write: each branch's token 2049 lands in the shared
-    // tail block, which is copied for it (queued, then one launch).
+    // The step: each branch's token 2049 lands in the shared tail block, which
+    // is copied for it; KVAppendBatch queues the 128 copies and runs them in
+    // the launch that stores the tokens' K/V rows (qvp_copy_append_kv). The
+    // host-placement allocator replays the same step with memcpy calls.
     void* stream = dev.stream();
     void *e0 = nullptr, *e1 = nullptr;
     check(qvp_event_create(&e0) == QVP_OK && qvp_event_create(&e1) == QVP_OK, "events");
-    const std::uint64_t launches_before = dev.copy_launches();
+    const std::uint32_t nb = prompts * branches;
+    std::vector<SequenceId> children(nb);
+    std::vector<TokenPosition> new_pos(nb, kPrompt + 1);
     std::vector<std::pair<PhysicalBlockId, PhysicalBlockId>> copies;
-    for (std::uint32_t p = 0; p < prompts; ++p) {
-        for (std::uint32_t c = 0; c < branches; ++c) {
-            const SequenceId child = 1000 + p * branches + c;
-            const PhysicalBlockId shared = *dev_cache.cache_view(child)->block_table->lookup(kPrompt / kTpb);
-            const auto fd = dev_cache.ensure_token_writable(child, kPrompt + 1);
-            const auto fh = host_cache.ensure_token_writable(child, kPrompt + 1);
-            check(fd.has_value() && fh.has_value() && *fd == *fh, "copy-on-write decisions differ");
-            copies.emplace_back(shared, *fd);
+    for (std::uint32_t i = 0; i < nb; ++i) {
+        children[i] = 1000 + i;
+        copies.emplace_back(*dev_cache.cache_view(children[i])->block_table->lookup(kPrompt / kTpb), 0);
+    }
+    const std::size_t row_elems = static_cast<std::size_t>(layers) * kHkv * kD;  // per token
+    std::vector<std::uint16_t> k_rows(nb * row_elems), v_rows(nb * row_elems);
+    for (auto* rows : {&k_rows, &v_rows}) {
+        for (auto& x : *rows) {
+            const float f = rng.gauss(0.5f);
+            std::uint32_t u;
+            std::memcpy(&u, &f, 4);
+            x = static_cast<std::uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
         }
     }
+    void *dk = nullptr, *dv = nullptr;
+    check(qvp_malloc(&dk, k_rows.size() * 2) == QVP_OK && qvp_malloc(&dv, v_rows.size() * 2) == QVP_OK, "rows");
+    check(qvp_memcpy_htod(dk, k_rows.data(), k_rows.size() * 2, stream) == QVP_OK &&
+              qvp_memcpy_htod(dv, v_rows.data(), v_rows.size() * 2, stream) == QVP_OK,
+          "upload rows");
+    const std::uint64_t launches_before = dev.copy_launches();
+    KVAppendBatch dev_append, host_append;
+    check(dev_append.append(dev_cache, dev, children, new_pos, 0, layers, dk, dv), dev_append.last_error());
+    check(host_append.append(host_cache, host, children, new_pos, 0, layers, k_rows.data(), v_rows.data()),
+          host_append.last_error());
     const std::size_t pending = dev.pending_operations();
-    check(dev.flush(), "flush: " + dev.last_error());
     check(qvp_stream_synchronize(stream) == QVP_OK, "sync");
     const std::uint64_t copy_launches = dev.copy_launches() - launches_before;
-    // Time the same batched copy again (the first launch of a kernel in a
-    // process also loads its code object): copying each source onto its
-    // destination once more changes nothing.
-    std::vector<std::uint32_t> src_ids, dst_ids;
+    for (std::uint32_t i = 0; i < nb; ++i) {
+        copies[i].second = *dev_cache.cache_view(children[i])->block_table->lookup(kPrompt / kTpb);
+        const PhysicalBlockId h = *host_cache.cache_view(children[i])->block_table->lookup(kPrompt / kTpb);
+        check(copies[i].second == h && copies[i].second != copies[i].first, "copy-on-write decisions differ");
+    }
+    // Time the same launch again (the first launch of a kernel in a process
+    // also loads its code object): copying each source onto its destination
+    // and storing the same rows once more changes nothing. Beside it, the
+    // step as two launches (qvp_copy_blocks, then qvp_append_kv).
+    std::vector<std::uint32_t> src_ids, dst_ids, slots(nb, (kPrompt + 1) % kTpb);
     for (auto [src, dst] : copies) {
         src_ids.push_back(src);
         dst_ids.push_back(dst);
     }
-    std::vector<float> copy_times;
-    for (std::uint32_t r = 0; r < std::max<std::uint32_t>(reps, 1); ++r) {
-        check(qvp_event_record(e0, stream) == QVP_OK, "record");
-        check(qvp_copy_blocks(dev.device_base(), dev.block_stride(), pool, src_ids.data(), dst_ids.data(),
-                              static_cast<std::uint32_t>(src_ids.size()), dev.block_stride(), stream) == QVP_OK,
+    qvp_append_args ap{};
+    ap.kv_base = dev.device_base();
+    ap.block_stride = dev.block_stride();
+    ap.num_blocks = pool;
+    ap.kv_dtype = QVP_DTYPE_BF16;
+    ap.num_layers = layers;
+    ap.first_layer = 0;
+    ap.layer_count = layers;
+    ap.num_kv_heads = kHkv;
+    ap.head_dim = kD;
+    ap.tokens_per_block = kTpb;
+    ap.head_stride = layout.head_stride();
+    ap.token_stride = layout.token_stride();
+    ap.stream_stride = layout.stream_stride();
+    ap.layer_stride = layout.layer_stride();
+    ap.k = dk;
+    ap.v = dv;
+    auto median_us = [&](auto&& step) {
+        std::vector<float> t;
+        for (std::uint32_t r = 0; r < std::max<std::uint32_t>(reps, 1); ++r) {
+            check(qvp_event_record(e0, stream) == QVP_OK, "record");
+            step();
+            check(qvp_event_record(e1, stream) == QVP_OK, "record");
+            check(qvp_stream_synchronize(stream) == QVP_OK, "sync");
+            t.push_back(elapsed_ms(e0, e1));
+        }
+        std::sort(t.begin(), t.end());
+        return 1e3 * t[t.size() / 2];
+    };
+    const double fused_us = median_us([&] {
+        check(qvp_copy_append_kv(&ap, src_ids.data(), dst_ids.data(), nb, dev.block_stride(), dst_ids.data(),
+                                 slots.data(), nb, stream) == QVP_OK,
               qvp_last_error());
-        check(qvp_event_record(e1, stream) == QVP_OK, "record");
-        check(qvp_stream_synchronize(stream) == QVP_OK, "sync");
-        copy_times.push_back(elapsed_ms(e0, e1));
-    }
-    std::sort(copy_times.begin(), copy_times.end());
-    const float copy_ms = copy_times[copy_times.size() / 2];
+    });
+    const double copy_us = median_us([&] {
+        check(qvp_copy_blocks(dev.device_base(), dev.block_stride(), pool, src_ids.data(), dst_ids.data(), nb,
+                              dev.block_stride(), stream) == QVP_OK,
+              qvp_last_error());
+    });
+    const double two_launch_us = median_us([&] {
+        check(qvp_copy_blocks(dev.device_base(), dev.block_stride(), pool, src_ids.data(), dst_ids.data(), nb,
+                              dev.block_stride(), stream) == QVP_OK &&
+                  qvp_append_kv(&ap, dst_ids.data(), slots.data(), nb, stream) == QVP_OK,
+              qvp_last_error());
+    });
 
     // Bit-exact: every frame of the device pool equals the host pool's.
     bool frames_equal = true;
@@ -199,16 +261,25 @@ int main(int argc, char** argv) {
         check(host.read_block_bytes(f, 0, b.data(), frame_bytes), "read host");
         frames_equal = a == b;
     }
+    // Each copy equals its source with the branch's rows stored over slot 1.
     bool copies_equal = true;
-    for (auto [src, dst] : copies) {
-        check(dev.read_block_bytes(src, 0, a.data(), frame_bytes), "read");
-        check(dev.read_block_bytes(dst, 0, b.data(), frame_bytes), "read");
+    for (std::uint32_t i = 0; i < nb; ++i) {
+        check(dev.read_block_bytes(copies[i].first, 0, a.data(), frame_bytes), "read");
+        check(dev.read_block_bytes(copies[i].second, 0, b.data(), frame_bytes), "read");
+        for (std::uint32_t l = 0; l < layers; ++l) {
+            for (const KVStream st : {KVStream::Key, KVStream::Value}) {
+                const std::uint16_t* rows = (st == KVStream::Key ? k_rows : v_rows).data() + i * row_elems;
+                for (std::uint32_t h = 0; h < kHkv; ++h) {
+                    const std::size_t off = *layout.element_offset(l, st, slots[i], h) * 2;
+                    std::memcpy(a.data() + off, rows + (static_cast<std::size_t>(l) * kHkv + h) * kD, kD * 2);
+                }
+            }
+        }
         copies_equal = copies_equal && a == b;
     }
 
     // Decode over every branch: context 2050 (the prompt, the shared tail
     // token and the branch's own token, all in frames read back below).
-    const std::uint32_t nb = prompts * branches;
     const std::uint32_t ctx = kPrompt + 2;
     std::vector<CacheView> views;
     std::vector<std::uint32_t> lens(nb, ctx);
@@ -321,6 +392,7 @@ int main(int argc, char** argv) {
     }
 
     const double copy_bytes = 2.0 * static_cast<double>(copies.size()) * dev.block_stride();
+    const double row_bytes = 2.0 * 2.0 * static_cast<double>(nb) * row_elems * 2;  // read + write, K and V
     const double per_token = static_cast<double>(kHkv) * kD * 2 * 2;
     const double logical = static_cast<double>(nb) * ctx * per_token;
     // Distinct cached tokens: each prompt's 2048 shared ones, and per branch
@@ -329,15 +401,16 @@ int main(int argc, char** argv) {
     const double qo = static_cast<double>(nb) * kHq * kD * 2 * 2;
     std::printf(
         "{\"mode\": \"config4_cow\", \"layers\": %u, \"prompts\": %u, \"branches_per_prompt\": %u, \"cow_pairs\": %zu, "
-        "\"pending_before_flush\": %zu, \"copy_launches\": %llu, \"copy_us_median\": %.3f, \"copy_read_plus_write_GBps\": "
-        "%.1f, \"frames_equal_host_allocator\": %s, \"copies_equal_source\": %s, \"decode_branches\": %u, "
+        "\"pending_after_append\": %zu, \"copy_launches\": %llu, \"copy_append_us_median\": %.3f, "
+        "\"copy_append_read_plus_write_GBps\": %.1f, \"copy_us_median\": %.3f, \"copy_then_append_us_median\": %.3f, "
+        "\"frames_equal_host_allocator\": %s, \"copies_equal_source_plus_rows\": %s, \"decode_branches\": %u, "
         "\"decode_ctx\": %u, \"step_us_median\": %.3f, \"pipelined_step_us\": %.3f, \"pack_ahead_step_us\": %.3f, "
         "\"host_us_per_step\": %.3f, \"pack_ahead_host_us_per_step\": %.3f, \"pipelined_over_kernel\": %.4f, "
         "\"pack_ahead_over_kernel\": %.4f, \"decode_us_median\": %.3f, \"decode_logical_GBps\": %.1f, \"decode_unique_GBps\": "
         "%.1f, \"decode_tokens_per_s\": %.1f, \"checked_elements\": %zu, \"worst_excess_over_tolerance\": %.3g, "
         "\"decode_within_tolerance\": %s}\n",
-        layers, prompts, branches, copies.size(), pending, static_cast<unsigned long long>(copy_launches), copy_ms * 1e3,
-        copy_bytes / (copy_ms * 1e-3) / 1e9, frames_equal ? "true" : "false", copies_equal ? "true" : "false", nb,
+        layers, prompts, branches, copies.size(), pending, static_cast<unsigned long long>(copy_launches), fused_us,
+        (copy_bytes + row_bytes) / (fused_us * 1e-6) / 1e9, copy_us, two_launch_us, frames_equal ? "true" : "false", copies_equal ? "true" : "false", nb,
         ctx, step_ms * 1e3, piped.loop.gpu_us_per_step, piped.ahead.gpu_us_per_step, piped.loop.host_us_per_step,
         piped.ahead.host_us_per_step, piped.loop.gpu_us_per_step / (decode_ms * 1e3),
         piped.ahead.gpu_us_per_step / (decode_ms * 1e3), decode_ms * 1e3, (logical + qo) / (decode_ms * 1e-3) / 1e9,
@@ -345,6 +418,8 @@ int main(int argc, char** argv) {
         nb / (decode_ms * 1e-3), checked, worst, worst <= 0.0 ? "true" : "false");
     (void)qvp_free(dq);
     (void)qvp_free(dout);
+    (void)qvp_free(dk);
+    (void)qvp_free(dv);
     (void)qvp_event_destroy(e0);
     (void)qvp_event_destroy(e1);
     return (frames_equal && copies_equal && worst <= 0.0) ? 0 : 2;

@@ -9,8 +9,10 @@
 // KVAppendBatch does the same for a whole step: the copy-on-write decisions on
 // the host, then, for device-placed frames, one launch of the stores
 // (qvp_append_kv) on the allocator's engine stream, ordered after the step's
-// queued block copies and before any later decode on that stream. For
-// host-placed frames the stores are memcpy calls, as in the harnesses.
+// queued block copies and before any later decode on that stream. A decode
+// step's copies (up to 128, with up to 128 tokens, none written into a frame
+// a copy reads) run in that same launch (qvp_copy_append_kv). For host-placed
+// frames the stores are memcpy calls, as in the harnesses.
 
 #include "qwenvl_paged/KVCacheManager.h"
 #include "qwenvl_paged/MemoryAllocator.h"
@@ -49,6 +51,8 @@ private:
 
     std::vector<std::uint32_t> frames_;
     std::vector<std::uint32_t> slots_;
+    std::vector<PhysicalBlockId> cow_src_;  // the step's copies run in the append's launch
+    std::vector<PhysicalBlockId> cow_dst_;
     std::string last_error_;
 };
 

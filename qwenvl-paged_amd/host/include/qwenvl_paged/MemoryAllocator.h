@@ -111,6 +111,14 @@ public:
     [[nodiscard]] std::size_t block_stride() const noexcept;
     // Runs every queued device operation in order; false on a device error.
     bool flush();
+    // flush(), except that a last batch of copies -- at most max_pairs, none
+    // reading a frame listed in `written` -- is not launched but handed to the
+    // caller (sources in src, destinations in dst, empty when there is none)
+    // to run in its own launch on the engine stream, which is already ordered
+    // after any swap touching those frames. The handed-out batch counts in
+    // copy_launches().
+    bool flush_except_last_copies(std::size_t max_pairs, const std::vector<PhysicalBlockId>& written,
+                                  std::vector<PhysicalBlockId>& src, std::vector<PhysicalBlockId>& dst);
     // Operations queued and not yet flushed.
     [[nodiscard]] std::size_t pending_operations() const noexcept;
     // Launches issued by flush() so far, by kind (copy, gather, scatter).
@@ -162,6 +170,9 @@ private:
 
     bool fail(const std::string& what);
     bool run_batch(OpKind kind, const std::vector<DeviceOp>& ops);
+    // flush() with an optional hand-out of the last copy batch.
+    bool flush_queue(std::size_t max_pairs, const std::vector<PhysicalBlockId>* written,
+                     std::vector<PhysicalBlockId>* src, std::vector<PhysicalBlockId>* dst);
     void set_ref_count(PhysicalBlockInfo& info, std::uint32_t count) noexcept;
     // Makes the engine stream wait for the swap batches the frames depend on.
     bool order_engine_after_swaps(const PhysicalBlockId* frames, std::size_t n, bool writes);

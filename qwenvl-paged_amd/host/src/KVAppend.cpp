@@ -11,6 +11,18 @@
 
 namespace qwenvl_paged {
 
+namespace {
+
+// Limits of qvp_copy_append_kv (one decode step): list lengths, tokens per
+// block and the frame stride.
+constexpr std::size_t kFusedCopyLimit = 128;
+constexpr std::size_t kFusedRowLimit = 128;
+constexpr std::uint32_t kFusedSlotLimit = 64;
+constexpr std::uint64_t kFusedStrideLimit = 0x80000000ull - 8192;
+
+}  // namespace
+
+
 bool KVAppendBatch::fail(std::string msg) {
     last_error_ = std::move(msg);
     return false;
@@ -103,10 +115,27 @@ bool KVAppendBatch::append(KVCacheManager& cache, MemoryAllocator& allocator, co
     }
 
     // The copies ensure_token_writable queued run first, on the same stream,
-    // and the frames written here wait for any swap still moving them.
-    if (!allocator.flush() || !allocator.order_frame_writes(frames_)) {
+    // and the frames written here wait for any swap still moving them. A
+    // step's copies (the last queued batch, when no token row goes into a
+    // frame one of them reads) run in the append's own launch: each chunk of a
+    // destination frame is copied and then overwritten by its rows by one
+    // workgroup, so the bytes equal those of the two launches in order.
+    const std::uint64_t align = reinterpret_cast<std::uintptr_t>(allocator.device_base()) |
+                                reinterpret_cast<std::uintptr_t>(k) | reinterpret_cast<std::uintptr_t>(v) |
+                                allocator.block_stride() | row | layout.head_stride() * bpe |
+                                layout.token_stride() * bpe | layout.stream_stride() * bpe |
+                                layout.layer_stride() * bpe;
+    const bool fuse = frames_.size() <= kFusedRowLimit && align % 16 == 0 &&
+                      shape.tokens_per_block <= kFusedSlotLimit && allocator.block_stride() <= kFusedStrideLimit;
+    if (fuse ? !allocator.flush_except_last_copies(kFusedCopyLimit, frames_, cow_src_, cow_dst_)
+             : !allocator.flush()) {
         return fail("flush: " + allocator.last_error());
     }
+    if (!fuse) {
+        cow_src_.clear();
+        cow_dst_.clear();
+    }
+    if (!allocator.order_frame_writes(frames_)) return fail("flush: " + allocator.last_error());
     qvp_append_args a{};
     a.kv_base = allocator.device_base();
     a.block_stride = allocator.block_stride();
@@ -124,6 +153,14 @@ bool KVAppendBatch::append(KVCacheManager& cache, MemoryAllocator& allocator, co
     a.layer_stride = layout.layer_stride();
     a.k = k;
     a.v = v;
+    if (!cow_src_.empty()) {
+        if (qvp_copy_append_kv(&a, cow_src_.data(), cow_dst_.data(), static_cast<std::uint32_t>(cow_src_.size()),
+                               allocator.block_stride(), frames_.data(), slots_.data(),
+                               static_cast<std::uint32_t>(frames_.size()), allocator.stream()) != QVP_OK) {
+            return fail(std::string("copy + append: ") + qvp_last_error());
+        }
+        return true;
+    }
     if (qvp_append_kv(&a, frames_.data(), slots_.data(), static_cast<std::uint32_t>(frames_.size()),
                       allocator.stream()) != QVP_OK) {
         return fail(std::string("append: ") + qvp_last_error());

@@ -351,7 +351,17 @@ bool MemoryAllocator::order_frame_writes(const std::vector<PhysicalBlockId>& fra
     return order_engine_after_swaps(frames.data(), frames.size(), true);
 }
 
-bool MemoryAllocator::flush() {
+bool MemoryAllocator::flush() { return flush_queue(0, nullptr, nullptr, nullptr); }
+
+bool MemoryAllocator::flush_except_last_copies(std::size_t max_pairs, const std::vector<PhysicalBlockId>& written,
+                                               std::vector<PhysicalBlockId>& src, std::vector<PhysicalBlockId>& dst) {
+    src.clear();
+    dst.clear();
+    return flush_queue(max_pairs, &written, &src, &dst);
+}
+
+bool MemoryAllocator::flush_queue(std::size_t max_pairs, const std::vector<PhysicalBlockId>* written,
+                                  std::vector<PhysicalBlockId>* src, std::vector<PhysicalBlockId>* dst) {
     if (config_.placement != BlockPlacement::Device) return true;
     if (!ok_) {
         queue_.clear();
@@ -391,6 +401,20 @@ bool MemoryAllocator::flush() {
                 regions.push_back(op.offset);
             } else {
                 writes.insert(op.frame_a);
+            }
+        }
+        if (src != nullptr && kind == OpKind::Copy && i == queue_.size() && batch.size() <= max_pairs) {
+            bool reads_written = false;
+            for (PhysicalBlockId w : *written) reads_written = reads_written || reads.count(w) != 0;
+            if (!reads_written) {
+                for (const DeviceOp& op : batch) {
+                    src->push_back(op.frame_a);
+                    dst->push_back(op.frame_b);
+                }
+                good = order_engine_after_swaps(src->data(), src->size(), false) &&
+                       order_engine_after_swaps(dst->data(), dst->size(), true);
+                if (good) ++copy_launches_;
+                break;
             }
         }
         if (!run_batch(kind, batch)) {

@@ -215,6 +215,8 @@ SIGNATURES = {
         [c_void_p, c_uint64, c_uint32, _u32p, _u64p, c_uint32, c_void_p, c_uint64, c_uint64, c_void_p],
     ),
     "qvp_append_kv": (c_int, [POINTER(AppendArgs), _u32p, _u32p, c_uint32, c_void_p]),
+    "qvp_copy_append_kv": (c_int, [POINTER(AppendArgs), _u32p, _u32p, c_uint32, c_uint64, _u32p, _u32p, c_uint32,
+                                   c_void_p]),
     "qvp_paged_prefill": (c_int, [POINTER(PrefillArgs), c_void_p]),
     "qvp_graph_begin_capture": (c_int, [c_void_p]),
     "qvp_graph_end_capture": (c_int, [c_void_p, POINTER(c_void_p)]),
@@ -711,6 +713,18 @@ def append_kv(args: AppendArgs, frames, slots, stream=None) -> None:
     if len(f_a) != len(s_a):
         raise ValueError("frames and slots differ in length")
     check(load().qvp_append_kv(byref(args), f_p, s_p, len(f_a), _sp(stream)))
+
+
+def copy_append_kv(args: AppendArgs, src, dst, copy_bytes: int, frames, slots, stream=None) -> None:
+    """A copy-on-write step in one launch (qvp_copy_append_kv): copy_blocks(src, dst, copy_bytes) then
+    append_kv(frames, slots) on the pool args describes."""
+    s_a, s_p = _u32(src)
+    d_a, d_p = _u32(dst)
+    f_a, f_p = _u32(frames)
+    t_a, t_p = _u32(slots)
+    if len(s_a) != len(d_a) or len(f_a) != len(t_a):
+        raise ValueError("src/dst or frames/slots differ in length")
+    check(load().qvp_copy_append_kv(byref(args), s_p, d_p, len(s_a), copy_bytes, f_p, t_p, len(f_a), _sp(stream)))
 
 
 def prefill_args(*, query: int, out: int, kv_base: int, block_stride: int, batch: "Batch", q_start, kv_dtype: int,

@@ -234,3 +234,55 @@ TEST(KVAppendTest, DecodeSeesEveryTokenTheBatchAppended) {
     const PhysicalBlockId shared = *dev.cache.cache_view(1)->block_table->lookup(0);
     for (SequenceId b : {2, 3}) EXPECT_EQ(*dev.cache.cache_view(b)->block_table->lookup(0), shared);
 }
+
+TEST(KVAppendTest, StepCopiesJoinTheAppendLaunchUnlessARowGoesIntoACopySource) {
+    // Forks whose next token lands in the block they share with their parent:
+    // every fork's copy runs inside the append's own launch (one copy launch
+    // counted, nothing left queued). In the second form the parent writes into
+    // the shared frame in the same step as its forks copy it -- a row into a
+    // copy's source -- and the copies run first, as their own launch. Both
+    // forms end byte for byte where host frames (memcpy) end.
+    for (const bool parent_writes : {false, true}) {
+        const BlockShape shape = shape_of(4, 2, 2, 8, 2);
+        constexpr std::uint32_t kFrames = 24;
+        HostHarness host(shape, kFrames);
+        DeviceHarness dev(shape, kFrames);
+        ASSERT_TRUE(dev.ready());
+        std::vector<std::uint8_t> fill(shape.byte_size());
+        for (PhysicalBlockId f = 0; f < kFrames; ++f) {
+            for (std::size_t i = 0; i < fill.size(); ++i) fill[i] = static_cast<std::uint8_t>((i * 13 + f * 29) % 251);
+            ASSERT_TRUE(host.allocator.write_block_bytes(f, 0, fill.data(), fill.size()));
+            ASSERT_TRUE(dev.allocator.write_block_bytes(f, 0, fill.data(), fill.size()));
+        }
+        for (auto* cache : {&host.cache, &dev.cache}) {
+            ASSERT_TRUE(cache->create_sequence(SequenceMetadata{1, 1, {}, {}}));
+            ASSERT_TRUE(cache->reserve_tokens(1, 6));  // block 1 holds tokens 4, 5 and room for 6, 7
+            for (SequenceId b : {2, 3, 4}) ASSERT_TRUE(cache->fork_sequence(1, SequenceMetadata{b, 1, {}, {}}));
+        }
+        std::vector<SequenceId> seqs{2, 3, 4};
+        std::vector<TokenPosition> pos{6, 6, 6};
+        if (parent_writes) {
+            seqs.push_back(1);
+            pos.push_back(6);
+        }
+        const auto hk = rows(seqs.size(), 2, shape, 3, 0);
+        const auto hv = rows(seqs.size(), 2, shape, 3, 1);
+        DeviceRows d(hk, hv);
+        ASSERT_NE(d.k, nullptr);
+        KVAppendBatch host_batch, dev_batch;
+        const std::uint64_t launches = dev.allocator.copy_launches();
+        ASSERT_TRUE(host_batch.append(host.cache, host.allocator, seqs, pos, 0, 2, hk.data(), hv.data()))
+            << host_batch.last_error();
+        ASSERT_TRUE(dev_batch.append(dev.cache, dev.allocator, seqs, pos, 0, 2, d.k, d.v)) << dev_batch.last_error();
+        EXPECT_EQ(dev.allocator.pending_operations(), 0u);
+        EXPECT_EQ(dev.allocator.copy_launches() - launches, 1u) << "parent_writes " << parent_writes;
+        ASSERT_TRUE(dev.allocator.synchronize());
+        for (PhysicalBlockId f = 0; f < kFrames; ++f) {
+            ASSERT_EQ(frame_bytes(dev.allocator, f), frame_bytes(host.allocator, f))
+                << "parent_writes " << parent_writes << " frame " << f;
+        }
+        // The forks own their tail frames now; the parent keeps the original.
+        const PhysicalBlockId tail = *dev.cache.cache_view(1)->block_table->lookup(1);
+        for (SequenceId b : {2, 3, 4}) EXPECT_NE(*dev.cache.cache_view(b)->block_table->lookup(1), tail);
+    }
+}

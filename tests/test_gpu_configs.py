@@ -43,13 +43,16 @@ def run(name: str, *args: str) -> dict:
 @pytest.mark.parametrize("layers", [1, 28])
 def test_copy_on_write_configuration_full_size(layers):
     """config4 as specified: 16 prompts x 8 branches, 128 copy-on-write pairs
-    in one batched copy, decode over the 128 branches; with one layer per frame
-    and with whole 28-layer Qwen2-VL-7B frames (917,504 B copies)."""
+    and the branches' 128 new tokens in one launch (KVAppendBatch), decode over
+    the 128 branches; with one layer per frame and with whole 28-layer
+    Qwen2-VL-7B frames (917,504 B copies). The device pool after the step
+    equals the host-placement allocator's (memcpy copies, then memcpy rows)
+    byte for byte."""
     r = run("cow_bench", "--layers", str(layers), "--reps", "5")
     assert r["layers"] == layers and r["cow_pairs"] == 128
-    assert r["pending_before_flush"] == 128
+    assert r["pending_after_append"] == 0
     assert r["copy_launches"] == 1
-    assert r["frames_equal_host_allocator"] and r["copies_equal_source"]
+    assert r["frames_equal_host_allocator"] and r["copies_equal_source_plus_rows"]
     assert r["decode_within_tolerance"] and r["checked_elements"] > 0
 
 

@@ -1,8 +1,8 @@
 """qvp_paged_decode_noalloc (the decode on the library's fixed device scratch
 array, for callers that cannot allocate) against qvp_paged_decode: the same
 bits on two calls in a row, the second with a smaller batch, on the bf16 MFMA
-kernel and on the generic kernel; refusals leave the output untouched; the
-calls change no device memory accounting."""
+kernel and on the split kernels (fp32 and generic); refusals leave the output
+untouched; the calls change no device memory accounting."""
 
 from __future__ import annotations
 
@@ -88,13 +88,20 @@ def test_noalloc_matches_the_allocating_decode_on_two_calls_the_second_smaller()
         assert_close_bf16(got, ref32, f"noalloc call {i + 1}")
 
 
-def test_noalloc_on_the_split_kernels_two_calls_the_second_smaller():
+@pytest.mark.parametrize("kernel", ["f32_grouped", "generic"])
+def test_noalloc_on_the_split_kernels_two_calls_the_second_smaller(kernel):
+    # fp32 caches with a negative scale take the fp32 split kernel (the
+    # persistent decode takes positive scales); head_dim 64 takes the generic
+    # split kernel.
     for i, lens in enumerate(([37, 600, 1500, 4096, 129, 2049], [90, 700])):
-        print(f"case: noalloc generic call {i + 1}, lens={lens}", flush=True)
-        w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=40 + i, kv_sigma=1.0)
+        print(f"case: noalloc {kernel} call {i + 1}, lens={lens}", flush=True)
+        if kernel == "f32_grouped":
+            w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=40 + i, kv_sigma=1.0, scale=-0.0625)
+        else:
+            w = W.custom(lens, 28, 4, 64, seed=50 + i)
         run = GpuRun(w)
         ref, got = _both(run, hinted=False)
-        assert run.batch.decode_plan()["kernel"] == "f32_grouped"
+        assert run.batch.decode_plan()["kernel"] == kernel
         assert np.array_equal(ref.view(np.uint32), got.view(np.uint32)), f"call {i + 1} differs"
 
 
