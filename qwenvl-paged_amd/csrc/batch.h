@@ -16,19 +16,22 @@ struct qvp_piece {
 };
 
 // A shared-prefix work item of the persistent decode: tiles [t0, t1) of kv
-// head g for nmem sequences whose block tables hold the same frames over
-// those tiles (member b[0]'s table supplies them), decoded once for all of
-// them. Member m's partial result goes to workspace slot slot[m] of its
-// (sequence, kv head) segment of nslots[m] slots, whose completion counter
-// is counters[seg_slot0[m]]. The segment's other slots are the other chunks
-// of the prefix and its private suffix: a short suffix is one entry of the
-// prefix launch's suffix list (a qvp_piece, one wave each), a longer one is
-// made of ordinary pieces of the main decode launch.
+// head g for the nmem sequences of one MFMA column block whose block tables
+// hold the same frames over those tiles (member b[0]'s table supplies them),
+// decoded once for all of them; member m's own tiles [t1, sfx_t1[m]) (a short
+// private suffix, context ctx[m]) run in the item too. With slot[m] = -1 the
+// item completes member m's (sequence, kv head) segment and writes its
+// output; otherwise its partial result goes to workspace slot slot[m] of the
+// segment's nslots[m] slots, whose completion counter is
+// counters[seg_slot0[m]]. The segment's other slots are the prefix's other
+// chunks and, for a long private suffix, ordinary pieces of the main launch.
 constexpr int kPrefixMaxMembers = 8;
 struct qvp_prefix_item {
     int32_t g, t0, t1, nmem;
     int32_t b[kPrefixMaxMembers];
-    int32_t slot[kPrefixMaxMembers];
+    int32_t ctx[kPrefixMaxMembers];
+    int32_t sfx_t1[kPrefixMaxMembers];  // end of the member's private tiles run by the item (t1: none)
+    int32_t slot[kPrefixMaxMembers];    // -1: the item completes the member's segment
     int32_t seg_slot0[kPrefixMaxMembers];
     int32_t nslots[kPrefixMaxMembers];
 };

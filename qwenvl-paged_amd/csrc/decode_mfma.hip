@@ -215,6 +215,43 @@ __device__ inline void load_tile(const DecodeGeometry& p, const TileRef& r, int 
     }
 }
 
+// load_tile through buffer resources, for kernels bound by their vector ALU
+// (the shared-prefix launch): a half tile's frame address is uniform and goes
+// into the resource (SGPRs), the lane's part of each address is fixed for the
+// kernel and goes into voffset, and the half tile's token offset into
+// soffset -- no per-load 64-bit address arithmetic. With tiles starting on
+// 16-token boundaries and tokens_per_block a power of two >= 16, token
+// 32t + 16u + x (x < 16) sits at slot ((32t + 16u) mod tpb) + x of its frame.
+// lane_k = ((c >> 2) + 4 (c & 3)) token_stride + 16 j and lane_v =
+// j token_stride + 16 c are the fixed lane offsets of load_tile's K and V rows.
+constexpr int kBufferWord3Raw = 0x00020000;  // word 3 of a raw buffer resource on gfx9 parts
+
+__device__ inline void load_tile_buffer(const DecodeGeometry& p, const TileRef& r, uint32_t lane_k, uint32_t lane_v,
+                                        KvTile& tile) {
+    const uint32_t tmask = p.tpb - 1;
+    const int tok0 = r.t * kTileTokens;
+    const uint8_t* head_base = p.kv_base + static_cast<uint64_t>(r.g) * p.head_stride;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        uint8_t* frame = const_cast<uint8_t*>(head_base + static_cast<uint64_t>(u == 0 ? r.blk0 : r.blk1) * p.block_stride);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(frame, 0, 0x7fffffff, kBufferWord3Raw);
+        const uint32_t tok = static_cast<uint32_t>((tok0 + 16 * u) & tmask) * static_cast<uint32_t>(p.token_stride);
+        const int koff = static_cast<int>(static_cast<uint32_t>(p.k_off) + tok);
+        const int voff = static_cast<int>(static_cast<uint32_t>(p.v_off) + tok);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            tile.k[u][i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(lane_k + 64u * i), koff, 0));
+        }
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+            tile.v[4 * u + qq] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           rs, static_cast<int>(lane_v), voff + static_cast<int>(4u * qq * p.token_stride), 0));
+        }
+    }
+}
+
 // kVG = 0: matrix-core tiles; 1, 2: vector tiles for query groups up to kVG.
 // kElem: the cache's element type (kElemBf16, kElemF16, kElemF32); fp16 and
 // fp32 caches run matrix-core tiles only.
@@ -657,19 +694,13 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_mfma_persistent(De
     }
 }
 
-// Dynamic LDS of the shared-prefix launch: one 32-token tile (16 KiB) per wave.
-constexpr uint32_t kPrefixLdsBytes = kWaves * 16 * 64 * sizeof(u32x4);
-static_assert(kWaves * 16 * kRowPad * sizeof(float) <= kPrefixLdsBytes, "lane merge reuses the tile slots");
-
 struct PrefixArgs {
     const qvp_prefix_item* items;
-    const qvp_piece* suffix;  // short private suffixes, eight per workgroup after the items
     int32_t* counters;
     float* ws_ml;   // the main launch's workspace layout: [slot][group][2]
     float* ws_acc;  // [slot][group][128]
     void* out;
     int num_items;
-    int num_suffix;
 };
 
 // Segments the prefix launch completes hold only its own slots: the prefix
@@ -750,192 +781,127 @@ __device__ void merge_prefix_segments(const DecodeGeometry& p, const PrefixArgs&
     }
 }
 
-// Shared-prefix launch: one workgroup per work item (tiles [t0, t1) of kv
-// head g shared by up to eight sequences). The eight waves are four column
-// blocks x two tile lanes: column block k holds sequences k * (16 / G) ..
-// in its MFMA columns (G query heads each), and the two tile lanes take the
-// item's tiles in steps of eight: each wave fetches one tile of the step and
-// copies it to LDS, where the other column blocks read it. The tiles are whole (the
-// prefix ends before every member's last tile), so no mask applies. At the
-// end the two lanes of each column block merge through LDS and every member's
-// (m, l, O) goes to its slot with agent-scope stores; after they have
-// completed, one increment per member counts the chunk into its segment.
-// Workgroups after the items decode short private suffixes, one segment per
-// wave (tiles [t0, t1) of the member's own frames, masked at its context
-// end), and count them in the same way. The workgroup whose increment
-// completes a segment merges it and writes the output; a segment with a long
-// suffix is completed by its pieces in the main launch, later on the stream.
+// Shared-prefix launch: one workgroup per item -- kv head g of a prefix
+// group, one MFMA column block of its members (up to 16 / G sequences of G
+// query heads, column c = member c / G, head c % G; columns past the last
+// member repeat it and are never stored), shared tiles [t0, t1) of one chunk
+// of the prefix. An item of the prefix's last chunk also runs its members'
+// short private suffixes (member m's tiles [t1, sfx_t1[m]) from its own
+// frames, the other members' columns masked). The items of one (group, kv
+// head, chunk) differ only in their columns and read the same tiles; the
+// planner numbers them so the dispatcher puts them on one XCD, where all but
+// the first read of a tile come from L2. Each wave streams every eighth tile
+// with the next one in flight and the frames of the one after resolved, like
+// the persistent decode, reading them through buffer
+// resources (load_tile_buffer: the kernel is bound by its vector ALU); the
+// eight waves merge through LDS. A member whose segment the item completes (one chunk, short
+// suffix) gets its output written here; otherwise the item's (m, l, O) goes to
+// the member's slot and counts in (agent-scope stores, then, after they have
+// completed, one increment per member), and the workgroup completing a
+// segment merges it -- or the persistent decode does, later on the stream,
+// for a member with a long suffix.
 template <typename OutT>
-__global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(DecodeGeometry p, PrefixArgs a) {
+__global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_columns(DecodeGeometry p, PrefixArgs a) {
     __shared__ float sm_m[kWaves][16];
     __shared__ float sm_l[kWaves][16];
-    __shared__ int sm_seg[kWaves][4];
+    __shared__ float sm_o[kWaves][16][kRowPad];
+    __shared__ int sm_seg[kPrefixMaxMembers][4];
     __shared__ int sm_nseg;
-    // One tile per wave, [wave][register][lane] (kPrefixLdsBytes), reused for
-    // the lanes' merge once the tiles are done.
-    extern __shared__ u32x4 sm_tiles[];
-    float(&sm_o)[kWaves][16][kRowPad] = *reinterpret_cast<float(*)[kWaves][16][kRowPad]>(sm_tiles);
-    if (static_cast<int>(blockIdx.x) >= a.num_items) {
-        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-        const int lane = threadIdx.x & 63;
-        const int c = lane & 15;
-        const int j = lane >> 4;
-        const int G = static_cast<int>(p.group);
-        const int e = (static_cast<int>(blockIdx.x) - a.num_items) * kWaves + wave;
-        const bool have = e < a.num_suffix;
-        qvp_piece d{};
-        if (have) {
-            d = piece_at(a.suffix, e);
-            const uint16_t* qp = static_cast<const uint16_t*>(p.query) +
-                                 (static_cast<uint64_t>(d.b) * p.num_q_heads + d.g * G + min(c, G - 1)) * kD;
-            u32x4 qop[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i + 8 * j);
-            const auto* row = as_const(p.tables) + static_cast<uint64_t>(d.b) * p.max_nb;
-            auto sref = [&](int t) {
-                TileRef r{};
-                r.b = d.b;
-                r.g = d.g;
-                r.t = t;
-                r.ctx = d.ctx;
-                r.blk0 = row[min(t * kTileTokens, d.ctx - 1) >> p.tpb_shift];
-                r.blk1 = row[min(t * kTileTokens + 16, d.ctx - 1) >> p.tpb_shift];
-                return r;
-            };
-            floatx4 o[8];
-#pragma unroll
-            for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-            float m_run = -INFINITY;
-            float l_run = 0.f;
-            KvTile nxt;
-            TileRef r2{};
-            load_tile<false>(p, sref(d.t0), c, j, nxt);
-            if (d.t0 + 1 < d.t1) r2 = sref(d.t0 + 1);
-            for (int t = d.t0; t < d.t1; ++t) {
-                KvTile cur = nxt;
-                if (t + 1 < d.t1) load_tile<false>(p, r2, c, j, nxt);
-                if (t + 2 < d.t1) r2 = sref(t + 2);
-                compute_tile(cur, qop, t * kTileTokens, d.ctx - 1, d.ctx, p.scale_log2, j, m_run, l_run, o);
-            }
-            l_run = sum_over_j(l_run);
-            if (c < G) {
-                const uint64_t ri = static_cast<uint64_t>(d.slot) * G + c;
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int n = 0; n < 8; ++n) {
-                        __hip_atomic_store(&a.ws_acc[ri * kD + 32 * j + 8 * r + n], o[n][r], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                if (j == 0) {
-                    __hip_atomic_store(&a.ws_ml[ri * 2 + 0], m_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(&a.ws_ml[ri * 2 + 1], l_run, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-        }
-        // Every wave's slot stores have completed before any segment is counted.
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        if (threadIdx.x == 0) sm_nseg = 0;
-        __syncthreads();
-        if (have && lane == 0) {
-            const int done = __hip_atomic_fetch_add(&a.counters[d.seg_slot0], 1, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-            if (done == d.seg_nslots - 1) {
-                const int at = __hip_atomic_fetch_add(&sm_nseg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                sm_seg[at][0] = d.b;
-                sm_seg[at][1] = d.g;
-                sm_seg[at][2] = d.seg_slot0;
-                sm_seg[at][3] = d.seg_nslots;
-            }
-        }
-        __syncthreads();
-        const int nseg = __builtin_amdgcn_readfirstlane(sm_nseg);
-        if (nseg > 0) merge_prefix_segments<OutT>(p, a, nseg, sm_seg);
-        return;
-    }
     const auto* it = as_const(a.items) + blockIdx.x;
     const int gq = it->g;
     const int t0 = it->t0;
     const int t1 = it->t1;
     const int nmem = it->nmem;
-    const int b0 = it->b[0];
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int lane = threadIdx.x & 63;
     const int c = lane & 15;
     const int j = lane >> 4;
     const int G = static_cast<int>(p.group);
-    const int mpb = 16 / G;   // sequences per column block
-    const int ncol = mpb * G;
-    const int cb = wave & 3;  // column block
-    const int tl = wave >> 2; // tile lane
-    // Column c: sequence cb * mpb + c / G, query head c % G of kv head gq;
-    // columns past the block's last sequence repeat it and are never stored.
+    const int ncol = nmem * G;
     const int cc = min(c, ncol - 1);
-    const int mem = min(cb * mpb + cc / G, nmem - 1);
-    const int bq = as_const(a.items)[blockIdx.x].b[mem];
-    const uint16_t* qp = static_cast<const uint16_t*>(p.query) +
-                         (static_cast<uint64_t>(bq) * p.num_q_heads + gq * G + cc % G) * kD;
+    const int mem = cc / G;
     u32x4 qop[4];
+    {
+        const uint16_t* qp = static_cast<const uint16_t*>(p.query) +
+                             (static_cast<uint64_t>(it->b[mem]) * p.num_q_heads + gq * G + cc % G) * kD;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i + 8 * j);
+        for (int i = 0; i < 4; ++i) qop[i] = *reinterpret_cast<const u32x4*>(qp + 32 * i + 8 * j);
+    }
 
-    const auto* row = as_const(p.tables) + static_cast<uint64_t>(b0) * p.max_nb;
-    auto ref = [&](int t) {
+    // The item's tiles, numbered: shared tiles t0 .. t1 - 1, then the suffix
+    // tiles member by member; wave w takes numbers w, w + kWaves, ... (a fixed
+    // assignment: the waves' merge then adds the same partial results in the
+    // same order on every launch, so the output repeats bit for bit).
+    const int nshared = t1 - t0;
+    int total = nshared;
+    for (int m = 0; m < nmem; ++m) total += it->sfx_t1[m] - t1;
+    // Tile k: its frames, and for a suffix tile the member (-1: a shared
+    // tile, every column sees it).
+    const auto* row0 = as_const(p.tables) + static_cast<uint64_t>(it->b[0]) * p.max_nb;
+    auto tile_of = [&](int k, int& member) {
         TileRef r{};
-        r.b = b0;
         r.g = gq;
-        r.t = t;
-        r.ctx = t1 * kTileTokens;
-        r.blk0 = row[(t * kTileTokens) >> p.tpb_shift];
-        r.blk1 = row[(t * kTileTokens + 16) >> p.tpb_shift];
+        if (k < nshared) {
+            member = -1;
+            r.b = it->b[0];
+            r.t = t0 + k;
+            r.ctx = t1 * kTileTokens;
+            r.blk0 = row0[(r.t * kTileTokens) >> p.tpb_shift];
+            r.blk1 = row0[(r.t * kTileTokens + 16) >> p.tpb_shift];
+            return r;
+        }
+        int e = k - nshared;
+        member = 0;
+        while (member + 1 < nmem && e >= it->sfx_t1[member] - t1) {
+            e -= it->sfx_t1[member] - t1;
+            ++member;
+        }
+        r.t = t1 + e;
+        r.b = it->b[member];
+        r.ctx = it->ctx[member];
+        const auto* row = as_const(p.tables) + static_cast<uint64_t>(r.b) * p.max_nb;
+        r.blk0 = row[min(r.t * kTileTokens, r.ctx - 1) >> p.tpb_shift];
+        r.blk1 = row[min(r.t * kTileTokens + 16, r.ctx - 1) >> p.tpb_shift];
         return r;
     };
+
     floatx4 o[8];
 #pragma unroll
     for (int n = 0; n < 8; ++n) o[n] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY;
     float l_run = 0.f;
-    const int end_tok = t1 * kTileTokens;
-    // Steps of eight tiles: wave w fetches tile w of the step (one tile in
-    // flight per wave, the frames of its next one resolved meanwhile) and
-    // copies it to its LDS slot; wave (cb, tl) then runs tiles 4 tl .. 4 tl + 3
-    // of the step for its column block, its own from registers first and the
-    // other three from LDS. Each tile is read from HBM once, with eight
-    // distinct tiles in flight per workgroup.
+    const uint32_t lane_k = static_cast<uint32_t>((c >> 2) + 4 * (c & 3)) * static_cast<uint32_t>(p.token_stride) + 16u * j;
+    const uint32_t lane_v = static_cast<uint32_t>(j) * static_cast<uint32_t>(p.token_stride) + 16u * c;
     KvTile nxt;
-    TileRef r2{};
-    if (t0 + wave < t1) load_tile<false>(p, ref(t0 + wave), c, j, nxt);
-    if (t0 + kWaves + wave < t1) r2 = ref(t0 + kWaves + wave);
-    u32x4* const my_slot = sm_tiles + wave * 16 * 64 + lane;
-    for (int s0 = t0; s0 < t1; s0 += kWaves) {
-        const int tw = s0 + wave;
-        KvTile cur;
-        if (tw < t1) {
-            cur = nxt;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) my_slot[r * 64] = cur.k[r >> 2][r & 3];
-#pragma unroll
-            for (int r = 0; r < 8; ++r) my_slot[(8 + r) * 64] = cur.v[r];
-        }
-        if (tw + kWaves < t1) load_tile<false>(p, r2, c, j, nxt);
-        if (tw + 2 * kWaves < t1) r2 = ref(tw + 2 * kWaves);
-        lds_barrier();
-#pragma unroll 1
-        for (int x = 0; x < 4; ++x) {
-            const int k = 4 * tl + ((cb + x) & 3);
-            const int t = s0 + k;
-            if (t >= t1) continue;
-            if (x > 0) {
-                const u32x4* src = sm_tiles + k * 16 * 64 + lane;
-#pragma unroll
-                for (int r = 0; r < 8; ++r) cur.k[r >> 2][r & 3] = src[r * 64];
-#pragma unroll
-                for (int r = 0; r < 8; ++r) cur.v[r] = src[(8 + r) * 64];
-            }
-            compute_tile(cur, qop, t * kTileTokens, end_tok - 1, end_tok, p.scale_log2, j, m_run, l_run, o);
-        }
-        lds_barrier();
+    TileRef r_nxt{}, r_after{};
+    int mem_nxt = -1, mem_after = -1;
+    int k_nxt = wave;
+    int k_after = wave + kWaves;
+    if (k_nxt < total) {
+        r_nxt = tile_of(k_nxt, mem_nxt);
+        load_tile_buffer(p, r_nxt, lane_k, lane_v, nxt);
     }
+    if (k_after < total) r_after = tile_of(k_after, mem_after);
+    while (k_nxt < total) {
+        KvTile cur = nxt;
+        const TileRef r_cur = r_nxt;
+        const int mem_cur = mem_nxt;
+        k_nxt = k_after;
+        if (k_nxt < total) {
+            load_tile_buffer(p, r_after, lane_k, lane_v, nxt);
+            r_nxt = r_after;
+            mem_nxt = mem_after;
+            k_after += kWaves;
+            if (k_after < total) r_after = tile_of(k_after, mem_after);
+        }
+        // One body for both kinds of tile (a shared tile masks nothing).
+        const int col_last = mem_cur < 0 || mem == mem_cur ? r_cur.ctx - 1 : -1;
+        compute_tile<false, true>(cur, qop, r_cur.t * kTileTokens, col_last, r_cur.ctx, p.scale_log2, j, m_run, l_run,
+                                  o);
+    }
+
+    // Merge the eight waves (a wave with no tile for a column holds -inf, 0
+    // and zeros there).
     l_run = sum_over_j(l_run);
     if (j == 0) {
         sm_m[wave][c] = m_run;
@@ -946,39 +912,52 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(Deco
 #pragma unroll
         for (int n = 0; n < 8; ++n) sm_o[wave][c][32 * j + 8 * r + n] = o[n][r];
     lds_barrier();
-    for (int e = threadIdx.x; e < 4 * 16 * kD; e += kThreads) {
-        const int blk = e >> 11;
-        const int col = (e >> 7) & 15;
+    bool counted = false;
+    for (int m = 0; m < nmem; ++m) counted = counted || it->slot[m] >= 0;
+    OutT* out = static_cast<OutT*>(a.out);
+    for (int e = threadIdx.x; e < 16 * kD; e += kThreads) {
+        const int col = e >> 7;
         const int dd = e & (kD - 1);
-        const int m = blk * mpb + col / G;
-        if (col >= ncol || m >= nmem) continue;
-        // A lane with no tile holds -inf, 0 and zeros.
-        const float m1 = sm_m[blk][col];
-        const float m2 = sm_m[blk + 4][col];
-        const float mx = fmaxf(m1, m2);
-        const float f1 = m1 == -INFINITY ? 0.f : fast_exp2(m1 - mx);
-        const float f2 = m2 == -INFINITY ? 0.f : fast_exp2(m2 - mx);
-        const float acc = sm_o[blk][col][dd] * f1 + sm_o[blk + 4][col][dd] * f2;
-        const uint64_t ri = static_cast<uint64_t>(as_const(a.items)[blockIdx.x].slot[m]) * G + col % G;
-        __hip_atomic_store(&a.ws_acc[ri * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (dd == 0) {
-            const float lsum = sm_l[blk][col] * f1 + sm_l[blk + 4][col] * f2;
-            __hip_atomic_store(&a.ws_ml[ri * 2 + 0], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.ws_ml[ri * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (col >= ncol) continue;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, sm_m[w][col]);
+        float acc = 0.f;
+        float lsum = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = sm_m[w][col];
+            const float f = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);
+            acc += sm_o[w][col][dd] * f;
+            lsum += sm_l[w][col] * f;
+        }
+        const int mm = col / G;
+        const int h = col - mm * G;
+        const int slot = it->slot[mm];
+        if (slot < 0) {
+            out[(static_cast<uint64_t>(it->b[mm]) * p.num_q_heads + gq * G + h) * kD + dd] = from_float<OutT>(acc / lsum);
+        } else {
+            const uint64_t ri = static_cast<uint64_t>(slot) * G + h;
+            __hip_atomic_store(&a.ws_acc[ri * kD + dd], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (dd == 0) {
+                __hip_atomic_store(&a.ws_ml[ri * 2 + 0], mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&a.ws_ml[ri * 2 + 1], lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
+    if (!counted) return;
     // Every wave's slot stores have completed before any member is counted.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (threadIdx.x == 0) sm_nseg = 0;
     __syncthreads();
-    if (static_cast<int>(threadIdx.x) < nmem) {
+    if (static_cast<int>(threadIdx.x) < nmem && it->slot[threadIdx.x] >= 0) {
         const int mi = static_cast<int>(threadIdx.x);
-        const int seg0 = as_const(a.items)[blockIdx.x].seg_slot0[mi];
-        const int nsl = as_const(a.items)[blockIdx.x].nslots[mi];
+        const int seg0 = it->seg_slot0[mi];
+        const int nsl = it->nslots[mi];
         const int done = __hip_atomic_fetch_add(&a.counters[seg0], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (done == nsl - 1) {
             const int at = __hip_atomic_fetch_add(&sm_nseg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            sm_seg[at][0] = as_const(a.items)[blockIdx.x].b[mi];
+            sm_seg[at][0] = it->b[mi];
             sm_seg[at][1] = gq;
             sm_seg[at][2] = seg0;
             sm_seg[at][3] = nsl;
@@ -991,7 +970,7 @@ __global__ __launch_bounds__(kThreads, kWgsPerCu) void decode_prefix_groups(Deco
 
 template <typename OutT>
 const void* prefix_kernel_for() {
-    return reinterpret_cast<const void*>(&decode_prefix_groups<OutT>);
+    return reinterpret_cast<const void*>(&decode_prefix_columns<OutT>);
 }
 
 const void* prefix_kernel(uint32_t out_dtype) {
@@ -1054,10 +1033,6 @@ int device_max_wgs(uint32_t* wgs) {
                 QVP_HIP(hipFuncSetAttribute(decode_kernel(dt, 0, el), hipFuncAttributeMaxDynamicSharedMemorySize,
                                             static_cast<int>(kMaxLdsBytes - static_lds_bytes(0))));
             }
-        }
-        for (uint32_t dt : {QVP_DTYPE_F32, QVP_DTYPE_BF16, QVP_DTYPE_F16}) {
-            QVP_HIP(hipFuncSetAttribute(prefix_kernel(dt), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        static_cast<int>(kPrefixLdsBytes)));
         }
         int cus = 0;
         QVP_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
@@ -1331,7 +1306,8 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     std::vector<PrefixGroup> groups = allow_prefix ? find_prefix_groups(in, g, hps) : std::vector<PrefixGroup>{};
     std::vector<uint32_t> start(nseq, 0);
     // A member whose private suffix is short has it decoded by the prefix
-    // launch too (one wave per segment) and leaves the main launch.
+    // launch too (in the items of the prefix's last chunk) and leaves the
+    // main launch.
     std::vector<uint8_t> short_suffix(nseq, 0);
     for (const PrefixGroup& pg : groups) {
         for (int m = 0; m < pg.nmem; ++m) {
@@ -1448,27 +1424,25 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
     const size_t nseg = static_cast<size_t>(nseq) * nq;
     std::vector<int32_t> seg_count(nseg, 0), seg_base(nseg, -1), seg_next(nseg, 0);
     for (const qvp_piece& pc : pieces) ++seg_count[static_cast<size_t>(pc.b) * nq + pc.g];
-    // A shared prefix is cut into chunks of about equal size, so that the
-    // prefix launch has about one work item per CU; each chunk is one more
-    // piece (and slot) of every member's segment, and comes first in it.
-    // The short suffixes take workgroups of the same launch, eight segments
-    // each.
-    uint64_t prefix_tiles = 0;
-    uint64_t n_suffix = 0;
+    // Prefix-launch items are (group, kv head, MFMA column block, chunk): a
+    // prefix is cut into the number of chunks of about equal size that keeps
+    // the items at about one per CU -- one chunk when the column blocks alone
+    // fill the CUs, and the items then complete their members' segments. Each
+    // chunk is one more slot of every member's segment and comes first in it;
+    // a short suffix runs in the last chunk's items.
+    const uint32_t mpb = 16 / g.group;  // sequences per column block
+    uint64_t base_items = 0;
     for (const PrefixGroup& pg : groups) {
-        prefix_tiles += static_cast<uint64_t>(pg.tiles) * nq;
-        for (int m = 0; m < pg.nmem; ++m) n_suffix += short_suffix[pg.b[m]] ? nq : 0;
+        base_items += static_cast<uint64_t>(nq) * ((static_cast<uint32_t>(pg.nmem) + mpb - 1) / mpb);
     }
-    const uint64_t suffix_wgs = (n_suffix + kWaves - 1) / kWaves;
-    const uint64_t chunk_wgs = max_wgs > suffix_wgs + 1 ? max_wgs - suffix_wgs : 1;
-    const uint64_t chunk_tiles = std::max<uint64_t>(kPrefixMinChunkTiles, (prefix_tiles + chunk_wgs - 1) / chunk_wgs);
+    const uint64_t want_chunks = base_items > 0 ? std::max<uint64_t>(1, max_wgs / base_items) : 1;
     for (PrefixGroup& pg : groups) {
-        pg.chunks = static_cast<int>(std::min<uint64_t>(kPrefixMaxChunks, (pg.tiles + chunk_tiles - 1) / chunk_tiles));
+        pg.chunks = static_cast<int>(std::max<uint64_t>(
+            1, std::min<uint64_t>({want_chunks, kPrefixMaxChunks, pg.tiles / kPrefixMinChunkTiles})));
         for (int m = 0; m < pg.nmem; ++m) {
-            const int extra = short_suffix[pg.b[m]] ? 1 : 0;
             for (uint32_t q = 0; q < nq; ++q) {
                 const size_t k = static_cast<size_t>(pg.b[m]) * nq + q;
-                seg_count[k] += pg.chunks + extra;
+                seg_count[k] += pg.chunks;
                 seg_next[k] = pg.chunks;
             }
         }
@@ -1500,50 +1474,51 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
         pc.seg_slot0 = seg_base[k];
         pc.seg_nslots = seg_count[k];
     }
+    // Items of one (group, kv head, chunk) read the same tiles: they get ids
+    // equal modulo the XCD count, which the dispatcher places on one XCD, so
+    // the tiles are shared through its L2.
+    constexpr size_t kXcds = 8;
+    std::vector<qvp_prefix_item> by_xcd[kXcds];
+    size_t unit = 0;
+    for (const PrefixGroup& pg : groups) {
+        const int ncb = (pg.nmem + static_cast<int>(mpb) - 1) / static_cast<int>(mpb);
+        for (uint32_t q = 0; q < nq; ++q) {
+            for (int ch = 0; ch < pg.chunks; ++ch, ++unit) {
+                for (int cb = 0; cb < ncb; ++cb) {
+                    qvp_prefix_item it{};
+                    it.g = static_cast<int32_t>(q);
+                    it.t0 = static_cast<int32_t>(static_cast<int64_t>(pg.tiles) * ch / pg.chunks);
+                    it.t1 = static_cast<int32_t>(static_cast<int64_t>(pg.tiles) * (ch + 1) / pg.chunks);
+                    it.nmem = std::min<int>(static_cast<int>(mpb), pg.nmem - cb * static_cast<int>(mpb));
+                    for (int m = 0; m < kPrefixMaxMembers; ++m) {
+                        const uint32_t b = pg.b[cb * static_cast<int>(mpb) + std::min(m, it.nmem - 1)];
+                        const size_t k = static_cast<size_t>(b) * nq + q;
+                        it.b[m] = static_cast<int32_t>(b);
+                        it.ctx[m] = static_cast<int32_t>(in.lens[b]);
+                        it.sfx_t1[m] = ch == pg.chunks - 1 && short_suffix[b] ? static_cast<int32_t>(start[b]) : it.t1;
+                        it.slot[m] = seg_base[k] >= 0 ? seg_base[k] + ch : -1;
+                        it.seg_slot0[m] = seg_base[k];
+                        it.nslots[m] = seg_count[k];
+                    }
+                    by_xcd[unit % kXcds].push_back(it);
+                }
+            }
+        }
+    }
     std::vector<qvp_prefix_item>& items = s.plan_prefix;
     items.clear();
-    for (const PrefixGroup& pg : groups) {
-        for (uint32_t q = 0; q < nq; ++q) {
-            for (int ch = 0; ch < pg.chunks; ++ch) {
-                qvp_prefix_item it{};
-                it.g = static_cast<int32_t>(q);
-                it.t0 = static_cast<int32_t>(static_cast<int64_t>(pg.tiles) * ch / pg.chunks);
-                it.t1 = static_cast<int32_t>(static_cast<int64_t>(pg.tiles) * (ch + 1) / pg.chunks);
-                it.nmem = pg.nmem;
-                for (int m = 0; m < kPrefixMaxMembers; ++m) {
-                    const int mm = std::min(m, pg.nmem - 1);
-                    const size_t k = static_cast<size_t>(pg.b[mm]) * nq + q;
-                    it.b[m] = static_cast<int32_t>(pg.b[mm]);
-                    it.seg_slot0[m] = seg_base[k];
-                    it.slot[m] = seg_base[k] + ch;
-                    it.nslots[m] = seg_count[k];
-                }
-                items.push_back(it);
+    for (size_t at = 0;; ++at) {
+        bool any = false;
+        for (size_t x = 0; x < kXcds; ++x) {
+            if (at < by_xcd[x].size()) {
+                items.push_back(by_xcd[x][at]);
+                any = true;
             }
         }
+        if (!any) break;
     }
-    // Short suffixes: the slot after the member's prefix chunks.
     std::vector<qvp_piece>& suffix = s.plan_suffix;
     suffix.clear();
-    for (const PrefixGroup& pg : groups) {
-        for (int m = 0; m < pg.nmem; ++m) {
-            const uint32_t b = pg.b[m];
-            if (!short_suffix[b]) continue;
-            for (uint32_t q = 0; q < nq; ++q) {
-                const size_t k = static_cast<size_t>(b) * nq + q;
-                qvp_piece pc{};
-                pc.b = static_cast<int32_t>(b);
-                pc.g = static_cast<int32_t>(q);
-                pc.t0 = static_cast<int32_t>(pg.tiles);
-                pc.t1 = static_cast<int32_t>(start[b]);
-                pc.ctx = static_cast<int32_t>(in.lens[b]);
-                pc.slot = seg_base[k] + seg_next[k];
-                pc.seg_slot0 = seg_base[k];
-                pc.seg_nslots = seg_count[k];
-                suffix.push_back(pc);
-            }
-        }
-    }
     // The kernel counts in at most kMaxMergesPerWg partial pieces per range:
     // without shared prefixes only a range's first and last piece are
     // partial; a schedule whose prefix groups would exceed the bound (many
@@ -1776,16 +1751,13 @@ int launch_mfma_decode(const DecodeGeometry& g, const qvp_batch* batch, uint32_t
         if (g.kv_elem != kElemBf16) return fail(QVP_ERR_INVALID_ARGUMENT, "shared-prefix schedule for a non-bf16 cache");
         PrefixArgs pa{};
         pa.items = reinterpret_cast<const qvp_prefix_item*>(s.words + s.off_prefix);
-        pa.suffix = reinterpret_cast<const qvp_piece*>(s.words + s.off_suffix);
         pa.counters = a.counters;
         pa.ws_ml = a.ws_ml;
         pa.ws_acc = a.ws_acc;
         pa.out = out;
         pa.num_items = static_cast<int>(s.num_prefix_items);
-        pa.num_suffix = static_cast<int>(s.num_suffix);
-        const uint32_t grid = s.num_prefix_items + (s.num_suffix + kWaves - 1) / kWaves;
         void* pargs[] = {&gk, &pa};
-        QVP_HIP(hipLaunchKernel(prefix_kernel(out_dtype), dim3(grid), dim3(kThreads), pargs, kPrefixLdsBytes, stream));
+        QVP_HIP(hipLaunchKernel(prefix_kernel(out_dtype), dim3(s.num_prefix_items), dim3(kThreads), pargs, 0, stream));
     }
     // Every sequence may be covered by the prefix launch (then only a carried
     // upload, if any, needs this one).

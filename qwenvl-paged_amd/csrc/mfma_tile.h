@@ -109,18 +109,22 @@ constexpr float kF16WeightLog2 = 15.0f;
 // hi and lo B operands of the PV MFMAs: for bf16, hi = P truncated to bf16 and
 // lo = P - hi rounded to nearest even; for fp16 (weights scaled by 2^15, see
 // kF16WeightLog2) hi = P and lo = P - hi, each rounded to nearest even.
-template <bool kF16 = false>
+// kGuard: a column may have seen no token yet after this tile (running
+// maximum still -inf); its weights and alpha are then 0 instead of
+// exp2(-inf - -inf).
+template <bool kF16 = false, bool kGuard = false>
 __device__ inline void softmax_p(const floatx4 (&s)[2], float scale_log2, float& m_run, float& l_run, u32x4& bhi,
                                  u32x4& blo, float& alpha) {
     float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     mt = max_over_j(mt) * scale_log2;
     const float m_new = fmaxf(m_run, mt);
-    alpha = fast_exp2(m_run - m_new);
+    const float m_use = kGuard && m_new == -INFINITY ? 0.f : m_new;
+    alpha = fast_exp2(m_run - m_use);
     m_run = m_new;
     float psum = 0.f;
     uint32_t phi[4], plo[4];
-    const float bias = kF16 ? kF16WeightLog2 - m_new : -m_new;
+    const float bias = kF16 ? kF16WeightLog2 - m_use : -m_use;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
@@ -170,12 +174,20 @@ __device__ inline void pv_tile(const u32x4 (&a)[8], const u32x4& bhi, const u32x
 // only when some column's maximum moved. V's A operands come from the loaded
 // rows by byte permutes: lane (c, j) holds dims 8c .. 8c + 7 of tokens
 // 4q + j, and PV MFMA n takes element n of each, two tokens per dword.
-template <bool kF16 = false>
+// kMasked: col_last differs between columns and may be below the tile (a
+// sequence's private tile run beside other sequences' columns): the mask is
+// applied without a branch and a column that has seen no token keeps weight 0.
+template <bool kF16 = false, bool kMasked = false>
 __device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0, int col_last, int v_end,
                                     float scale_log2, int j, float& m_run, float& l_run, floatx4 (&o)[8]) {
     floatx4 s[2];
     qk_tile<kF16>(cur.k, qop, s);
-    if (tok0 + kTileTokens - 1 > col_last) {
+    if constexpr (kMasked) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[u][r] = tok0 + j + 16 * u + 4 * r > col_last ? -INFINITY : s[u][r];
+    } else if (tok0 + kTileTokens - 1 > col_last) {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -185,7 +197,7 @@ __device__ inline void compute_tile(KvTile& cur, const u32x4 (&qop)[4], int tok0
     }
     u32x4 bhi, blo;
     float alpha;
-    softmax_p<kF16>(s, scale_log2, m_run, l_run, bhi, blo, alpha);
+    softmax_p<kF16, kMasked>(s, scale_log2, m_run, l_run, bhi, blo, alpha);
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
         for (int n = 0; n < 8; ++n) o[n] *= alpha;
