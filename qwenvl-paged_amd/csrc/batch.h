@@ -85,6 +85,13 @@ struct qvp_schedule {
     std::vector<double> weights;  // streaming weight per kv-head group the ranges were cut for
     bool defer{false};            // piece results held in LDS until a range is done
     uint32_t lds_bytes{0};        // dynamic LDS per workgroup for them
+    // What the plan was made from besides the geometry fields above: tiles
+    // per sequence and the shared-prefix groups found (members, shared
+    // tiles). A batch with the same key gets the same plan but for the
+    // context lengths it records (qvp_piece::ctx, qvp_prefix_item::ctx).
+    bool key_valid{false};
+    std::vector<uint32_t> key_tiles;
+    std::vector<uint32_t> key_groups;
     // Shared prefixes decoded once for their sequences (a launch before the
     // main one): work items and the sequence groups they came from.
     uint32_t num_prefix_items{0};

@@ -1580,8 +1580,46 @@ int plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry
 
 }  // namespace
 
+// A decode loop packs every step, and from one step to the next a sequence
+// usually gains one token: its tile count and its frames' sharing stay the
+// same, and so does the plan except for the context lengths stored in it.
+// The key (tiles per sequence, the shared-prefix groups found, geometry) is
+// compared first; on a match only those lengths are rewritten.
 int mfma_plan_schedule(qvp_schedule& s, const ScheduleInput& in, const DecodeGeometry& g) {
-    return plan_schedule(s, in, g, true);
+    uint32_t max_wgs = 0;
+    QVP_TRY(device_max_wgs(&max_wgs));
+    std::vector<uint32_t> tiles(in.num_seqs);
+    uint64_t total = 0;
+    for (uint32_t b = 0; b < in.num_seqs; ++b) {
+        tiles[b] = (static_cast<uint32_t>(in.lens[b]) + kTileTokens - 1) / kTileTokens;
+        total += tiles[b];
+    }
+    const uint32_t hps = head_group_size(g.num_kv_heads, total, max_wgs);
+    std::vector<uint32_t> groups;
+    for (const PrefixGroup& pg : find_prefix_groups(in, g, hps)) {
+        groups.push_back(static_cast<uint32_t>(pg.nmem));
+        groups.push_back(pg.tiles);
+        groups.insert(groups.end(), pg.b, pg.b + pg.nmem);
+    }
+    const bool same_geometry = s.key_valid && s.num_kv_heads == g.num_kv_heads && s.group == g.group &&
+                               s.tile_group == g.tile_group && s.kv_elem == g.kv_elem &&
+                               s.partition_tiles == in.partition_tiles && s.max_wgs == max_wgs && s.hps == hps &&
+                               s.weights == head_group_weights(g, hps, g.num_kv_heads / hps);
+    if (same_geometry && tiles == s.key_tiles && groups == s.key_groups) {
+        for (qvp_piece& pc : s.plan_pieces) pc.ctx = in.lens[pc.b];
+        for (qvp_piece& pc : s.plan_suffix) pc.ctx = in.lens[pc.b];
+        for (qvp_prefix_item& it : s.plan_prefix) {
+            for (int m = 0; m < kPrefixMaxMembers; ++m) it.ctx[m] = in.lens[it.b[m]];
+        }
+        s.pack_generation = in.generation;
+        return QVP_OK;
+    }
+    s.key_valid = false;
+    QVP_TRY(plan_schedule(s, in, g, true));
+    s.key_tiles = std::move(tiles);
+    s.key_groups = std::move(groups);
+    s.key_valid = true;
+    return QVP_OK;
 }
 
 void mfma_write_schedule(const qvp_schedule& s, const ScheduleInput& in, int32_t* h) {
