@@ -112,13 +112,20 @@ constexpr float kF16WeightLog2 = 15.0f;
 // kGuard: a column may have seen no token yet after this tile (running
 // maximum still -inf); its weights and alpha are then 0 instead of
 // exp2(-inf - -inf).
-template <bool kF16 = false, bool kGuard = false>
+// kLazy: the running maximum moves only when the tile's maximum exceeds it by
+// more than kLazyMaxLog2, so weights stay below 2^kLazyMaxLog2 and O is
+// rescaled on few tiles (alpha is exactly 1 otherwise). O / l is unchanged:
+// O and l always carry the same factor. Every column must have seen a token
+// (the causal prefill's tile 0 holds token 0 for every position).
+constexpr float kLazyMaxLog2 = 8.0f;
+
+template <bool kF16 = false, bool kGuard = false, bool kLazy = false>
 __device__ inline void softmax_p(const floatx4 (&s)[2], float scale_log2, float& m_run, float& l_run, u32x4& bhi,
                                  u32x4& blo, float& alpha) {
     float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                      fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
     mt = max_over_j(mt) * scale_log2;
-    const float m_new = fmaxf(m_run, mt);
+    const float m_new = kLazy ? (mt > m_run + kLazyMaxLog2 ? mt : m_run) : fmaxf(m_run, mt);
     const float m_use = kGuard && m_new == -INFINITY ? 0.f : m_new;
     alpha = fast_exp2(m_run - m_use);
     m_run = m_new;

@@ -228,14 +228,16 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
         qk_tile(kf, qa, sa);
         if constexpr (kTwo) qk_tile(kf, qb, sb);
         if (t_diag == 0) mask2(sa, sb, 0);
-        softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
-        if constexpr (kTwo) softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
+        softmax_p<false, false, true>(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
+        if constexpr (kTwo) softmax_p<false, false, true>(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
         store_tile(1, r0, min(1, last_tile));
         __syncthreads();
         // O is rescaled for tile t's maximum just before PV(t) accumulates
         // into it, skipped when no column's maximum moved (the factor is then
         // exactly 1); the branch sits at the top of the iteration, outside
-        // the block above.
+        // the block above. The maximum moves lazily (softmax_p's kLazy: only
+        // past kLazyMaxLog2 above the current one), so after the first tiles
+        // almost no iteration rescales.
         auto rescale = [&]() {
             if (__builtin_amdgcn_ballot_w64(alpha_a != 1.0f || alpha_b != 1.0f) != 0) {
 #pragma unroll
@@ -258,8 +260,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
             if constexpr (kTwo) pv_tile(vf, bhi, blo, ob);
             read_v(nb, vf);
             if constexpr (decltype(masked)::value) mask2(sa, sb, t + 1);
-            softmax_p(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
-            if constexpr (kTwo) softmax_p(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
+            softmax_p<false, false, true>(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
+            if constexpr (kTwo) softmax_p<false, false, true>(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
             // Schedule: the QK MFMAs first, then the PV MFMAs spread over the
             // softmax's VALU work.
             constexpr int kHeads = kTwo ? 2 : 1;
