@@ -101,34 +101,18 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 // O) of equal scale -- is unchanged.
 constexpr float kF16WeightLog2 = 15.0f;
 
-// Online-softmax step of one tile for column c of this lane. The running
-// maximum m is kept in scaled base-2 units, so with scale_log2 > 0 the
-// maximum is taken on the raw scores and each weight is one fma and one exp2.
-// l is rescaled here; O must be scaled by the returned alpha by the caller
-// (alpha is exactly 1 when no column's maximum moved). P is returned as the
-// hi and lo B operands of the PV MFMAs: for bf16, hi = P truncated to bf16 and
-// lo = P - hi rounded to nearest even; for fp16 (weights scaled by 2^15, see
-// kF16WeightLog2) hi = P and lo = P - hi, each rounded to nearest even.
-// kGuard: a column may have seen no token yet after this tile (running
-// maximum still -inf); its weights and alpha are then 0 instead of
-// exp2(-inf - -inf).
-// kLazy: the running maximum moves only when the tile's maximum exceeds it by
-// more than kLazyMaxLog2, so weights stay below 2^kLazyMaxLog2 and O is
-// rescaled on few tiles (alpha is exactly 1 otherwise). O / l is unchanged:
-// O and l always carry the same factor. Every column must have seen a token
-// (the causal prefill's tile 0 holds token 0 for every position).
-constexpr float kLazyMaxLog2 = 8.0f;
+// Largest score of one tile for column c of this lane (raw, before scaling).
+__device__ inline float tile_max(const floatx4 (&s)[2]) {
+    const float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
+                           fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+    return max_over_j(mt);
+}
 
-template <bool kF16 = false, bool kGuard = false, bool kLazy = false>
-__device__ inline void softmax_p(const floatx4 (&s)[2], float scale_log2, float& m_run, float& l_run, u32x4& bhi,
-                                 u32x4& blo, float& alpha) {
-    float mt = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                     fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
-    mt = max_over_j(mt) * scale_log2;
-    const float m_new = kLazy ? (mt > m_run + kLazyMaxLog2 ? mt : m_run) : fmaxf(m_run, mt);
-    const float m_use = kGuard && m_new == -INFINITY ? 0.f : m_new;
-    alpha = fast_exp2(m_run - m_use);
-    m_run = m_new;
+// Weights of one tile against the maximum m_use (scaled base-2 units): P as
+// the hi and lo B operands of the PV MFMAs (see softmax_p); returns this
+// lane's sum of its eight weights.
+template <bool kF16 = false>
+__device__ inline float tile_weights(const floatx4 (&s)[2], float scale_log2, float m_use, u32x4& bhi, u32x4& blo) {
     float psum = 0.f;
     uint32_t phi[4], plo[4];
     const float bias = kF16 ? kF16WeightLog2 - m_use : -m_use;
@@ -156,9 +140,39 @@ __device__ inline void softmax_p(const floatx4 (&s)[2], float scale_log2, float&
             }
         }
     }
-    l_run = l_run * alpha + psum;
     bhi = u32x4{phi[0], phi[1], phi[2], phi[3]};
     blo = u32x4{plo[0], plo[1], plo[2], plo[3]};
+    return psum;
+}
+
+// Online-softmax step of one tile for column c of this lane. The running
+// maximum m is kept in scaled base-2 units, so with scale_log2 > 0 the
+// maximum is taken on the raw scores and each weight is one fma and one exp2.
+// l is rescaled here; O must be scaled by the returned alpha by the caller
+// (alpha is exactly 1 when no column's maximum moved). P is returned as the
+// hi and lo B operands of the PV MFMAs: for bf16, hi = P truncated to bf16 and
+// lo = P - hi rounded to nearest even; for fp16 (weights scaled by 2^15, see
+// kF16WeightLog2) hi = P and lo = P - hi, each rounded to nearest even.
+// kGuard: a column may have seen no token yet after this tile (running
+// maximum still -inf); its weights and alpha are then 0 instead of
+// exp2(-inf - -inf).
+// kLazy: the running maximum moves only when the tile's maximum exceeds it by
+// more than kLazyMaxLog2, so weights stay below 2^kLazyMaxLog2 and O is
+// rescaled on few tiles (alpha is exactly 1 otherwise). O / l is unchanged:
+// O and l always carry the same factor. Every column must have seen a token
+// (the causal prefill's tile 0 holds token 0 for every position).
+constexpr float kLazyMaxLog2 = 8.0f;
+
+template <bool kF16 = false, bool kGuard = false, bool kLazy = false>
+__device__ inline void softmax_p(const floatx4 (&s)[2], float scale_log2, float& m_run, float& l_run, u32x4& bhi,
+                                 u32x4& blo, float& alpha) {
+    const float mt = tile_max(s) * scale_log2;
+    const float m_new = kLazy ? (mt > m_run + kLazyMaxLog2 ? mt : m_run) : fmaxf(m_run, mt);
+    const float m_use = kGuard && m_new == -INFINITY ? 0.f : m_new;
+    alpha = fast_exp2(m_run - m_use);
+    m_run = m_new;
+    const float psum = tile_weights<kF16>(s, scale_log2, m_use, bhi, blo);
+    l_run = l_run * alpha + psum;
 }
 
 // O^T += V^T P^T for one tile: `a` holds V^T operands (lane (c, j) of MFMA n:

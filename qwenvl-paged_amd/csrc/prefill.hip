@@ -289,13 +289,37 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     }
 
     OutT* out = static_cast<OutT*>(out_ptr);
+    // Lane (c, j) holds dims 32j .. 32j + 31 of column c: eight contiguous
+    // outputs per r, stored 16 bytes at a time, so a store instruction writes
+    // 64 contiguous bytes per lane quartet of each of its 16 rows (one 2-byte
+    // store per element scattered over 16 rows and took 20 % of the kernel).
     auto write = [&](int hq, const floatx4 (&o)[8], float l) {
         if (c >= np) return;
-        OutT* dst = out + (static_cast<uint64_t>(row0 + c) * p.num_q_heads + static_cast<uint64_t>(g) * G + hq) * 128;
+        OutT* dst = out + (static_cast<uint64_t>(row0 + c) * p.num_q_heads + static_cast<uint64_t>(g) * G + hq) * 128 +
+                    32 * j;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < 4; ++r) {
+            if constexpr (sizeof(OutT) == 4) {
+                u32x4 a, b2;
 #pragma unroll
-            for (int n = 0; n < 8; ++n) dst[32 * j + 8 * r + n] = from_float<OutT>(o[n][r] / l);
+                for (int n = 0; n < 4; ++n) {
+                    a[n] = __float_as_uint(o[n][r] / l);
+                    b2[n] = __float_as_uint(o[n + 4][r] / l);
+                }
+                *reinterpret_cast<u32x4*>(dst + 8 * r) = a;
+                *reinterpret_cast<u32x4*>(dst + 8 * r + 4) = b2;
+            } else {
+                u32x4 a;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const OutT lo_v = from_float<OutT>(o[2 * k][r] / l);
+                    const OutT hi_v = from_float<OutT>(o[2 * k + 1][r] / l);
+                    a[k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo_v)) |
+                           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi_v)) << 16);
+                }
+                *reinterpret_cast<u32x4*>(dst + 8 * r) = a;
+            }
+        }
     };
     la = sum_over_j(la);
     lb = sum_over_j(lb);
@@ -303,11 +327,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     if (has_b) write(h0 + wave + kPrefillWaves, ob, lb);
 }
 
-bool prefill_mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr, uintptr_t kv_base_addr) {
+bool prefill_mfma_supported(const DecodeGeometry& g, uint32_t kv_dtype, uintptr_t query_addr, uintptr_t kv_base_addr,
+                            uintptr_t out_addr) {
     const bool pow2 = g.tpb != 0 && (g.tpb & (g.tpb - 1)) == 0;
     const bool aligned = (g.block_stride % 16 == 0) && (g.k_off % 16 == 0) && (g.v_off % 16 == 0) &&
                          (g.token_stride % 16 == 0) && (g.head_stride % 16 == 0) && (kv_base_addr % 16 == 0) &&
-                         (query_addr % 16 == 0);
+                         (query_addr % 16 == 0) && (out_addr % 16 == 0);
     return kv_dtype == QVP_DTYPE_BF16 && g.head_dim == 128 && g.group >= 1 && g.group <= 16 && pow2 && g.tpb >= 16 &&
            aligned;
 }
@@ -404,7 +429,8 @@ extern "C" int qvp_paged_prefill(const qvp_prefill_args* a, void* stream) {
 
     // The MFMA kernel takes its running maximum on raw scores: scale > 0.
     if (!(a->scale > 0.0f) || !qvp::prefill_mfma_supported(g, a->kv_dtype, reinterpret_cast<uintptr_t>(a->query),
-                                                            reinterpret_cast<uintptr_t>(a->kv_base))) {
+                                                            reinterpret_cast<uintptr_t>(a->kv_base),
+                                                            reinterpret_cast<uintptr_t>(a->out))) {
         // One virtual sequence per new position, over the same frames, run in
         // chunks of at most kMaxVirtualIds block ids (a long prompt needs
         // about n^2 / (2 tokens_per_block) of them). Chunks are packed and

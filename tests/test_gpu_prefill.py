@@ -44,11 +44,12 @@ def _queries(w: W.Workload, total: int, seed: int) -> np.ndarray:
     return q if w.kv_dtype == qvp.DTYPE_F32 else W.f32_to_bf16_bits(q)
 
 
-def _run(w: W.Workload, q_start, out_dtype: int, seed: int = 1, image=None):
+def _run(w: W.Workload, q_start, out_dtype: int, seed: int = 1, image=None, queries=None):
     run = GpuRun(w, image=image)
     q_start = np.asarray(q_start, np.uint32)
     total = int((w.context_lens.astype(np.int64) - q_start).sum())
-    queries = _queries(w, total, seed)
+    if queries is None:
+        queries = _queries(w, total, seed)
     dq = qvp.DeviceBuffer.from_array(queries)
     n = total * w.num_query_heads * w.head_dim
     out = qvp.DeviceBuffer(n * qvp.DTYPE_BYTES[out_dtype])
@@ -103,6 +104,32 @@ def test_prefill_of_a_1024_token_prompt():
     w = W.custom([1024, 700], 28, 4, 128, seed=3)
     got, ref_out, ref32, _ = _run(w, [0, 0], qvp.DTYPE_F32)
     _check(w, got, ref_out, ref32, qvp.DTYPE_F32, "1024-token prefill")
+
+
+@pytest.mark.parametrize("out_dtype", [qvp.DTYPE_F32, qvp.DTYPE_BF16])
+def test_scores_far_above_the_first_tile_move_the_running_maximum(out_dtype):
+    # The MFMA prefill's running maximum moves lazily: only when a tile's
+    # maximum exceeds it by more than 2^8 in weight, and O and l are then
+    # rescaled. Here every query shares a direction (entries 1 + N(0, 0.3^2))
+    # and one token per sequence has K = 3.0 along it: its score is ~384
+    # (scaled: ~49 in log2 units) against ~15 at most in the first tile, so
+    # every position from that token on moves its maximum by far more than the
+    # lazy threshold and rescales O by ~2^-47. Every row must equal the oracle.
+    print(f"case: prefill, scores far above the first tile, out={out_dtype}", flush=True)
+    w = W.custom([300, 130], 28, 4, 128, seed=21)
+    image = w.pool_image()
+    st = w.strides
+    bright = W.f32_to_bf16_bits(np.full(128, 3.0, np.float32)).view(np.uint8)
+    for b, tok in ((0, 200), (1, 100)):
+        blk = int(w.ids[w.cu_blocks[b] + tok // w.tokens_per_block])
+        for g in range(w.num_kv_heads):
+            off = blk * w.block_stride + 2 * ((tok % w.tokens_per_block) * st["token_stride"] + g * st["head_stride"])
+            image[off:off + 256] = bright
+    total = int(w.context_lens.sum())
+    rng = np.random.default_rng(22)
+    queries = W.f32_to_bf16_bits((1.0 + rng.normal(0.0, 0.3, (total, 28, 128))).astype(np.float32))
+    got, ref_out, ref32, _ = _run(w, [0, 0], out_dtype, image=image, queries=queries)
+    _check(w, got, ref_out, ref32, out_dtype, "scores far above the first tile")
 
 
 @pytest.mark.parametrize("shape", [(8, 2, 64, qvp.DTYPE_F32), (8, 2, 128, qvp.DTYPE_F32), (4, 2, 80, qvp.DTYPE_BF16)])
