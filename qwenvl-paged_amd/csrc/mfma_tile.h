@@ -176,7 +176,9 @@ __device__ inline void softmax_p(const floatx4 (&s)[2], float scale_log2, float&
 }
 
 // O^T += V^T P^T for one tile: `a` holds V^T operands (lane (c, j) of MFMA n:
-// dims 16n + c, the tile's tokens in the P operand's k order).
+// the caller's dim for row c of block n, the tile's tokens in the P operand's
+// k order); C register r of MFMA n in lane (c, j) is O[column c][that block's
+// row 4j + r].
 template <bool kF16 = false>
 __device__ inline void pv_tile(const u32x4 (&a)[8], const u32x4& bhi, const u32x4& blo, floatx4 (&o)[8]) {
 #pragma unroll

@@ -9,9 +9,10 @@
 // positions p0 .. p0 + 15, up to 8 query heads of g's group). Its workgroup
 // streams tokens [0, p0 + 16) of kv head g in 32-token tiles: each tile is
 // loaded once, by all 256 threads, one tile of compute ahead of its use, into
-// an LDS double buffer holding K rows (padded to 272 bytes so the fragment
-// reads spread over the banks) and V transposed (so the PV operands need no
-// register transpose), and every wave runs the tile math of mfma_tile.h for
+// an LDS double buffer holding the K and V rows as in the frame (padded to
+// 272 bytes so the fragment reads spread over the banks; the PV operands come
+// out of V transposed by ds_read_b64_tr_b16), and every wave runs the tile
+// math of mfma_tile.h for
 // its two query heads with the 16 positions in the MFMA columns, column c
 // seeing tokens t <= p0 + c (masks only on tiles that reach p0). The tile
 // loop is software-pipelined: PV of tile t runs beside QK and the softmax of
@@ -39,18 +40,20 @@ constexpr int kPrefillThreads = kPrefillWaves * 64;
 constexpr int kPrefillPositions = 16;     // MFMA columns
 constexpr int kPrefillHeadsPerItem = 8;   // two query heads per wave
 constexpr int kHeadBytes = 256;           // 128 bf16
-constexpr int kLdsRow = kHeadBytes + 16;  // padded LDS row of one token's K
-constexpr int kVtRow = 64 + 16;           // padded LDS row of one dim of V^T (32 tokens)
+constexpr int kLdsRow = kHeadBytes + 16;  // padded LDS row of one token's K or V
 // Block ids per virtual batch of the decode-kernel path.
 constexpr size_t kMaxVirtualIds = size_t{1} << 20;
 
-// One K/V tile in LDS: K rows as in the frame (token-major), V transposed
-// (dim-major) so each PV operand is one 16-byte read. V^T row n * 16 + x
-// holds dim 8x + n; within a row, element 8 (t % 4) + t / 4 holds token t
-// (the k order of the PV MFMAs' P operand).
+// One K/V tile in LDS: K and V rows as in the frame (token-major). PV MFMA n
+// takes dims 16n .. 16n + 15 as its rows; lane (c, j) needs V[4i + j][16n + c]
+// for i = 0 .. 7 (the k order of the P operand). ds_read_b64_tr_b16 hands lane
+// c of each 16-lane group element c % 4 of the 8 bytes that lane 4e + c / 4
+// of the group addressed, as element e: so lane (c, j) addresses dims
+// 16n + 4 (c % 4) .. + 3 of token 4 (c / 4 + 4h) + j, and two such reads
+// (h = 0, 1) give its eight operand elements.
 struct PrefillTile {
     uint8_t k[kTileTokens][kLdsRow];
-    uint8_t vt[128][kVtRow];
+    uint8_t v[kTileTokens][kLdsRow];
 };
 
 struct PrefillItem {
@@ -69,6 +72,8 @@ __device__ inline const __attribute__((address_space(4))) T* as_const(const T* p
 }
 
 __device__ inline u32x4 lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef uint32_t uint2v __attribute__((ext_vector_type(2)));
 
 template <typename OutT>
 __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometry p, const PrefillItem* items,
@@ -116,23 +121,14 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     float ma = -INFINITY, la = 0.f, mb = -INFINITY, lb = 0.f;
 
     // Cooperative tile loads: thread t moves 16-byte chunk x = t % 16 of the K
-    // and V rows of tokens r and r + 4, r = t / 64 + 8 ((t / 16) % 4), and
-    // writes the V pair transposed. Wave w thus writes V^T chunk w of every
-    // row, each lane group its own dword of the chunk: the 64 lanes of a
-    // transposed store hit 64 distinct LDS banks.
+    // and V rows of tokens r and r + 4, r = t / 64 + 8 ((t / 16) % 4).
     const int lx = threadIdx.x & 15;
     const int lr = (threadIdx.x >> 6) + 8 * ((threadIdx.x >> 4) & 3);
-    const int vt_col = 2 * (8 * (lr & 3) + (lr >> 2));  // byte offset of token lr (lr + 4 follows it)
     auto store_lds = [&](int buf, const u32x4 (&r)[4]) {
         *reinterpret_cast<u32x4*>(&sm[buf].k[lr][16 * lx]) = r[0];
         *reinterpret_cast<u32x4*>(&sm[buf].k[lr + 4][16 * lx]) = r[1];
-#pragma unroll
-        for (int n = 0; n < 8; ++n) {
-            const uint32_t x = r[2][n >> 1];
-            const uint32_t y = r[3][n >> 1];
-            const uint32_t pair = (n & 1) ? ((x >> 16) | (y & 0xffff0000u)) : ((x & 0xffffu) | (y << 16));
-            *reinterpret_cast<uint32_t*>(&sm[buf].vt[n * 16 + lx][vt_col]) = pair;
-        }
+        *reinterpret_cast<u32x4*>(&sm[buf].v[lr][16 * lx]) = r[2];
+        *reinterpret_cast<u32x4*>(&sm[buf].v[lr + 4][16 * lx]) = r[3];
     };
 
     // Addressing: a tile's two 16-token halves lie in one block each
@@ -186,7 +182,18 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     };
     auto read_v = [&](int buf, u32x4 (&vf)[8]) {
 #pragma unroll
-        for (int n = 0; n < 8; ++n) vf[n] = lds16(&sm[buf].vt[n * 16 + c][16 * j]);
+        for (int n = 0; n < 8; ++n) {
+            u32x4 a;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int row = 4 * ((c >> 2) + 4 * hh) + j;
+                const v4i16 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (v4i16 __attribute__((address_space(3)))*)(&sm[buf].v[row][2 * (16 * n + 4 * (c & 3))]));
+                a[2 * hh] = __builtin_bit_cast(uint2v, t)[0];
+                a[2 * hh + 1] = __builtin_bit_cast(uint2v, t)[1];
+            }
+            vf[n] = a;
+        }
     };
     // Causal mask of tile t for both heads: column c sees tokens <= col_last.
     auto mask2 = [&](floatx4 (&sa)[2], floatx4 (&sb)[2], int t) {
@@ -289,35 +296,31 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     }
 
     OutT* out = static_cast<OutT*>(out_ptr);
-    // Lane (c, j) holds dims 32j .. 32j + 31 of column c: eight contiguous
-    // outputs per r, stored 16 bytes at a time, so a store instruction writes
-    // 64 contiguous bytes per lane quartet of each of its 16 rows (one 2-byte
-    // store per element scattered over 16 rows and took 20 % of the kernel).
+    // C register r of PV MFMA n in lane (c, j) is O[column c][dim 16n + 4j +
+    // r]: four contiguous outputs per n, stored as one vector, so a store
+    // instruction writes 16 contiguous dims (4 lanes) of each of its 16 rows
+    // (one 2-byte store per element took a fifth of the kernel).
     auto write = [&](int hq, const floatx4 (&o)[8], float l) {
         if (c >= np) return;
         OutT* dst = out + (static_cast<uint64_t>(row0 + c) * p.num_q_heads + static_cast<uint64_t>(g) * G + hq) * 128 +
-                    32 * j;
+                    4 * j;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int n = 0; n < 8; ++n) {
             if constexpr (sizeof(OutT) == 4) {
-                u32x4 a, b2;
-#pragma unroll
-                for (int n = 0; n < 4; ++n) {
-                    a[n] = __float_as_uint(o[n][r] / l);
-                    b2[n] = __float_as_uint(o[n + 4][r] / l);
-                }
-                *reinterpret_cast<u32x4*>(dst + 8 * r) = a;
-                *reinterpret_cast<u32x4*>(dst + 8 * r + 4) = b2;
-            } else {
                 u32x4 a;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const OutT lo_v = from_float<OutT>(o[2 * k][r] / l);
-                    const OutT hi_v = from_float<OutT>(o[2 * k + 1][r] / l);
+                for (int r = 0; r < 4; ++r) a[r] = __float_as_uint(o[n][r] / l);
+                *reinterpret_cast<u32x4*>(dst + 16 * n) = a;
+            } else {
+                uint2v a;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const OutT lo_v = from_float<OutT>(o[n][2 * k] / l);
+                    const OutT hi_v = from_float<OutT>(o[n][2 * k + 1] / l);
                     a[k] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo_v)) |
                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi_v)) << 16);
                 }
-                *reinterpret_cast<u32x4*>(dst + 8 * r) = a;
+                *reinterpret_cast<uint2v*>(dst + 16 * n) = a;
             }
         }
     };
