@@ -8,12 +8,12 @@
 // tokens_per_block >= 16). A work item is (sequence b, kv head g, 16 new
 // positions p0 .. p0 + 15, up to 8 query heads of g's group). Its workgroup
 // streams tokens [0, p0 + 16) of kv head g in 32-token tiles: each tile is
-// loaded once, by all 256 threads, one tile of compute ahead of its use, into
-// an LDS double buffer holding the K and V rows as in the frame (padded to
-// 272 bytes so the fragment reads spread over the banks; the PV operands come
-// out of V transposed by ds_read_b64_tr_b16), and every wave runs the tile
-// math of mfma_tile.h for
-// its two query heads with the 16 positions in the MFMA columns, column c
+// loaded once, from HBM straight into LDS, one tile of compute ahead of its
+// use, into a double buffer holding the K and V rows as in the frame (16-byte
+// chunks XOR-permuted by row so the fragment reads spread over the banks; the
+// PV operands come out of V transposed by ds_read_b64_tr_b16), and every wave
+// runs the tile math of mfma_tile.h for its two query heads with the 16
+// positions in the MFMA columns, column c
 // seeing tokens t <= p0 + c (masks only on tiles that reach p0). The tile
 // loop is software-pipelined: PV of tile t runs beside QK and the softmax of
 // tile t + 1. A wave therefore covers the whole causal context of its
@@ -40,7 +40,6 @@ constexpr int kPrefillThreads = kPrefillWaves * 64;
 constexpr int kPrefillPositions = 16;     // MFMA columns
 constexpr int kPrefillHeadsPerItem = 8;   // two query heads per wave
 constexpr int kHeadBytes = 256;           // 128 bf16
-constexpr int kLdsRow = kHeadBytes + 16;  // padded LDS row of one token's K or V
 // Block ids per virtual batch of the decode-kernel path.
 constexpr size_t kMaxVirtualIds = size_t{1} << 20;
 
@@ -52,9 +51,13 @@ constexpr size_t kMaxVirtualIds = size_t{1} << 20;
 // 16n + 4 (c % 4) .. + 3 of token 4 (c / 4 + 4h) + j, and two such reads
 // (h = 0, 1) give its eight operand elements.
 struct PrefillTile {
-    uint8_t k[kTileTokens][kLdsRow];
-    uint8_t v[kTileTokens][kLdsRow];
+    uint8_t k[kTileTokens][kHeadBytes];
+    uint8_t v[kTileTokens][kHeadBytes];
 };
+// Byte of (row, logical byte) in a swizzled 256-byte row: 16-byte chunk x at x ^ (row % 16).
+__device__ inline uint32_t swz(int row, int byte) {
+    return 16u * static_cast<uint32_t>((byte >> 4) ^ (row & 15)) + static_cast<uint32_t>(byte & 15);
+}
 
 struct PrefillItem {
     int32_t b;     // sequence
@@ -120,65 +123,56 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     }
     float ma = -INFINITY, la = 0.f, mb = -INFINITY, lb = 0.f;
 
-    // Cooperative tile loads: thread t moves 16-byte chunk x = t % 16 of the K
-    // and V rows of tokens r and r + 4, r = t / 64 + 8 ((t / 16) % 4).
-    const int lx = threadIdx.x & 15;
-    const int lr = (threadIdx.x >> 6) + 8 * ((threadIdx.x >> 4) & 3);
-    auto store_lds = [&](int buf, const u32x4 (&r)[4]) {
-        *reinterpret_cast<u32x4*>(&sm[buf].k[lr][16 * lx]) = r[0];
-        *reinterpret_cast<u32x4*>(&sm[buf].k[lr + 4][16 * lx]) = r[1];
-        *reinterpret_cast<u32x4*>(&sm[buf].v[lr][16 * lx]) = r[2];
-        *reinterpret_cast<u32x4*>(&sm[buf].v[lr + 4][16 * lx]) = r[3];
-    };
-
-    // Addressing: a tile's two 16-token halves lie in one block each
-    // (tokens_per_block is a power of two >= 16), so their frame offsets are
-    // uniform values computed once per tile and each lane adds a constant for
-    // its token rows (tokens lr and lr + 4 share a half). Halves past the
-    // context's last block re-read that block: their scores are masked and
-    // their V rows zeroed, so every address stays inside a mapped frame.
+    // Tile loads go from HBM straight into LDS (global_load_lds_dwordx4): one
+    // instruction fills four rows (1 KiB), lane l landing at byte 16 l of them
+    // -- row r0 + l / 16, physical chunk l % 16, which holds logical chunk
+    // (l % 16) ^ (row % 16). A tile's two 16-token halves lie in one block each
+    // (tokens_per_block is a power of two >= 16); a half past the context's
+    // last block reads that block, and rows past the context load the
+    // context's last token (finite data under weights of 0), so every address
+    // stays inside a mapped frame. With an odd group the last wave holds one
+    // head and issues all sixteen loads of a tile (K and V, rows 0 .. 31),
+    // leaving the two-head waves none to issue or wait for; otherwise wave w
+    // loads rows 8w .. 8w + 7.
     const auto* trow = as_const(p.tables) + static_cast<uint64_t>(b) * p.max_nb;
     const int last_tok = ctx_end - 1;
     const int last_blk = last_tok >> p.tpb_shift;
-    const int lane_half = lr >> 4;
-    uint64_t lane_off[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        lane_off[e] = static_cast<uint64_t>((lr + 4 * e) & 15) * p.token_stride +
-                      static_cast<uint64_t>(g) * p.head_stride + 16 * lx;
-    }
     const uint8_t* kbase = p.kv_base + p.k_off;
     const uint8_t* vbase = p.kv_base + p.v_off;
-    auto load_tile_regs = [&](int tile, u32x4 (&r)[4]) {
-        uint64_t half_off[2];
+    const bool one_loader = nh == kPrefillHeadsPerItem - 1;
+    auto load_rows = [&](int buf, int tile, int r0) {
+        const int row = r0 + (lane >> 4);
+        const int tok = min(tile * kTileTokens + row, last_tok);
+        const int half_tok0 = tile * kTileTokens + (r0 & 16);
+        const uint64_t off = static_cast<uint64_t>(trow[min(half_tok0 >> p.tpb_shift, last_blk)]) * p.block_stride +
+                             static_cast<uint64_t>(g) * p.head_stride +
+                             static_cast<uint64_t>(tok & (p.tpb - 1)) * p.token_stride +
+                             16u * static_cast<uint32_t>((lane & 15) ^ (row & 15));
+        __builtin_amdgcn_global_load_lds(kbase + off, (__attribute__((address_space(3))) void*)(&sm[buf].k[r0][0]), 16,
+                                         0, 0);
+        __builtin_amdgcn_global_load_lds(vbase + off, (__attribute__((address_space(3))) void*)(&sm[buf].v[r0][0]), 16,
+                                         0, 0);
+    };
+    auto load_tile_lds = [&](int buf, int tile) {
+        if (one_loader) {
+            if (wave == kPrefillWaves - 1) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int tok0 = tile * kTileTokens + 16 * h;
-            const int blk = min(tok0 >> p.tpb_shift, last_blk);
-            half_off[h] = static_cast<uint64_t>(trow[blk]) * p.block_stride +
-                          static_cast<uint64_t>(tok0 & (p.tpb - 1) & ~15) * p.token_stride;
-        }
-        const uint64_t off = lane_half ? half_off[1] : half_off[0];
+                for (int q = 0; q < 8; ++q) load_rows(buf, tile, 4 * q);
+            }
+        } else {
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            r[e] = load16(kbase + off + lane_off[e]);
-            r[2 + e] = load16(vbase + off + lane_off[e]);
+            for (int q = 0; q < 2; ++q) load_rows(buf, tile, 8 * wave + 4 * q);
         }
     };
-    // V rows past the context are not data (0 * NaN would poison O): they are
-    // zeroed when the tile goes to LDS, a tile of compute after their loads.
-    auto store_tile = [&](int buf, u32x4 (&r)[4], int tile) {
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            if (tile * kTileTokens + lr + 4 * e > last_tok) r[2 + e] = u32x4{0u, 0u, 0u, 0u};
-        }
-        store_lds(buf, r);
-    };
+
     auto read_k = [&](int buf, u32x4 (&kf)[2][4]) {
 #pragma unroll
         for (int u = 0; u < 2; ++u)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) kf[u][i] = lds16(&sm[buf].k[16 * u + (c >> 2) + 4 * (c & 3)][16 * j + 64 * i]);
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * u + (c >> 2) + 4 * (c & 3);
+                kf[u][i] = lds16(&sm[buf].k[row][swz(row, 16 * j + 64 * i)]);
+            }
     };
     auto read_v = [&](int buf, u32x4 (&vf)[8]) {
 #pragma unroll
@@ -188,7 +182,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
             for (int hh = 0; hh < 2; ++hh) {
                 const int row = 4 * ((c >> 2) + 4 * hh) + j;
                 const v4i16 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                    (v4i16 __attribute__((address_space(3)))*)(&sm[buf].v[row][2 * (16 * n + 4 * (c & 3))]));
+                    (v4i16 __attribute__((address_space(3)))*)(&sm[buf].v[row][swz(row, 2 * (16 * n + 4 * (c & 3)))]));
                 a[2 * hh] = __builtin_bit_cast(uint2v, t)[0];
                 a[2 * hh + 1] = __builtin_bit_cast(uint2v, t)[1];
             }
@@ -210,8 +204,9 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     // Software pipeline over tiles. Iteration t issues PV(t) (P and V of tile
     // t already in registers) in one basic block with QK and the softmax of
     // tile t + 1, which do not depend on it, so the MFMAs of one overlap the
-    // VALU work of the other; tile t + 2 travels from registers to the LDS
-    // buffer tile t used. Tiles from t_diag on reach the block's first
+    // VALU work of the other; tile t + 2 is loaded into the LDS buffer tile t
+    // used, and every wave waits for its loads before the iteration's closing
+    // barrier. Tiles from t_diag on reach the block's first
     // position and take the causal mask; the loop is split there so the
     // others carry no mask code. A wave with two query heads runs both in one
     // block; a wave with one (the last wave of an odd group) runs a
@@ -221,15 +216,17 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
     const int last_tile = ntiles - 1;
     auto run = [&](auto two_heads) {
         constexpr bool kTwo = decltype(two_heads)::value;
-        u32x4 r0[4];
         u32x4 kf[2][4], vf[8];
         floatx4 sa[2], sb[2];
         u32x4 ahi, alo, bhi, blo;
         float alpha_a, alpha_b = 1.0f;
-        load_tile_regs(0, r0);
-        store_tile(0, r0, 0);
-        load_tile_regs(min(1, last_tile), r0);
+        // A direct load has landed in LDS once vmcnt counts it done: each wave
+        // waits for all of its loads (s_waitcnt 0) before the barrier that
+        // hands the tile to the other waves.
+        load_tile_lds(0, 0);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if (last_tile >= 1) load_tile_lds(1, 1);
         read_k(0, kf);
         read_v(0, vf);
         qk_tile(kf, qa, sa);
@@ -237,7 +234,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
         if (t_diag == 0) mask2(sa, sb, 0);
         softmax_p<false, false, true>(sa, p.scale_log2, ma, la, ahi, alo, alpha_a);
         if constexpr (kTwo) softmax_p<false, false, true>(sb, p.scale_log2, mb, lb, bhi, blo, alpha_b);
-        store_tile(1, r0, min(1, last_tile));
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         // O is rescaled for tile t's maximum just before PV(t) accumulates
         // into it, skipped when no column's maximum moved (the factor is then
@@ -259,7 +256,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
             rescale();
             // Tile t + 2; near the end the last tile again, which lands in a
             // buffer no later iteration reads.
-            load_tile_regs(min(t + 2, last_tile), r0);
+            // Tile t + 2 into the buffer tile t used (read at iteration t - 1).
+            if (t + 2 <= last_tile) load_tile_lds(t & 1, t + 2);
             read_k(nb, kf);
             qk_tile(kf, qa, sa);
             if constexpr (kTwo) qk_tile(kf, qb, sb);
@@ -279,7 +277,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void prefill_mfma(DecodeGeometr
                 __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             }
-            store_tile(t & 1, r0, min(t + 2, last_tile));
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         };
         int t = 0;
