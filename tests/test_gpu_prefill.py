@@ -44,7 +44,7 @@ def _queries(w: W.Workload, total: int, seed: int) -> np.ndarray:
     return q if w.kv_dtype == qvp.DTYPE_F32 else W.f32_to_bf16_bits(q)
 
 
-def _run(w: W.Workload, q_start, out_dtype: int, seed: int = 1, image=None, queries=None):
+def _run(w: W.Workload, q_start, out_dtype: int, seed: int = 1, image=None, queries=None, out_offset: int = 0):
     run = GpuRun(w, image=image)
     q_start = np.asarray(q_start, np.uint32)
     total = int((w.context_lens.astype(np.int64) - q_start).sum())
@@ -52,17 +52,26 @@ def _run(w: W.Workload, q_start, out_dtype: int, seed: int = 1, image=None, quer
         queries = _queries(w, total, seed)
     dq = qvp.DeviceBuffer.from_array(queries)
     n = total * w.num_query_heads * w.head_dim
-    out = qvp.DeviceBuffer(n * qvp.DTYPE_BYTES[out_dtype])
+    nbytes = n * qvp.DTYPE_BYTES[out_dtype]
+    # out_offset > 0: the output starts that many bytes into a larger buffer
+    # whose other bytes must stay 0xFF.
+    out = qvp.DeviceBuffer(nbytes + (2 * out_offset if out_offset else 0))
     out.fill(0xFF)
     run.batch.pack(w.ids, w.cu_blocks, w.context_lens, w.tokens_per_block, w.num_pool_blocks, w.split_tokens)
-    args = qvp.prefill_args(query=dq.ptr, out=out.ptr, kv_base=run.pool.base, block_stride=run.pool.stride,
-                            batch=run.batch, q_start=q_start, kv_dtype=w.kv_dtype, out_dtype=out_dtype,
-                            layer=w.layer, num_layers=w.num_layers, num_query_heads=w.num_query_heads,
-                            num_kv_heads=w.num_kv_heads, head_dim=w.head_dim, tokens_per_block=w.tokens_per_block,
-                            scale=w.scale, strides=w.strides)
+    args = qvp.prefill_args(query=dq.ptr, out=out.ptr + out_offset, kv_base=run.pool.base,
+                            block_stride=run.pool.stride, batch=run.batch, q_start=q_start, kv_dtype=w.kv_dtype,
+                            out_dtype=out_dtype, layer=w.layer, num_layers=w.num_layers,
+                            num_query_heads=w.num_query_heads, num_kv_heads=w.num_kv_heads, head_dim=w.head_dim,
+                            tokens_per_block=w.tokens_per_block, scale=w.scale, strides=w.strides)
     qvp.paged_prefill(args)
     np_dtype = np.float32 if out_dtype == qvp.DTYPE_F32 else np.uint16
-    got = out.download(np_dtype, (total, w.num_query_heads, w.head_dim))
+    if out_offset:
+        raw = out.download(np.uint8, (out.nbytes,))
+        assert (raw[:out_offset] == 0xFF).all() and (raw[out_offset + nbytes:] == 0xFF).all(), \
+            "bytes outside the output were written"
+        got = raw[out_offset:out_offset + nbytes].copy().view(np_dtype).reshape(total, w.num_query_heads, w.head_dim)
+    else:
+        got = out.download(np_dtype, (total, w.num_query_heads, w.head_dim))
     ref_out, ref32 = _oracle_prefill(w, run.image, queries, q_start)
     return got, ref_out, ref32, (run, args, out, dq)
 
@@ -139,6 +148,17 @@ def test_other_shapes_use_the_decode_path(shape):
     w = W.custom([37, 128, 250], hq, hkv, d, kv_dtype=dtype, seed=d)
     got, ref_out, ref32, _ = _run(w, [0, 64, 249], qvp.DTYPE_F32)
     _check(w, got, ref_out, ref32, qvp.DTYPE_F32, f"fallback {shape}")
+
+
+@pytest.mark.parametrize("out_dtype", [qvp.DTYPE_F32, qvp.DTYPE_BF16])
+def test_output_off_a_16_byte_boundary_takes_the_decode_path(out_dtype):
+    # The tile kernel stores each lane's outputs as 16-byte (fp32) or 8-byte
+    # (bf16) vectors; an output pointer 4 bytes past a 16-byte boundary goes to
+    # the decode-kernel path, which must write the same rows and nothing else.
+    print(f"case: prefill with out 4 bytes off alignment, out={out_dtype}", flush=True)
+    w = W.custom([37, 300], 28, 4, 128, seed=4)
+    got, ref_out, ref32, _ = _run(w, [0, 100], out_dtype, out_offset=4)
+    _check(w, got, ref_out, ref32, out_dtype, "unaligned output")
 
 
 def test_decode_path_runs_long_prompts_in_chunks():
