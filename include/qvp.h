@@ -418,9 +418,11 @@ typedef struct qvp_prefill_args {
 
 /* Validates everything on the host (the decode's rules, plus q_start[b] <
  * seq_lens[b]), then enqueues the prefill on `stream`. bf16 caches with
- * head_dim 128 and a positive scale run the MFMA prefill kernel; other shapes
- * run the decode kernels over one virtual sequence per new position (packed
- * in chunks of at most 2^20 block ids, decoded in order on `stream`). */
+ * head_dim 128, a positive scale, power-of-two tokens_per_block >= 16, and
+ * query, out, kv_base and the strides in bytes all multiples of 16 run the
+ * MFMA prefill kernel; everything else runs the decode kernels over one
+ * virtual sequence per new position (packed in chunks of at most 2^20 block
+ * ids, decoded in order on `stream`). */
 int qvp_paged_prefill(const qvp_prefill_args* args, void* stream);
 
 /* ------------------------------------------------------------------------ */
