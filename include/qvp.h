@@ -357,7 +357,8 @@ typedef enum qvp_decode_kernel {
     QVP_DECODE_NONE = 0,        /* nothing decoded since the last qvp_pack */
     QVP_DECODE_MFMA = 1,        /* persistent bf16 MFMA kernel, cost-balanced tile ranges */
     QVP_DECODE_F32_GROUPED = 2, /* fp32 MFMA kernel over split_tokens partitions + merge */
-    QVP_DECODE_GENERIC = 3      /* VALU kernel over split_tokens partitions + merge */
+    QVP_DECODE_GENERIC = 3,     /* VALU kernel per query head over split_tokens partitions + merge */
+    QVP_DECODE_GROUPED = 4      /* VALU kernel per kv head (GQA group folded) over split_tokens partitions + merge */
 } qvp_decode_kernel;
 
 typedef struct qvp_decode_plan {

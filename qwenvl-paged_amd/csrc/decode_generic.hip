@@ -8,6 +8,8 @@
 // the MFMA kernel does not cover.
 #include "decode_common.h"
 
+#include <algorithm>
+
 namespace qvp {
 namespace {
 
@@ -131,7 +133,224 @@ __global__ __launch_bounds__(128) void merge_splits(const float* __restrict__ ws
     }
 }
 
+constexpr int kGroupedThreads = 256;
+constexpr int kGroupedWaves = kGroupedThreads / 64;
+
+// Reduces each of a thread's kG per-head values over the workgroup (every
+// thread gets the results): shuffles within each wave, one LDS exchange.
+template <int kG, bool kMax>
+__device__ inline void reduce_heads(float (&v)[kG], float (*red)[kG]) {
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+        for (int off = 32; off > 0; off >>= 1) {
+            const float o = __shfl_xor(v[h], off);
+            v[h] = kMax ? fmaxf(v[h], o) : v[h] + o;
+        }
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int h = 0; h < kG; ++h) red[wave][h] = v[h];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+        float r = red[0][h];
+#pragma unroll
+        for (int w = 1; w < kGroupedWaves; ++w) r = kMax ? fmaxf(r, red[w][h]) : r + red[w][h];
+        v[h] = r;
+    }
+    __syncthreads();
+}
+
+// GQA-folded split decode for any element type and head_dim: one workgroup
+// per (split, kv head) computes the split's (m, l, O) for all G query heads
+// of the kv head, so each K/V element is read once per group (the generic
+// kernel reads it once per query head). The same two passes as
+// decode_generic (PagedAttention.h:98-118): per token the G scores, each a
+// dot product over d in order; per head the maximum; then weights, their sum
+// and the value accumulator; the generic split merge finishes. kG >= G is the
+// register width of the per-head arrays: query rows past G are zero, and
+// their scores and sums are computed but never stored.
+template <typename T, int kG>
+__global__ __launch_bounds__(kGroupedThreads) void decode_grouped(DecodeGeometry p, SplitArgs sa) {
+    extern __shared__ float smem[];
+    __shared__ float red[kGroupedWaves][kG];
+    const int G = static_cast<int>(p.group);
+    const uint32_t D = p.head_dim;
+    const uint32_t S = sa.split_tokens;
+    float* q_s = smem;           // [kG][D]
+    float* s_s = smem + kG * D;  // [kG][S]: scores, then weights
+
+    const uint32_t split = blockIdx.x / p.num_kv_heads;
+    const uint32_t g = blockIdx.x - split * p.num_kv_heads;
+    const int b = sa.split_seq[split];
+    const int start = sa.split_start[split];
+    const int ctx = p.seq_lens[b];
+    const int len = min(static_cast<int>(S), ctx - start);
+    const int32_t* row = p.tables + static_cast<uint64_t>(b) * p.max_nb;
+    const uint64_t head0 = static_cast<uint64_t>(b) * p.num_q_heads + static_cast<uint64_t>(g) * G;
+
+    const T* q = static_cast<const T*>(p.query) + head0 * D;
+    for (uint32_t e = threadIdx.x; e < kG * D; e += kGroupedThreads) {
+        q_s[e] = e < static_cast<uint32_t>(G) * D ? to_float<T>(q[e]) : 0.f;
+    }
+    __syncthreads();
+
+    const uint64_t head_off = static_cast<uint64_t>(g) * p.head_stride;
+    float mloc[kG];
+#pragma unroll
+    for (int h = 0; h < kG; ++h) mloc[h] = -INFINITY;
+    for (int t = threadIdx.x; t < len; t += kGroupedThreads) {
+        const uint32_t tok = static_cast<uint32_t>(start + t);
+        const int32_t blk = row[tok / p.tpb];
+        const T* k = reinterpret_cast<const T*>(p.kv_base + static_cast<uint64_t>(blk) * p.block_stride + p.k_off +
+                                                (tok % p.tpb) * p.token_stride + head_off);
+        float dot[kG];
+#pragma unroll
+        for (int h = 0; h < kG; ++h) dot[h] = 0.f;
+        for (uint32_t d = 0; d < D; ++d) {
+            const float kv = to_float<T>(k[d]);
+#pragma unroll
+            for (int h = 0; h < kG; ++h) dot[h] += q_s[h * D + d] * kv;
+        }
+#pragma unroll
+        for (int h = 0; h < kG; ++h) {
+            const float sv = dot[h] * p.scale_log2;
+            s_s[h * S + t] = sv;
+            mloc[h] = fmaxf(mloc[h], sv);
+        }
+    }
+    reduce_heads<kG, true>(mloc, red);
+    float lloc[kG];
+#pragma unroll
+    for (int h = 0; h < kG; ++h) lloc[h] = 0.f;
+    for (int t = threadIdx.x; t < len; t += kGroupedThreads) {
+#pragma unroll
+        for (int h = 0; h < kG; ++h) {
+            const float w = fast_exp2(s_s[h * S + t] - mloc[h]);
+            s_s[h * S + t] = w;
+            lloc[h] += w;
+        }
+    }
+    // Also orders the weight writes before the reads below.
+    reduce_heads<kG, false>(lloc, red);
+
+    float* acc_out = sa.ws_acc + static_cast<uint64_t>(split) * p.num_q_heads * D + static_cast<uint64_t>(g) * G * D;
+    auto v_at = [&](int t, uint32_t d) {
+        const uint32_t tok = static_cast<uint32_t>(start + t);
+        const int32_t blk = row[tok / p.tpb];
+        const T* v = reinterpret_cast<const T*>(p.kv_base + static_cast<uint64_t>(blk) * p.block_stride + p.v_off +
+                                                (tok % p.tpb) * p.token_stride + head_off);
+        return to_float<T>(v[d]);
+    };
+    if (D <= static_cast<uint32_t>(kGroupedThreads)) {
+        // Thread (tg, d): dim d over tokens tg, tg + ng, ...; the ng partial
+        // sums of each (head, dim) are then added in tg order.
+        const int ng = kGroupedThreads / static_cast<int>(D);
+        const int tg = static_cast<int>(threadIdx.x / D);
+        const uint32_t d = threadIdx.x - static_cast<uint32_t>(tg) * D;
+        float acc[kG];
+#pragma unroll
+        for (int h = 0; h < kG; ++h) acc[h] = 0.f;
+        if (tg < ng) {
+            for (int t = tg; t < len; t += ng) {
+                const float vv = v_at(t, d);
+#pragma unroll
+                for (int h = 0; h < kG; ++h) acc[h] += s_s[h * S + t] * vv;
+            }
+        }
+        __syncthreads();  // every weight read before the partial sums reuse the LDS
+        float* part = smem;  // [ng][kG][D]
+        if (tg < ng) {
+#pragma unroll
+            for (int h = 0; h < kG; ++h) part[(tg * kG + h) * D + d] = acc[h];
+        }
+        __syncthreads();
+        for (uint32_t e = threadIdx.x; e < static_cast<uint32_t>(G) * D; e += kGroupedThreads) {
+            const uint32_t h = e / D;
+            const uint32_t dd = e - h * D;
+            float o = 0.f;
+            for (int x = 0; x < ng; ++x) o += part[(x * kG + h) * D + dd];
+            acc_out[e] = o;
+        }
+    } else {
+        for (uint32_t d = threadIdx.x; d < D; d += kGroupedThreads) {
+            float acc[kG];
+#pragma unroll
+            for (int h = 0; h < kG; ++h) acc[h] = 0.f;
+            for (int t = 0; t < len; ++t) {
+                const float vv = v_at(t, d);
+#pragma unroll
+                for (int h = 0; h < kG; ++h) acc[h] += s_s[h * S + t] * vv;
+            }
+#pragma unroll
+            for (int h = 0; h < kG; ++h) {
+                if (h < G) acc_out[h * D + d] = acc[h];
+            }
+        }
+    }
+    float* ml = sa.ws_ml + (static_cast<uint64_t>(split) * p.num_q_heads + static_cast<uint64_t>(g) * G) * 2;
+#pragma unroll
+    for (int h = 0; h < kG; ++h) {
+        if (h < G && static_cast<int>(threadIdx.x) == h) {
+            ml[2 * h] = mloc[h];
+            ml[2 * h + 1] = lloc[h];
+        }
+    }
+}
+
+// Register width of the folded kernel's per-head arrays for a group.
+int grouped_width(uint32_t group) { return group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16; }
+
+size_t grouped_shmem(const DecodeGeometry& g, uint32_t split_tokens) {
+    const size_t kg = static_cast<size_t>(grouped_width(g.group));
+    const size_t d = g.head_dim;
+    const size_t parts = d <= kGroupedThreads ? (kGroupedThreads / d) * kg * d : 0;
+    return std::max(kg * (d + split_tokens), parts) * sizeof(float);
+}
+
+template <typename T>
+void launch_grouped_for(const DecodeGeometry& g, const SplitArgs& sa, dim3 grid, size_t shmem, hipStream_t stream) {
+    switch (grouped_width(g.group)) {
+        case 2: hipLaunchKernelGGL((decode_grouped<T, 2>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
+        case 4: hipLaunchKernelGGL((decode_grouped<T, 4>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
+        case 8: hipLaunchKernelGGL((decode_grouped<T, 8>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
+        default: hipLaunchKernelGGL((decode_grouped<T, 16>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
+    }
+}
+
 }  // namespace
+
+bool grouped_supported(const DecodeGeometry& g, uint32_t split_tokens) {
+    return g.group >= 2 && g.group <= 16 && g.head_dim >= 1 && split_tokens >= 1 &&
+           grouped_shmem(g, split_tokens) <= 64 * 1024;
+}
+
+int launch_grouped_decode(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t kv_dtype, uint32_t out_dtype,
+                          void* out, void* workspace, hipEvent_t split_event, hipStream_t stream) {
+    if (!grouped_supported(g, v.split_tokens)) {
+        return fail(QVP_ERR_INVALID_ARGUMENT, "group %u, head_dim %u, split %u: not a folded-decode shape", g.group,
+                    g.head_dim, v.split_tokens);
+    }
+    const uint64_t heads = static_cast<uint64_t>(v.num_splits) * g.num_q_heads;
+    SplitArgs sa{};
+    sa.split_seq = v.split_seq;
+    sa.split_start = v.split_start;
+    sa.split_tokens = v.split_tokens;
+    sa.ws_ml = static_cast<float*>(workspace);
+    sa.ws_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + round_up(heads * 2 * sizeof(float), 256));
+    const size_t shmem = grouped_shmem(g, v.split_tokens);
+    const dim3 grid(static_cast<unsigned>(static_cast<uint64_t>(v.num_splits) * g.num_kv_heads));
+    switch (kv_dtype) {
+        case QVP_DTYPE_F32: launch_grouped_for<float>(g, sa, grid, shmem, stream); break;
+        case QVP_DTYPE_BF16: launch_grouped_for<uint16_t>(g, sa, grid, shmem, stream); break;
+        default: launch_grouped_for<_Float16>(g, sa, grid, shmem, stream); break;
+    }
+    QVP_HIP(hipGetLastError());
+    if (split_event != nullptr) QVP_HIP(hipEventRecord(split_event, stream));
+    return launch_merge_splits(g, v, out_dtype, out, sa.ws_ml, sa.ws_acc, stream);
+}
 
 uint64_t generic_workspace_bytes(const qvp_packed_view& v, uint32_t hq, uint32_t d) {
     const uint64_t heads = static_cast<uint64_t>(v.num_splits) * hq;

@@ -6,9 +6,10 @@
 // ones a device kernel needs (the layout stays inside a frame, buffers are
 // large enough); the packer already refused unmapped or swapped blocks
 // (:73-89). Only then is anything enqueued, so a refused call leaves `out`
-// untouched. bf16 caches with head_dim 128 run the persistent MFMA kernel
-// (decode_mfma.hip); everything else runs the generic kernel
-// (decode_generic.hip).
+// untouched. bf16, fp16 and fp32 caches with head_dim 128 run the persistent
+// MFMA kernel (decode_mfma.hip); other shapes run a split kernel: the fp32
+// MFMA one (decode_f32.hip), the GQA-folded one for groups of 2 .. 16, or the
+// per-query-head generic one (both in decode_generic.hip).
 #include "decode_common.h"
 
 #include <algorithm>
@@ -276,10 +277,12 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         const bool f32 = qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens,
                                                     reinterpret_cast<uintptr_t>(a->query),
                                                     reinterpret_cast<uintptr_t>(a->kv_base));
-        status = f32 ? qvp::launch_f32_grouped_decode(g, v, a->out_dtype, a->out, ws, ev, s)
-                     : qvp::launch_generic_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s);
-        plan.kernel = f32 ? QVP_DECODE_F32_GROUPED : QVP_DECODE_GENERIC;
-        plan.workgroups = v.num_splits * (f32 ? a->num_kv_heads : a->num_query_heads);
+        const bool grouped = !f32 && qvp::grouped_supported(g, v.split_tokens);
+        status = f32       ? qvp::launch_f32_grouped_decode(g, v, a->out_dtype, a->out, ws, ev, s)
+                 : grouped ? qvp::launch_grouped_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s)
+                           : qvp::launch_generic_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s);
+        plan.kernel = f32 ? QVP_DECODE_F32_GROUPED : grouped ? QVP_DECODE_GROUPED : QVP_DECODE_GENERIC;
+        plan.workgroups = v.num_splits * (f32 || grouped ? a->num_kv_heads : a->num_query_heads);
         plan.pieces = v.num_splits;
         plan.slots = v.num_splits;
         plan.kv_heads_per_segment = 1;

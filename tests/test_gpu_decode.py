@@ -44,16 +44,61 @@ def test_config1_fp32_matches_oracle():
     _parity(W.config1())
 
 
+# Hq, Hkv, D for the GQA-folded split kernel: groups of 2 .. 16 (register
+# widths 2, 4, 8 and 16), head dims below, at and above its 256 threads.
+FOLDED_SHAPES = [(8, 2, 64), (28, 4, 80), (12, 4, 256), (10, 5, 32), (48, 3, 96), (4, 2, 320)]
+
+
+@pytest.mark.parametrize("kv_dtype", [qvp.DTYPE_F32, qvp.DTYPE_BF16, qvp.DTYPE_F16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", FOLDED_SHAPES, ids=[f"hq{a}-hkv{b}-d{c}" for a, b, c in FOLDED_SHAPES])
+def test_gqa_folded_split_kernel_matches_the_oracle(shape, kv_dtype):
+    """Head dims other than 128 (and the element types the reference template
+    takes) run one workgroup per (split, kv head) for the whole query group:
+    each K/V element is read once per group. Same bars as every decode."""
+    hq, hkv, d = shape
+    print(f"case: folded split decode hq={hq} hkv={hkv} d={d} kv_dtype={kv_dtype}", flush=True)
+    w = W.custom([37, 300, 777, 1025], hq, hkv, d, kv_dtype=kv_dtype, seed=hq + d)
+    run = GpuRun(w)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    plan = run.batch.decode_plan()
+    assert plan["kernel"] == "grouped", plan
+    assert plan["workgroups"] == plan["pieces"] * hkv, plan
+    if kv_dtype == qvp.DTYPE_F32:
+        err = float(np.abs(got - ref32).max())
+        assert err <= F32_ABS_TOL, f"fp32 max abs {err:.3e}"
+    else:
+        assert_close_bf16(got, ref32, f"folded {shape} fp32 out")
+        got16 = run.decode(out_dtype=kv_dtype)
+        assert_close_16bit(got16, ref32, kv_dtype, f"folded {shape} 16-bit out")
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (34, 2)], ids=["group-1", "group-17"])
+def test_groups_outside_2_to_16_run_the_per_head_split_kernel(hq, hkv):
+    print(f"case: per-head split decode hq={hq} hkv={hkv}", flush=True)
+    w = W.custom([90, 600, 1300], hq, hkv, 64, seed=hq)
+    run = GpuRun(w)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    plan = run.batch.decode_plan()
+    assert plan["kernel"] == "generic", plan
+    assert plan["workgroups"] == plan["pieces"] * hq, plan
+    assert_close_bf16(got, ref32, f"per-head hq={hq} hkv={hkv}")
+
+
 def test_config2_bf16_matches_oracle_fp32_and_bf16_outputs():
     print("case: config2 bf16 B=64", flush=True)
     _parity(W.config2(), out_dtypes=(qvp.DTYPE_F32, qvp.DTYPE_BF16))
 
 
 @pytest.mark.parametrize("split", [128, 256, 512, 1024, 4096])
-@pytest.mark.parametrize("kv_dtype", [qvp.DTYPE_F32, qvp.DTYPE_F16], ids=["f32-grouped", "generic-f16"])
+@pytest.mark.parametrize("kv_dtype", [qvp.DTYPE_F32, qvp.DTYPE_F16], ids=["f32-grouped", "split-f16"])
 def test_split_kernels_follow_the_split_size(kv_dtype, split):
-    """The fp32 and generic kernels partition each sequence into split_tokens
-    pieces and merge them; every partition size gives the oracle's result."""
+    """The split kernels partition each sequence into split_tokens pieces and
+    merge them; every partition size gives the oracle's result. The fp16 case
+    (group 7, head_dim 64) runs the GQA-folded kernel while its scores fit in
+    64 KiB of LDS (register width 8 x (64 + split) floats) and the per-head
+    generic kernel beyond."""
     print(f"case: split kernels dtype={kv_dtype} split={split}", flush=True)
     lens = [37, 600, 1500, 4096, 129, 2049]
     if kv_dtype == qvp.DTYPE_F32:
@@ -71,7 +116,8 @@ def test_split_kernels_follow_the_split_size(kv_dtype, split):
     _, ref32 = oracle_decode(w, run.image, run.query)
     got = run.decode(out_dtype=qvp.DTYPE_F32, split_tokens=split)
     plan = run.batch.decode_plan()
-    assert plan["kernel"] == ("f32_grouped" if kv_dtype == qvp.DTYPE_F32 else "generic"), plan
+    folded = 8 * (64 + split) * 4 <= 64 * 1024
+    assert plan["kernel"] == ("f32_grouped" if kv_dtype == qvp.DTYPE_F32 else "grouped" if folded else "generic"), plan
     assert plan["split_tokens"] == split, plan
     expect_splits = int(sum(-(-int(n) // split) for n in lens))
     assert plan["pieces"] == expect_splits, plan
@@ -161,12 +207,13 @@ def test_ragged_lengths_across_block_and_split_edges(kv_dtype):
 def test_any_softmax_scale(scale):
     """The persistent kernel takes its running maximum on raw scores, which
     holds for scale > 0; a zero or negative scale (uniform weights, reversed
-    order of the scores) runs on the generic kernel. Both match the oracle."""
+    order of the scores) runs on a split kernel (the GQA-folded one for this
+    group of 7). Both match the oracle."""
     print(f"case: scale {scale}", flush=True)
     w = W.custom([70, 300, 513, 2000], 28, 4, 128, seed=19, scale=scale)
     run = GpuRun(w)
     got = run.decode(out_dtype=qvp.DTYPE_F32)
-    assert run.batch.decode_plan()["kernel"] == ("mfma" if scale > 0 else "generic")
+    assert run.batch.decode_plan()["kernel"] == ("mfma" if scale > 0 else "grouped")
     _, ref32 = oracle_decode(w, run.image, run.query)
     assert_close_bf16(got, ref32, f"scale {scale}")
 
@@ -380,8 +427,8 @@ def test_multi_layer_frames_read_only_the_requested_layer():
         _parity(w, out_dtypes=(qvp.DTYPE_F32,))
 
 
-def test_fp16_cache_generic_path():
-    print("case: fp16 cache, head_dim 96 (generic kernel)", flush=True)
+def test_fp16_cache_folded_split_path():
+    print("case: fp16 cache, head_dim 96 (GQA-folded split kernel)", flush=True)
     w = W.custom([50, 130], 8, 2, 96, kv_dtype=qvp.DTYPE_F16, seed=3)
     # fp16 pool: reinterpret the fp32 draws rounded to fp16.
     image32 = W.custom([50, 130], 8, 2, 96, kv_dtype=qvp.DTYPE_F32, seed=3)
@@ -391,7 +438,7 @@ def test_fp16_cache_generic_path():
     run = GpuRun(w, image=image, query=q)
     _, ref32 = oracle_decode(w, image, q)
     got = run.decode(out_dtype=qvp.DTYPE_F32)
-    assert run.batch.decode_plan()["kernel"] == "generic"
+    assert run.batch.decode_plan()["kernel"] == "grouped"
     assert_close_bf16(got, ref32, "fp16 cache")
 
 
