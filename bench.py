@@ -594,18 +594,21 @@ def swap_bench(steps: int, warmup: int) -> int:
     return 0
 
 
-def dtype_bench(kv_dtype: int, steps: int, warmup: int, pools_n: int, cpu_reps: int, with_cpu: bool) -> int:
-    """The config2 batch (same 64 context lengths, Hq28/Hkv4/D128, block 16)
-    with an fp32 or fp16 cache -- the reference's paged_attention_decode<T>
-    for T = float or a two-byte half -- on the persistent matrix-core decode
-    (fp32 or f16 MFMA tiles; free cost-balanced cuts as in the headline);
-    `pools_n` pool copies rotate between steps. One step = one decode call;
-    the kernel's average launch duration is two HIP events around the K
-    steps, over K."""
-    name = "fp32" if kv_dtype == qvp.DTYPE_F32 else "fp16"
+def dtype_bench(kv_dtype: int, steps: int, warmup: int, pools_n: int, cpu_reps: int, with_cpu: bool,
+                head_dim: int = 128) -> int:
+    """The config2 batch (same 64 context lengths, Hq28/Hkv4, block 16) with
+    an fp32 or fp16 cache -- the reference's paged_attention_decode<T> for T =
+    float or a two-byte half -- on the persistent matrix-core decode (fp32 or
+    f16 MFMA tiles; free cost-balanced cuts as in the headline), or at another
+    head_dim (any element type) on the GQA-folded split decode; `pools_n`
+    pool copies rotate between steps. One step = one decode call; the
+    kernel's average launch duration is two HIP events around the K steps,
+    over K (for the split decode: its split kernel and the merge)."""
+    name = {qvp.DTYPE_F32: "fp32", qvp.DTYPE_F16: "fp16"}.get(kv_dtype, "bf16")
     c2 = W.config2()
-    w = W.custom(list(c2.context_lens), 28, 4, 128, kv_dtype=kv_dtype, seed=2, spare=0.1)
-    w.name = f"config2-shape {name}"
+    D = head_dim
+    w = W.custom(list(c2.context_lens), 28, 4, D, kv_dtype=kv_dtype, seed=2, spare=0.1)
+    w.name = f"config2-shape {name}" + (f" head_dim {D}" if D != 128 else "")
     rng = np.random.default_rng(2)
     chunk = W.to_elements(rng.normal(0, 0.5, 16_777_259).astype(np.float32), kv_dtype)
     total = w.num_pool_blocks * w.block_stride // chunk.itemsize
@@ -617,14 +620,14 @@ def dtype_bench(kv_dtype: int, steps: int, warmup: int, pools_n: int, cpu_reps: 
         pool.upload_all(image)
         pools.append(pool)
     q = qvp.DeviceBuffer.from_array(query)
-    out = qvp.DeviceBuffer(w.num_seqs * 28 * 128 * 4)
+    out = qvp.DeviceBuffer(w.num_seqs * 28 * D * 4)
     stream = qvp.Stream()
     batch = qvp.Batch()
     batch.pack(w.ids, w.cu_blocks, w.context_lens, 16, w.num_pool_blocks, 0, stream)
-    ws = qvp.DeviceBuffer(batch.workspace_bytes(28, 128))
+    ws = qvp.DeviceBuffer(batch.workspace_bytes(28, D))
     args = [qvp.decode_args(query=q.ptr, out=out.ptr, kv_base=pool.base, block_stride=pool.stride, batch=batch,
                             kv_dtype=kv_dtype, out_dtype=qvp.DTYPE_F32, layer=0, num_layers=1,
-                            num_query_heads=28, num_kv_heads=4, head_dim=128, tokens_per_block=16, scale=w.scale,
+                            num_query_heads=28, num_kv_heads=4, head_dim=D, tokens_per_block=16, scale=w.scale,
                             workspace=ws.ptr, workspace_bytes=ws.nbytes) for pool in pools]
     for i in range(max(warmup, 200)):
         qvp.paged_decode(args[i % len(args)], stream)
@@ -738,6 +741,9 @@ def main() -> int:
     ap.add_argument("--copy", action="store_true", help="time copy_blocks of 128 frame pairs at 7B frame sizes")
     ap.add_argument("--fp32", action="store_true", help="time the config2 batch with an fp32 cache")
     ap.add_argument("--fp16", action="store_true", help="time the config2 batch with an fp16 cache")
+    ap.add_argument("--head-dim", type=int, default=128,
+                    help="time the config2 batch at this head dim (bf16 unless --fp16/--fp32; not 128: the "
+                         "GQA-folded split decode)")
     ap.add_argument("--tiles", action="store_true",
                     help="time matrix-core against vector-ALU decode tiles at GQA groups 1, 2 and 7")
     ap.add_argument("--torch-sdpa", action="store_true", help=argparse.SUPPRESS)
@@ -763,9 +769,9 @@ def main() -> int:
         return mrope_bench(args.steps, args.warmup, not args.no_cpu)
     if args.swap:
         return swap_bench(args.steps, args.warmup)
-    if args.fp32 or args.fp16:
-        return dtype_bench(qvp.DTYPE_F32 if args.fp32 else qvp.DTYPE_F16, args.steps, args.warmup, args.pools,
-                           args.cpu_reps, not args.no_cpu)
+    if args.fp32 or args.fp16 or args.head_dim != 128:
+        kv = qvp.DTYPE_F32 if args.fp32 else qvp.DTYPE_F16 if args.fp16 else qvp.DTYPE_BF16
+        return dtype_bench(kv, args.steps, args.warmup, args.pools, args.cpu_reps, not args.no_cpu, args.head_dim)
     if args.tiles:
         return tiles_bench(args.steps, args.warmup, args.pools)
     if args.torch_sdpa:
