@@ -163,14 +163,39 @@ __device__ inline void reduce_heads(float (&v)[kG], float (*red)[kG]) {
     __syncthreads();
 }
 
-// GQA-folded split decode for any element type and head_dim: one workgroup
-// per (split, kv head) computes the split's (m, l, O) for all G query heads
-// of the kv head, so each K/V element is read once per group (the generic
-// kernel reads it once per query head). The same two passes as
-// decode_generic (PagedAttention.h:98-118): per token the G scores, each a
-// dot product over d in order; per head the maximum; then weights, their sum
-// and the value accumulator; the generic split merge finishes. kG >= G is the
-// register width of the per-head arrays: query rows past G are zero, and
+// Four consecutive elements of a K or V row as floats (the row offset is a
+// multiple of four elements and the address of four elements' bytes).
+template <typename T>
+__device__ inline float4 load4(const T* ptr);
+template <>
+__device__ inline float4 load4<float>(const float* ptr) {
+    return *reinterpret_cast<const float4*>(ptr);
+}
+template <>
+__device__ inline float4 load4<uint16_t>(const uint16_t* ptr) {
+    const uint2 r = *reinterpret_cast<const uint2*>(ptr);
+    return float4{bf16_bits_to_float(static_cast<uint16_t>(r.x & 0xffffu)), bf16_bits_to_float(static_cast<uint16_t>(r.x >> 16)),
+                  bf16_bits_to_float(static_cast<uint16_t>(r.y & 0xffffu)), bf16_bits_to_float(static_cast<uint16_t>(r.y >> 16))};
+}
+template <>
+__device__ inline float4 load4<_Float16>(const _Float16* ptr) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 r = *reinterpret_cast<const h4*>(ptr);
+    return float4{static_cast<float>(r[0]), static_cast<float>(r[1]), static_cast<float>(r[2]), static_cast<float>(r[3])};
+}
+
+// GQA-folded split decode for any element type and head_dim (a multiple of
+// four, rows aligned to four elements): one workgroup per (split, kv head)
+// computes the split's (m, l, O) for all G query heads of the kv head, so
+// each K/V element is read once per group (the generic kernel reads it once
+// per query head). The same two passes as decode_generic
+// (PagedAttention.h:98-118): per token the G scores, each a dot product over
+// d in order (four elements per load, the query rows read four floats at a
+// time from LDS); per head the maximum; then weights, their sum and the value
+// accumulator, each thread holding four dims of all heads over a contiguous
+// run of tokens (weights read four tokens at a time); the runs' partial sums
+// are added in run order and the generic split merge finishes. kG >= G is
+// the register width of the per-head arrays: query rows past G are zero, and
 // their scores and sums are computed but never stored.
 template <typename T, int kG>
 __global__ __launch_bounds__(kGroupedThreads) void decode_grouped(DecodeGeometry p, SplitArgs sa) {
@@ -198,21 +223,30 @@ __global__ __launch_bounds__(kGroupedThreads) void decode_grouped(DecodeGeometry
     __syncthreads();
 
     const uint64_t head_off = static_cast<uint64_t>(g) * p.head_stride;
+    auto row_of = [&](int t, uint64_t off) {
+        const uint32_t tok = static_cast<uint32_t>(start + t);
+        const int32_t blk = row[tok / p.tpb];
+        return reinterpret_cast<const T*>(p.kv_base + static_cast<uint64_t>(blk) * p.block_stride + off +
+                                          (tok % p.tpb) * p.token_stride + head_off);
+    };
     float mloc[kG];
 #pragma unroll
     for (int h = 0; h < kG; ++h) mloc[h] = -INFINITY;
     for (int t = threadIdx.x; t < len; t += kGroupedThreads) {
-        const uint32_t tok = static_cast<uint32_t>(start + t);
-        const int32_t blk = row[tok / p.tpb];
-        const T* k = reinterpret_cast<const T*>(p.kv_base + static_cast<uint64_t>(blk) * p.block_stride + p.k_off +
-                                                (tok % p.tpb) * p.token_stride + head_off);
+        const T* k = row_of(t, p.k_off);
         float dot[kG];
 #pragma unroll
         for (int h = 0; h < kG; ++h) dot[h] = 0.f;
-        for (uint32_t d = 0; d < D; ++d) {
-            const float kv = to_float<T>(k[d]);
+        for (uint32_t d = 0; d < D; d += 4) {
+            const float4 kv = load4<T>(k + d);
 #pragma unroll
-            for (int h = 0; h < kG; ++h) dot[h] += q_s[h * D + d] * kv;
+            for (int h = 0; h < kG; ++h) {
+                const float4 qv = *reinterpret_cast<const float4*>(&q_s[h * D + d]);
+                dot[h] = fmaf(qv.x, kv.x, dot[h]);
+                dot[h] = fmaf(qv.y, kv.y, dot[h]);
+                dot[h] = fmaf(qv.z, kv.z, dot[h]);
+                dot[h] = fmaf(qv.w, kv.w, dot[h]);
+            }
         }
 #pragma unroll
         for (int h = 0; h < kG; ++h) {
@@ -236,59 +270,67 @@ __global__ __launch_bounds__(kGroupedThreads) void decode_grouped(DecodeGeometry
     // Also orders the weight writes before the reads below.
     reduce_heads<kG, false>(lloc, red);
 
-    float* acc_out = sa.ws_acc + static_cast<uint64_t>(split) * p.num_q_heads * D + static_cast<uint64_t>(g) * G * D;
-    auto v_at = [&](int t, uint32_t d) {
-        const uint32_t tok = static_cast<uint32_t>(start + t);
-        const int32_t blk = row[tok / p.tpb];
-        const T* v = reinterpret_cast<const T*>(p.kv_base + static_cast<uint64_t>(blk) * p.block_stride + p.v_off +
-                                                (tok % p.tpb) * p.token_stride + head_off);
-        return to_float<T>(v[d]);
-    };
-    if (D <= static_cast<uint32_t>(kGroupedThreads)) {
-        // Thread (tg, d): dim d over tokens tg, tg + ng, ...; the ng partial
-        // sums of each (head, dim) are then added in tg order.
-        const int ng = kGroupedThreads / static_cast<int>(D);
-        const int tg = static_cast<int>(threadIdx.x / D);
-        const uint32_t d = threadIdx.x - static_cast<uint32_t>(tg) * D;
-        float acc[kG];
+    // Thread (run r, chunk c): dims 4c .. 4c + 3 over tokens [r * run,
+    // min(len, (r + 1) * run)), run a multiple of four tokens.
+    const int chunks = static_cast<int>(D / 4);
+    const int runs = kGroupedThreads / chunks;
+    const int r = static_cast<int>(threadIdx.x) / chunks;
+    const int c4 = 4 * (static_cast<int>(threadIdx.x) - r * chunks);
+    const int run = (((len + runs - 1) / runs) + 3) & ~3;
+    float acc[kG][4];
 #pragma unroll
-        for (int h = 0; h < kG; ++h) acc[h] = 0.f;
-        if (tg < ng) {
-            for (int t = tg; t < len; t += ng) {
-                const float vv = v_at(t, d);
+    for (int h = 0; h < kG; ++h)
 #pragma unroll
-                for (int h = 0; h < kG; ++h) acc[h] += s_s[h * S + t] * vv;
-            }
-        }
-        __syncthreads();  // every weight read before the partial sums reuse the LDS
-        float* part = smem;  // [ng][kG][D]
-        if (tg < ng) {
+        for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
+    if (r < runs) {
+        const int t0 = r * run;
+        const int t1 = min(len, t0 + run);
+        int t = t0;
+        for (; t + 4 <= t1; t += 4) {
+            float4 vv[4];
 #pragma unroll
-            for (int h = 0; h < kG; ++h) part[(tg * kG + h) * D + d] = acc[h];
-        }
-        __syncthreads();
-        for (uint32_t e = threadIdx.x; e < static_cast<uint32_t>(G) * D; e += kGroupedThreads) {
-            const uint32_t h = e / D;
-            const uint32_t dd = e - h * D;
-            float o = 0.f;
-            for (int x = 0; x < ng; ++x) o += part[(x * kG + h) * D + dd];
-            acc_out[e] = o;
-        }
-    } else {
-        for (uint32_t d = threadIdx.x; d < D; d += kGroupedThreads) {
-            float acc[kG];
-#pragma unroll
-            for (int h = 0; h < kG; ++h) acc[h] = 0.f;
-            for (int t = 0; t < len; ++t) {
-                const float vv = v_at(t, d);
-#pragma unroll
-                for (int h = 0; h < kG; ++h) acc[h] += s_s[h * S + t] * vv;
-            }
+            for (int u = 0; u < 4; ++u) vv[u] = load4<T>(row_of(t + u, p.v_off) + c4);
 #pragma unroll
             for (int h = 0; h < kG; ++h) {
-                if (h < G) acc_out[h * D + d] = acc[h];
+                const float4 w = *reinterpret_cast<const float4*>(&s_s[h * S + t]);
+                const float wu[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc[h][0] = fmaf(wu[u], vv[u].x, acc[h][0]);
+                    acc[h][1] = fmaf(wu[u], vv[u].y, acc[h][1]);
+                    acc[h][2] = fmaf(wu[u], vv[u].z, acc[h][2]);
+                    acc[h][3] = fmaf(wu[u], vv[u].w, acc[h][3]);
+                }
             }
         }
+        for (; t < t1; ++t) {
+            const float4 vv = load4<T>(row_of(t, p.v_off) + c4);
+#pragma unroll
+            for (int h = 0; h < kG; ++h) {
+                const float w = s_s[h * S + t];
+                acc[h][0] = fmaf(w, vv.x, acc[h][0]);
+                acc[h][1] = fmaf(w, vv.y, acc[h][1]);
+                acc[h][2] = fmaf(w, vv.z, acc[h][2]);
+                acc[h][3] = fmaf(w, vv.w, acc[h][3]);
+            }
+        }
+    }
+    __syncthreads();  // every weight read before the partial sums reuse the LDS
+    float* part = smem;  // [runs][kG][D]
+    if (r < runs) {
+#pragma unroll
+        for (int h = 0; h < kG; ++h) {
+            *reinterpret_cast<float4*>(&part[(r * kG + h) * D + c4]) = float4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+        }
+    }
+    __syncthreads();
+    float* acc_out = sa.ws_acc + static_cast<uint64_t>(split) * p.num_q_heads * D + static_cast<uint64_t>(g) * G * D;
+    for (uint32_t e = threadIdx.x; e < static_cast<uint32_t>(G) * D; e += kGroupedThreads) {
+        const uint32_t h = e / D;
+        const uint32_t dd = e - h * D;
+        float o = 0.f;
+        for (int x = 0; x < runs; ++x) o += part[(x * kG + h) * D + dd];
+        acc_out[e] = o;
     }
     float* ml = sa.ws_ml + (static_cast<uint64_t>(split) * p.num_q_heads + static_cast<uint64_t>(g) * G) * 2;
 #pragma unroll
@@ -303,11 +345,13 @@ __global__ __launch_bounds__(kGroupedThreads) void decode_grouped(DecodeGeometry
 // Register width of the folded kernel's per-head arrays for a group.
 int grouped_width(uint32_t group) { return group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16; }
 
+// LDS of the folded kernel: query rows and scores, later the runs' partial
+// sums ((256 / (D / 4)) runs x kG x D floats).
 size_t grouped_shmem(const DecodeGeometry& g, uint32_t split_tokens) {
     const size_t kg = static_cast<size_t>(grouped_width(g.group));
     const size_t d = g.head_dim;
-    const size_t parts = d <= kGroupedThreads ? (kGroupedThreads / d) * kg * d : 0;
-    return std::max(kg * (d + split_tokens), parts) * sizeof(float);
+    const size_t runs = d >= 4 ? kGroupedThreads / (d / 4) : 0;
+    return std::max(kg * (d + split_tokens), runs * kg * d) * sizeof(float);
 }
 
 template <typename T>
@@ -322,14 +366,21 @@ void launch_grouped_for(const DecodeGeometry& g, const SplitArgs& sa, dim3 grid,
 
 }  // namespace
 
-bool grouped_supported(const DecodeGeometry& g, uint32_t split_tokens) {
-    return g.group >= 2 && g.group <= 16 && g.head_dim >= 1 && split_tokens >= 1 &&
+bool grouped_supported(const DecodeGeometry& g, uint32_t kv_dtype, uint32_t split_tokens) {
+    // Four-element K/V loads: rows, frames and the pool aligned to four
+    // elements; head_dim a multiple of four with at most 256 four-dim chunks;
+    // weights read four tokens at a time (splits of a multiple of four).
+    const uint64_t a = 4ull * (kv_dtype == QVP_DTYPE_F32 ? 4 : 2);
+    const bool aligned = g.token_stride % a == 0 && g.head_stride % a == 0 && g.block_stride % a == 0 &&
+                         g.k_off % a == 0 && g.v_off % a == 0 && reinterpret_cast<uintptr_t>(g.kv_base) % a == 0;
+    return g.group >= 2 && g.group <= 16 && g.head_dim % 4 == 0 && g.head_dim >= 4 &&
+           g.head_dim <= 4 * kGroupedThreads && split_tokens >= 4 && split_tokens % 4 == 0 && aligned &&
            grouped_shmem(g, split_tokens) <= 64 * 1024;
 }
 
 int launch_grouped_decode(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t kv_dtype, uint32_t out_dtype,
                           void* out, void* workspace, hipEvent_t split_event, hipStream_t stream) {
-    if (!grouped_supported(g, v.split_tokens)) {
+    if (!grouped_supported(g, kv_dtype, v.split_tokens)) {
         return fail(QVP_ERR_INVALID_ARGUMENT, "group %u, head_dim %u, split %u: not a folded-decode shape", g.group,
                     g.head_dim, v.split_tokens);
     }

@@ -277,7 +277,7 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         const bool f32 = qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens,
                                                     reinterpret_cast<uintptr_t>(a->query),
                                                     reinterpret_cast<uintptr_t>(a->kv_base));
-        const bool grouped = !f32 && qvp::grouped_supported(g, v.split_tokens);
+        const bool grouped = !f32 && qvp::grouped_supported(g, a->kv_dtype, v.split_tokens);
         status = f32       ? qvp::launch_f32_grouped_decode(g, v, a->out_dtype, a->out, ws, ev, s)
                  : grouped ? qvp::launch_grouped_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s)
                            : qvp::launch_generic_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s);
