@@ -62,7 +62,7 @@ int launch_generic_decode(const DecodeGeometry& g, const qvp_packed_view& v, uin
                           uint32_t out_dtype, void* out, void* workspace, hipEvent_t split_event,
                           hipStream_t stream);
 uint64_t generic_workspace_bytes(const qvp_packed_view& v, uint32_t hq, uint32_t d);
-// GQA-folded split decode (groups of 2 .. 16, any element type, head_dim a
+// GQA-folded split decode (groups of 1 .. 16, any element type, head_dim a
 // multiple of four up to 1024 with rows aligned to four elements, its LDS
 // within 64 KiB): one workgroup per (split, kv head), the generic workspace
 // layout and merge. Returns a qvp_status.

@@ -343,7 +343,7 @@ __global__ __launch_bounds__(kGroupedThreads) void decode_grouped(DecodeGeometry
 }
 
 // Register width of the folded kernel's per-head arrays for a group.
-int grouped_width(uint32_t group) { return group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16; }
+int grouped_width(uint32_t group) { return group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : group <= 8 ? 8 : 16; }
 
 // LDS of the folded kernel: query rows and scores, later the runs' partial
 // sums ((256 / (D / 4)) runs x kG x D floats).
@@ -357,6 +357,7 @@ size_t grouped_shmem(const DecodeGeometry& g, uint32_t split_tokens) {
 template <typename T>
 void launch_grouped_for(const DecodeGeometry& g, const SplitArgs& sa, dim3 grid, size_t shmem, hipStream_t stream) {
     switch (grouped_width(g.group)) {
+        case 1: hipLaunchKernelGGL((decode_grouped<T, 1>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
         case 2: hipLaunchKernelGGL((decode_grouped<T, 2>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
         case 4: hipLaunchKernelGGL((decode_grouped<T, 4>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
         case 8: hipLaunchKernelGGL((decode_grouped<T, 8>), grid, dim3(kGroupedThreads), shmem, stream, g, sa); break;
@@ -373,7 +374,7 @@ bool grouped_supported(const DecodeGeometry& g, uint32_t kv_dtype, uint32_t spli
     const uint64_t a = 4ull * (kv_dtype == QVP_DTYPE_F32 ? 4 : 2);
     const bool aligned = g.token_stride % a == 0 && g.head_stride % a == 0 && g.block_stride % a == 0 &&
                          g.k_off % a == 0 && g.v_off % a == 0 && reinterpret_cast<uintptr_t>(g.kv_base) % a == 0;
-    return g.group >= 2 && g.group <= 16 && g.head_dim % 4 == 0 && g.head_dim >= 4 &&
+    return g.group >= 1 && g.group <= 16 && g.head_dim % 4 == 0 && g.head_dim >= 4 &&
            g.head_dim <= 4 * kGroupedThreads && split_tokens >= 4 && split_tokens % 4 == 0 && aligned &&
            grouped_shmem(g, split_tokens) <= 64 * 1024;
 }

@@ -8,8 +8,9 @@
 // (:73-89). Only then is anything enqueued, so a refused call leaves `out`
 // untouched. bf16, fp16 and fp32 caches with head_dim 128 run the persistent
 // MFMA kernel (decode_mfma.hip); other shapes run a split kernel: the fp32
-// MFMA one (decode_f32.hip), the GQA-folded one for groups of 2 .. 16, or the
-// per-query-head generic one (both in decode_generic.hip).
+// MFMA one (decode_f32.hip), the GQA-folded one for groups up to 16 with
+// four-element rows, or the per-query-head generic one (both in
+// decode_generic.hip).
 #include "decode_common.h"
 
 #include <algorithm>

@@ -44,9 +44,9 @@ def test_config1_fp32_matches_oracle():
     _parity(W.config1())
 
 
-# Hq, Hkv, D for the GQA-folded split kernel: groups of 2 .. 16 (register
-# widths 2, 4, 8 and 16), head dims below, at and above its 256 threads.
-FOLDED_SHAPES = [(8, 2, 64), (28, 4, 80), (12, 4, 256), (10, 5, 32), (48, 3, 96), (4, 2, 320)]
+# Hq, Hkv, D for the GQA-folded split kernel: groups of 1 .. 16 (register
+# widths 1, 2, 4, 8 and 16), head dims below, at and above its 256 threads.
+FOLDED_SHAPES = [(8, 2, 64), (28, 4, 80), (12, 4, 256), (10, 5, 32), (48, 3, 96), (4, 2, 320), (8, 8, 64)]
 
 
 @pytest.mark.parametrize("kv_dtype", [qvp.DTYPE_F32, qvp.DTYPE_BF16, qvp.DTYPE_F16], ids=["f32", "bf16", "f16"])
@@ -73,10 +73,12 @@ def test_gqa_folded_split_kernel_matches_the_oracle(shape, kv_dtype):
         assert_close_16bit(got16, ref32, kv_dtype, f"folded {shape} 16-bit out")
 
 
-@pytest.mark.parametrize("hq,hkv", [(8, 8), (34, 2)], ids=["group-1", "group-17"])
-def test_groups_outside_2_to_16_run_the_per_head_split_kernel(hq, hkv):
-    print(f"case: per-head split decode hq={hq} hkv={hkv}", flush=True)
-    w = W.custom([90, 600, 1300], hq, hkv, 64, seed=hq)
+@pytest.mark.parametrize("hq,hkv,d", [(34, 2, 64), (28, 4, 66)], ids=["group-17", "head-dim-66"])
+def test_other_split_shapes_run_the_per_head_split_kernel(hq, hkv, d):
+    # A group above 16, or rows that four-element loads cannot read (head_dim
+    # 66: 132-byte bf16 rows), take the per-query-head kernel.
+    print(f"case: per-head split decode hq={hq} hkv={hkv} d={d}", flush=True)
+    w = W.custom([90, 600, 1300], hq, hkv, d, seed=hq + d)
     run = GpuRun(w)
     _, ref32 = oracle_decode(w, run.image, run.query)
     got = run.decode(out_dtype=qvp.DTYPE_F32)

@@ -92,8 +92,8 @@ def test_noalloc_matches_the_allocating_decode_on_two_calls_the_second_smaller()
 def test_noalloc_on_the_split_kernels_two_calls_the_second_smaller(kernel):
     # fp32 caches with a negative scale take the fp32 split kernel (the
     # persistent decode takes positive scales); head_dim 64 takes the
-    # GQA-folded split kernel, or with one query head per kv head the
-    # per-head generic one.
+    # GQA-folded split kernel, or at head_dim 66 (rows four-element loads
+    # cannot read) the per-head generic one.
     for i, lens in enumerate(([37, 600, 1500, 4096, 129, 2049], [90, 700])):
         print(f"case: noalloc {kernel} call {i + 1}, lens={lens}", flush=True)
         if kernel == "f32_grouped":
@@ -101,7 +101,7 @@ def test_noalloc_on_the_split_kernels_two_calls_the_second_smaller(kernel):
         elif kernel == "grouped":
             w = W.custom(lens, 28, 4, 64, seed=50 + i)
         else:
-            w = W.custom(lens, 8, 8, 64, seed=60 + i)
+            w = W.custom(lens, 28, 4, 66, seed=60 + i)
         run = GpuRun(w)
         ref, got = _both(run, hinted=False)
         assert run.batch.decode_plan()["kernel"] == kernel
