@@ -783,7 +783,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build measures one GPU; the decode shards by sequence or kv head "
-                                   "with no exchange (see DESIGN.md), and multi-GPU runs are not part of it",
+                                   "with no exchange between GPUs, and multi-GPU runs are not part of it",
                           "n_gpus": args.gpus}))
         return 2
 
