@@ -73,6 +73,19 @@ def test_gqa_folded_split_kernel_matches_the_oracle(shape, kv_dtype):
         assert_close_16bit(got16, ref32, kv_dtype, f"folded {shape} 16-bit out")
 
 
+@pytest.mark.parametrize("tpb", [8, 12, 32])
+def test_gqa_folded_split_kernel_with_other_block_sizes(tpb):
+    # Frames are found per token (tok / tpb, tok % tpb), so blocks smaller
+    # than, not a power of two, or larger than 16 tokens read the same rows.
+    print(f"case: folded split decode tpb={tpb}", flush=True)
+    w = W.custom([37, 300, 777, 1025], 28, 4, 64, tokens_per_block=tpb, seed=tpb)
+    run = GpuRun(w)
+    _, ref32 = oracle_decode(w, run.image, run.query)
+    got = run.decode(out_dtype=qvp.DTYPE_F32)
+    assert run.batch.decode_plan()["kernel"] == "grouped"
+    assert_close_bf16(got, ref32, f"folded tpb={tpb}")
+
+
 @pytest.mark.parametrize("hq,hkv,d", [(34, 2, 64), (28, 4, 66)], ids=["group-17", "head-dim-66"])
 def test_other_split_shapes_run_the_per_head_split_kernel(hq, hkv, d):
     # A group above 16, or rows that four-element loads cannot read (head_dim
