@@ -74,7 +74,7 @@ int launch_grouped_decode(const DecodeGeometry& g, const qvp_packed_view& v, uin
 int launch_merge_splits(const DecodeGeometry& g, const qvp_packed_view& v, uint32_t out_dtype, void* out,
                         const float* ws_ml, const float* ws_acc, hipStream_t stream);
 
-// fp32 caches, head_dim 128, GQA group <= 16, power-of-two tpb >= 16, splits a
+// fp32 caches, head_dim 128 or 64, GQA group <= 16, power-of-two tpb >= 16, splits a
 // multiple of 16 tokens: the fp32 MFMA kernel, one workgroup per (split, kv
 // head), in the generic workspace layout. Returns a qvp_status.
 bool f32_grouped_supported(const DecodeGeometry& g, uint32_t kv_dtype, uint32_t split_tokens, uintptr_t query_addr,
