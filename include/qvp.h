@@ -358,7 +358,8 @@ typedef enum qvp_decode_kernel {
     QVP_DECODE_MFMA = 1,        /* persistent bf16 MFMA kernel, cost-balanced tile ranges */
     QVP_DECODE_F32_GROUPED = 2, /* fp32 MFMA kernel over split_tokens partitions + merge */
     QVP_DECODE_GENERIC = 3,     /* VALU kernel per query head over split_tokens partitions + merge */
-    QVP_DECODE_GROUPED = 4      /* VALU kernel per kv head (GQA group folded) over split_tokens partitions + merge */
+    QVP_DECODE_GROUPED = 4,     /* VALU kernel per kv head (GQA group folded) over split_tokens partitions + merge */
+    QVP_DECODE_SPLIT_MFMA = 5   /* bf16/fp16 MFMA kernel per kv head at head_dim 64 over split_tokens partitions + merge */
 } qvp_decode_kernel;
 
 typedef struct qvp_decode_plan {

@@ -45,7 +45,7 @@ HIP_FLAGS = [
     f"-I{ROOT / 'include'}",
     f"-I{PKG / 'csrc'}",
 ]
-HIP_SOURCES = ["runtime.hip", "pack.hip", "paged_decode.hip", "decode_generic.hip", "decode_f32.hip", "decode_mfma.hip", "block_ops.hip", "append.hip", "prefill.hip", "mrope.hip"]
+HIP_SOURCES = ["runtime.hip", "pack.hip", "paged_decode.hip", "decode_generic.hip", "decode_f32.hip", "decode_split16.hip", "decode_mfma.hip", "block_ops.hip", "append.hip", "prefill.hip", "mrope.hip"]
 
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:

@@ -8,10 +8,12 @@
 // (:73-89). Only then is anything enqueued, so a refused call leaves `out`
 // untouched. bf16, fp16 and fp32 caches with head_dim 128 run the persistent
 // MFMA kernel (decode_mfma.hip); other shapes run a split kernel: the fp32
-// MFMA one (decode_f32.hip), the GQA-folded one for groups up to 16 with
+// MFMA one (decode_f32.hip), the 16-bit MFMA one for head_dim 64
+// (decode_split16.hip), the GQA-folded one for groups up to 16 with
 // four-element rows, or the per-query-head generic one (both in
 // decode_generic.hip).
 #include "decode_common.h"
+#include "decode_split16.h"
 
 #include <algorithm>
 #include <mutex>
@@ -278,12 +280,18 @@ int decode_impl(const qvp_decode_args* a, void* stream, bool no_alloc) {
         const bool f32 = qvp::f32_grouped_supported(g, a->kv_dtype, v.split_tokens,
                                                     reinterpret_cast<uintptr_t>(a->query),
                                                     reinterpret_cast<uintptr_t>(a->kv_base));
-        const bool grouped = !f32 && qvp::grouped_supported(g, a->kv_dtype, v.split_tokens);
+        const bool s16 = !f32 && qvp::split16_supported(g, a->kv_dtype, v.split_tokens,
+                                                        reinterpret_cast<uintptr_t>(a->query));
+        const bool grouped = !f32 && !s16 && qvp::grouped_supported(g, a->kv_dtype, v.split_tokens);
         status = f32       ? qvp::launch_f32_grouped_decode(g, v, a->out_dtype, a->out, ws, ev, s)
+                 : s16     ? qvp::launch_split16_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s)
                  : grouped ? qvp::launch_grouped_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s)
                            : qvp::launch_generic_decode(g, v, a->kv_dtype, a->out_dtype, a->out, ws, ev, s);
-        plan.kernel = f32 ? QVP_DECODE_F32_GROUPED : grouped ? QVP_DECODE_GROUPED : QVP_DECODE_GENERIC;
-        plan.workgroups = v.num_splits * (f32 || grouped ? a->num_kv_heads : a->num_query_heads);
+        plan.kernel = f32       ? QVP_DECODE_F32_GROUPED
+                      : s16     ? QVP_DECODE_SPLIT_MFMA
+                      : grouped ? QVP_DECODE_GROUPED
+                                : QVP_DECODE_GENERIC;
+        plan.workgroups = v.num_splits * (f32 || s16 || grouped ? a->num_kv_heads : a->num_query_heads);
         plan.pieces = v.num_splits;
         plan.slots = v.num_splits;
         plan.kv_heads_per_segment = 1;

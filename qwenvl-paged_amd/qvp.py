@@ -146,7 +146,7 @@ class DecodePlan(ctypes.Structure):
     ]
 
 
-DECODE_KERNELS = {0: "none", 1: "mfma", 2: "f32_grouped", 3: "generic", 4: "grouped"}
+DECODE_KERNELS = {0: "none", 1: "mfma", 2: "f32_grouped", 3: "generic", 4: "grouped", 5: "split_mfma"}
 # qvp_tile_engine: arithmetic of the persistent bf16 kernel's tiles.
 TILE_AUTO = 0
 TILE_MATRIX = 1

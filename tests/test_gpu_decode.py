@@ -62,8 +62,9 @@ def test_gqa_folded_split_kernel_matches_the_oracle(shape, kv_dtype):
     _, ref32 = oracle_decode(w, run.image, run.query)
     got = run.decode(out_dtype=qvp.DTYPE_F32)
     plan = run.batch.decode_plan()
-    # fp32 at head_dim 64 takes the fp32 matrix-core split kernel instead.
-    assert plan["kernel"] == ("f32_grouped" if kv_dtype == qvp.DTYPE_F32 and d == 64 else "grouped"), plan
+    # At head_dim 64 the matrix-core split kernels take over: fp32 and 16-bit.
+    expect = "grouped" if d != 64 else "f32_grouped" if kv_dtype == qvp.DTYPE_F32 else "split_mfma"
+    assert plan["kernel"] == expect, plan
     assert plan["workgroups"] == plan["pieces"] * hkv, plan
     if kv_dtype == qvp.DTYPE_F32:
         err = float(np.abs(got - ref32).max())
@@ -79,7 +80,7 @@ def test_gqa_folded_split_kernel_with_other_block_sizes(tpb):
     # Frames are found per token (tok / tpb, tok % tpb), so blocks smaller
     # than, not a power of two, or larger than 16 tokens read the same rows.
     print(f"case: folded split decode tpb={tpb}", flush=True)
-    w = W.custom([37, 300, 777, 1025], 28, 4, 64, tokens_per_block=tpb, seed=tpb)
+    w = W.custom([37, 300, 777, 1025], 28, 4, 80, tokens_per_block=tpb, seed=tpb)
     run = GpuRun(w)
     _, ref32 = oracle_decode(w, run.image, run.query)
     got = run.decode(out_dtype=qvp.DTYPE_F32)
@@ -111,10 +112,8 @@ def test_config2_bf16_matches_oracle_fp32_and_bf16_outputs():
 @pytest.mark.parametrize("kv_dtype", [qvp.DTYPE_F32, qvp.DTYPE_F16], ids=["f32-grouped", "split-f16"])
 def test_split_kernels_follow_the_split_size(kv_dtype, split):
     """The split kernels partition each sequence into split_tokens pieces and
-    merge them; every partition size gives the oracle's result. The fp16 case
-    (group 7, head_dim 64) runs the GQA-folded kernel while its scores fit in
-    64 KiB of LDS (register width 8 x (64 + split) floats) and the per-head
-    generic kernel beyond."""
+    merge them; every partition size gives the oracle's result (the fp16 case,
+    group 7 at head_dim 64, on the 16-bit matrix-core split kernel)."""
     print(f"case: split kernels dtype={kv_dtype} split={split}", flush=True)
     lens = [37, 600, 1500, 4096, 129, 2049]
     if kv_dtype == qvp.DTYPE_F32:
@@ -132,8 +131,7 @@ def test_split_kernels_follow_the_split_size(kv_dtype, split):
     _, ref32 = oracle_decode(w, run.image, run.query)
     got = run.decode(out_dtype=qvp.DTYPE_F32, split_tokens=split)
     plan = run.batch.decode_plan()
-    folded = 8 * (64 + split) * 4 <= 64 * 1024
-    assert plan["kernel"] == ("f32_grouped" if kv_dtype == qvp.DTYPE_F32 else "grouped" if folded else "generic"), plan
+    assert plan["kernel"] == ("f32_grouped" if kv_dtype == qvp.DTYPE_F32 else "split_mfma"), plan
     assert plan["split_tokens"] == split, plan
     expect_splits = int(sum(-(-int(n) // split) for n in lens))
     assert plan["pieces"] == expect_splits, plan

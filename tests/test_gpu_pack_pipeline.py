@@ -214,7 +214,7 @@ def test_pack_ahead_without_a_carrier():
     run64 = GpuRun(w64)
     b.pack(w.ids, w.cu_blocks, lens1, 16, w.num_pool_blocks, stream=s, decode=a, ahead=True)
     run64.decode(out_dtype=qvp.DTYPE_F32, stream=s)
-    assert run64.batch.decode_plan()["kernel"] == "grouped"
+    assert run64.batch.decode_plan()["kernel"] == "split_mfma"
     qvp.paged_decode(a, s)
     got = out.download(np.float32, (w.num_seqs, w.num_query_heads, w.head_dim), s)
     assert np.array_equal(got.view(np.uint32), _plain_decode(run, w, lens1).view(np.uint32))

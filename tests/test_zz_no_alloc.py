@@ -88,18 +88,20 @@ def test_noalloc_matches_the_allocating_decode_on_two_calls_the_second_smaller()
         assert_close_bf16(got, ref32, f"noalloc call {i + 1}")
 
 
-@pytest.mark.parametrize("kernel", ["f32_grouped", "grouped", "generic"])
+@pytest.mark.parametrize("kernel", ["f32_grouped", "split_mfma", "grouped", "generic"])
 def test_noalloc_on_the_split_kernels_two_calls_the_second_smaller(kernel):
     # fp32 caches with a negative scale take the fp32 split kernel (the
-    # persistent decode takes positive scales); head_dim 64 takes the
-    # GQA-folded split kernel, or at head_dim 66 (rows four-element loads
-    # cannot read) the per-head generic one.
+    # persistent decode takes positive scales); bf16 at head_dim 64 the
+    # 16-bit matrix-core split kernel, at 80 the GQA-folded one, and at 66
+    # (rows four-element loads cannot read) the per-head generic one.
     for i, lens in enumerate(([37, 600, 1500, 4096, 129, 2049], [90, 700])):
         print(f"case: noalloc {kernel} call {i + 1}, lens={lens}", flush=True)
         if kernel == "f32_grouped":
             w = W.custom(lens, 28, 4, 128, kv_dtype=qvp.DTYPE_F32, seed=40 + i, kv_sigma=1.0, scale=-0.0625)
-        elif kernel == "grouped":
+        elif kernel == "split_mfma":
             w = W.custom(lens, 28, 4, 64, seed=50 + i)
+        elif kernel == "grouped":
+            w = W.custom(lens, 28, 4, 80, seed=70 + i)
         else:
             w = W.custom(lens, 28, 4, 66, seed=60 + i)
         run = GpuRun(w)
