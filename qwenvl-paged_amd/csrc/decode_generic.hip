@@ -107,14 +107,48 @@ __global__ __launch_bounds__(kGenericThreads) void decode_generic(DecodeGeometry
 }
 
 // out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) per (sequence, head).
+// Up to kMergeThreads splits: thread s reads split s's (m, l) once, the
+// maximum and the weighted sum are workgroup reductions and the splits'
+// factors sit in LDS for the accumulation pass (one round trip for the
+// (m, l) pairs instead of two dependent loops over them).
+constexpr int kMergeThreads = 128;
+
 template <typename OutT>
-__global__ __launch_bounds__(128) void merge_splits(const float* __restrict__ ws_ml, const float* __restrict__ ws_acc,
-                                                    const int32_t* __restrict__ cu_splits, OutT* __restrict__ out,
-                                                    uint32_t num_q_heads, uint32_t head_dim) {
+__global__ __launch_bounds__(kMergeThreads) void merge_splits(const float* __restrict__ ws_ml,
+                                                             const float* __restrict__ ws_acc,
+                                                             const int32_t* __restrict__ cu_splits,
+                                                             OutT* __restrict__ out, uint32_t num_q_heads,
+                                                             uint32_t head_dim) {
+    __shared__ float f_s[kMergeThreads];
+    __shared__ float red[kMergeThreads / 64];
     const uint32_t b = blockIdx.x / num_q_heads;
     const uint32_t h = blockIdx.x - b * num_q_heads;
     const int s0 = cu_splits[b];
     const int s1 = cu_splits[b + 1];
+    const int ns = s1 - s0;
+    if (ns <= kMergeThreads) {
+        const int t = static_cast<int>(threadIdx.x);
+        float m = -INFINITY;
+        float l = 0.f;
+        if (t < ns) {
+            const uint64_t idx = static_cast<uint64_t>(s0 + t) * num_q_heads + h;
+            m = ws_ml[idx * 2];
+            l = ws_ml[idx * 2 + 1];
+        }
+        const float mmax = block_reduce_max(m, red);
+        const float f = t < ns ? fast_exp2(m - mmax) : 0.f;
+        f_s[t] = f;
+        const float lsum = block_reduce_sum(l * f, red);  // also orders the f_s writes before the reads below
+        OutT* o = out + (static_cast<uint64_t>(b) * num_q_heads + h) * head_dim;
+        for (uint32_t d = threadIdx.x; d < head_dim; d += blockDim.x) {
+            float acc = 0.f;
+            for (int x = 0; x < ns; ++x) {
+                acc += ws_acc[(static_cast<uint64_t>(s0 + x) * num_q_heads + h) * head_dim + d] * f_s[x];
+            }
+            o[d] = from_float<OutT>(acc / lsum);
+        }
+        return;
+    }
     float mmax = -INFINITY;
     for (int s = s0; s < s1; ++s) mmax = fmaxf(mmax, ws_ml[(static_cast<uint64_t>(s) * num_q_heads + h) * 2]);
     float lsum = 0.f;
@@ -446,15 +480,15 @@ int launch_merge_splits(const DecodeGeometry& g, const qvp_packed_view& v, uint3
     const dim3 mgrid(v.num_seqs * g.num_q_heads);
     switch (out_dtype) {
         case QVP_DTYPE_F32:
-            hipLaunchKernelGGL(merge_splits<float>, mgrid, dim3(128), 0, stream, ws_ml, ws_acc, v.cu_splits,
+            hipLaunchKernelGGL(merge_splits<float>, mgrid, dim3(kMergeThreads), 0, stream, ws_ml, ws_acc, v.cu_splits,
                                static_cast<float*>(out), g.num_q_heads, g.head_dim);
             break;
         case QVP_DTYPE_BF16:
-            hipLaunchKernelGGL(merge_splits<uint16_t>, mgrid, dim3(128), 0, stream, ws_ml, ws_acc, v.cu_splits,
+            hipLaunchKernelGGL(merge_splits<uint16_t>, mgrid, dim3(kMergeThreads), 0, stream, ws_ml, ws_acc, v.cu_splits,
                                static_cast<uint16_t*>(out), g.num_q_heads, g.head_dim);
             break;
         default:
-            hipLaunchKernelGGL(merge_splits<_Float16>, mgrid, dim3(128), 0, stream, ws_ml, ws_acc, v.cu_splits,
+            hipLaunchKernelGGL(merge_splits<_Float16>, mgrid, dim3(kMergeThreads), 0, stream, ws_ml, ws_acc, v.cu_splits,
                                static_cast<_Float16*>(out), g.num_q_heads, g.head_dim);
             break;
     }
